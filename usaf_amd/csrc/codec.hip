@@ -1,0 +1,281 @@
+// 4-bit group codec: unpack+dequant (kernel a) and quantize.
+//
+// Dequant reproduces usaf/quantization.py:107-132 bit for bit:
+//   nibble i of the flat code bytes (low nibble first)  -> q in [0, 15]
+//   x = fp16( fp16(q * scale) + zero )                    (two fp16 roundings)
+// The fast kernel serves the production layout (group_size 128 -> 64 code
+// bytes per group): each lane loads 16 code bytes (one 128-bit load = 32
+// elements of one group), unpacks nibbles in registers with the 0x6400 magic
+// (fp16 1024 + q), runs packed fp16 mul and add, and writes four 128-bit
+// stores.  Contraction is disabled so mul+add never fuse into an FMA (an FMA
+// rounds once and would not match the reference's two roundings).
+#include "common.h"
+
+
+namespace usaf {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Eight codes of one 32-bit word (bytes b0..b3 hold elements e0..e7 as
+// lo(b0), hi(b0), lo(b1), ...) -> four fp16 pairs in natural element order,
+// each element fp16(fp16(q*s)+z).
+__device__ __forceinline__ void dequant_word_f16(uint32_t w, f16x2 s2, f16x2 z2, uint32_t out[4]) {
+#pragma clang fp contract(off)
+  const f16x2 magic = {(f16)1024.0f, (f16)1024.0f};
+  f16x2 p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // nibble i -> e_i (low half), nibble 4+i -> e_{4+i} (high half), each as 1024+q
+    uint32_t bits = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+    f16x2 q = __builtin_bit_cast(f16x2, bits) - magic;  // exact
+    f16x2 m = q * s2;                                    // fp16 round #1
+    p[i] = m + z2;                                       // fp16 round #2
+  }
+  // p[i] = (e_i, e_{i+4}); reorder to (e0,e1) (e2,e3) (e4,e5) (e6,e7)
+  uint32_t u0 = __builtin_bit_cast(uint32_t, p[0]);
+  uint32_t u1 = __builtin_bit_cast(uint32_t, p[1]);
+  uint32_t u2 = __builtin_bit_cast(uint32_t, p[2]);
+  uint32_t u3 = __builtin_bit_cast(uint32_t, p[3]);
+  out[0] = (u0 & 0xFFFFu) | (u1 << 16);
+  out[1] = (u2 & 0xFFFFu) | (u3 << 16);
+  out[2] = (u0 >> 16) | (u1 & 0xFFFF0000u);
+  out[3] = (u2 >> 16) | (u3 & 0xFFFF0000u);
+}
+
+// fp16 pair (as bits) -> bf16 pair (as bits), round-to-nearest-even.  NaN
+// inputs are handled by the caller's slow path (see group_is_finite).
+__device__ __forceinline__ uint32_t f16pair_to_bf16pair(uint32_t h2) {
+  f16x2 h = __builtin_bit_cast(f16x2, h2);
+  f32x2 f = {(float)h.x, (float)h.y};
+  bf16x2 b = __builtin_convertvector(f, bf16x2);  // v_cvt_pk_bf16_f32 on gfx950
+  return __builtin_bit_cast(uint32_t, b);
+}
+
+// Scalar fp16 -> bf16 bits with torch's NaN convention (canonical 0x7FC0).
+__device__ __forceinline__ uint16_t f16bits_to_bf16bits(uint16_t h) {
+  if ((h & 0x7FFFu) > 0x7C00u) return 0x7FC0u;
+  return f32_to_bf16_bits(f16_bits_to_f32(h));
+}
+
+// One reference dequant element: fp16(fp16(q*s)+z).
+__device__ __forceinline__ uint16_t dequant_one_f16(uint32_t q, uint16_t s_bits, uint16_t z_bits) {
+#pragma clang fp contract(off)
+  f16 qh = (f16)(float)q;
+  f16 s = __builtin_bit_cast(f16, s_bits);
+  f16 z = __builtin_bit_cast(f16, z_bits);
+  f16 m = qh * s;
+  f16 r = m + z;
+  return __builtin_bit_cast(uint16_t, r);
+}
+
+// Fast path: group_size 128, 64 code bytes per group, 16-byte aligned codes
+// and output.  Chunk c = code bytes [16c, 16c+16) = elements [32c, 32c+32),
+// all in group c/4.  `n_chunks` counts only chunks lying fully inside numel.
+template <int OUT_DT>
+__global__ __launch_bounds__(256) void dequant_g128_kernel(const u32x4* __restrict__ packed,
+                                                           const uint16_t* __restrict__ scale,
+                                                           const uint16_t* __restrict__ zero,
+                                                           u32x4* __restrict__ out, int64_t n_chunks) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < n_chunks; c += stride) {
+    const u32x4 w = __builtin_nontemporal_load(packed + c);
+    const int64_t g = c >> 2;
+    const uint16_t sb = scale[g];
+    const uint16_t zb = zero[g];
+    const f16 s = __builtin_bit_cast(f16, sb);
+    const f16 z = __builtin_bit_cast(f16, zb);
+    const f16x2 s2 = {s, s};
+    const f16x2 z2 = {z, z};
+    uint32_t h[16];
+    dequant_word_f16(w.x, s2, z2, h + 0);
+    dequant_word_f16(w.y, s2, z2, h + 4);
+    dequant_word_f16(w.z, s2, z2, h + 8);
+    dequant_word_f16(w.w, s2, z2, h + 12);
+    u32x4* dst = out + c * 4;
+    if constexpr (OUT_DT == USAF_F16) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        u32x4 v = {h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]};
+        __builtin_nontemporal_store(v, dst + k);
+      }
+    } else {
+      // Non-finite scale or zero can produce NaN; those groups take the
+      // scalar conversion that yields torch's canonical bf16 NaN.
+      const bool finite = ((sb & 0x7C00u) != 0x7C00u) && ((zb & 0x7C00u) != 0x7C00u);
+      uint32_t b[16];
+      if (finite) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) b[k] = f16pair_to_bf16pair(h[k]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          b[k] = (uint32_t)f16bits_to_bf16bits((uint16_t)(h[k] & 0xFFFFu)) |
+                 ((uint32_t)f16bits_to_bf16bits((uint16_t)(h[k] >> 16)) << 16);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        u32x4 v = {b[4 * k], b[4 * k + 1], b[4 * k + 2], b[4 * k + 3]};
+        __builtin_nontemporal_store(v, dst + k);
+      }
+    }
+  }
+}
+
+// General path: any group size / code-row width, one thread per element.
+// Element i reads nibble i of the flat code array (the reference interleaves
+// low/high nibbles of the flattened [G, packed_cols] bytes and then slices the
+// first G*eff_gs of them, quantization.py:115-127) and group i / eff_gs.
+template <int OUT_DT>
+__global__ __launch_bounds__(256) void dequant_generic_kernel(const uint8_t* __restrict__ packed,
+                                                              const uint16_t* __restrict__ scale,
+                                                              const uint16_t* __restrict__ zero,
+                                                              uint16_t* __restrict__ out, int64_t begin,
+                                                              int64_t numel, int64_t eff_gs) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < numel; i += stride) {
+    const uint32_t byte = packed[i >> 1];
+    const uint32_t q = (i & 1) ? (byte >> 4) : (byte & 0xFu);
+    const int64_t g = i / eff_gs;
+    const uint16_t h = dequant_one_f16(q, scale[g], zero[g]);
+    if constexpr (OUT_DT == USAF_F16) out[i] = h;
+    else out[i] = f16bits_to_bf16bits(h);
+  }
+}
+
+// ---- quantize ------------------------------------------------------------------
+
+__device__ __forceinline__ float nan_min(float a, float b) { return (a != a) ? a : ((b != b) ? b : fminf(a, b)); }
+__device__ __forceinline__ float nan_max(float a, float b) { return (a != a) ? a : ((b != b) ? b : fmaxf(a, b)); }
+
+// One wavefront per group.  Lane l owns code bytes j = l, l+64, ... of the
+// group, i.e. elements 2j and 2j+1.  Elements past numel are the reference's
+// zero padding and take part in min/max (quantization.py:54-60).
+template <int IN_DT>
+__global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ x, int64_t numel, int64_t eff_gs,
+                                                       int64_t n_groups, uint8_t* __restrict__ packed,
+                                                       uint16_t* __restrict__ scale, uint16_t* __restrict__ zero) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t g = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (g >= n_groups) return;
+  const int64_t base = g * eff_gs;
+  const int64_t pb = (eff_gs + 1) >> 1;
+
+  float mn = INFINITY, mx = -INFINITY;
+  for (int64_t e = lane; e < eff_gs; e += 64) {
+    const int64_t i = base + e;
+    const float v = (i < numel) ? load_as_f32<IN_DT>(x, i) : 0.0f;
+    mn = nan_min(mn, v);
+    mx = nan_max(mx, v);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    mn = nan_min(mn, __shfl_xor(mn, off, 64));
+    mx = nan_max(mx, __shfl_xor(mx, off, 64));
+  }
+  float sc = (mx - mn) / 15.0f;
+  sc = fmaxf(sc, 1e-12f);
+  if (mx != mx || mn != mn) sc = NAN;  // torch.clamp_min propagates NaN
+
+  for (int64_t j = lane; j < pb; j += 64) {
+    uint32_t qq[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t e = 2 * j + h;
+      uint32_t q = 0;
+      if (e < eff_gs) {
+        const int64_t i = base + e;
+        const float v = (i < numel) ? load_as_f32<IN_DT>(x, i) : 0.0f;
+        float r = rintf((v - mn) / sc);
+        r = fminf(fmaxf(r, 0.0f), 15.0f);
+        q = (uint32_t)r;
+      }
+      qq[h] = q;
+    }
+    packed[g * pb + j] = (uint8_t)(qq[0] | (qq[1] << 4));
+  }
+  if (lane == 0) {
+    scale[g] = f32_to_f16_bits(sc);
+    zero[g] = f32_to_f16_bits(mn);
+  }
+}
+
+int launch_blocks(int64_t work_items, int per_block, int max_blocks_per_cu) {
+  int64_t blocks = (work_items + per_block - 1) / per_block;
+  const int64_t cap = (int64_t)device_cu_count() * max_blocks_per_cu;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
+
+}  // namespace
+}  // namespace usaf
+
+using namespace usaf;
+
+extern "C" int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
+                                   int64_t n_groups, int64_t packed_cols, int64_t group_size, int64_t numel,
+                                   void* out, int32_t out_dtype, void* stream) {
+  if (numel < 0 || n_groups < 0 || packed_cols < 0 || group_size <= 0)
+    return set_error(USAF_ERR_INVALID, "dequant_q4: negative size or non-positive group_size");
+  if (out_dtype != USAF_F16 && out_dtype != USAF_BF16)
+    return set_error(USAF_ERR_INVALID, "dequant_q4: out_dtype must be fp16 or bf16, got %d", (int)out_dtype);
+  if (numel == 0) return clear_error();
+  if (!packed || !scale_f16 || !zero_f16 || !out) return set_error(USAF_ERR_INVALID, "dequant_q4: null pointer");
+  const int64_t eff_gs = group_size < numel ? group_size : numel;
+  const int64_t actual = n_groups * eff_gs;
+  if (actual > 2 * n_groups * packed_cols)
+    return set_error(USAF_ERR_INVALID, "dequant_q4: %lld groups of %lld elements exceed %lld code nibbles",
+                     (long long)n_groups, (long long)eff_gs, (long long)(2 * n_groups * packed_cols));
+  if (actual < numel)
+    return set_error(USAF_ERR_INVALID, "dequant_q4: %lld groups of %lld elements cannot hold %lld elements",
+                     (long long)n_groups, (long long)eff_gs, (long long)numel);
+  hipStream_t st = as_stream(stream);
+
+  int64_t done = 0;
+  const bool fast = eff_gs == 128 && packed_cols == 64 && (((uintptr_t)packed & 15) == 0) &&
+                    (((uintptr_t)out & 15) == 0);
+  if (fast) {
+    const int64_t n_chunks = numel / 32;
+    if (n_chunks > 0) {
+      const int blocks = launch_blocks(n_chunks, 256, 16);
+      if (out_dtype == USAF_F16)
+        dequant_g128_kernel<USAF_F16><<<blocks, 256, 0, st>>>((const u32x4*)packed, scale_f16, zero_f16,
+                                                              (u32x4*)out, n_chunks);
+      else
+        dequant_g128_kernel<USAF_BF16><<<blocks, 256, 0, st>>>((const u32x4*)packed, scale_f16, zero_f16,
+                                                               (u32x4*)out, n_chunks);
+      int rc = check_launch("dequant_q4");
+      if (rc) return rc;
+    }
+    done = n_chunks * 32;
+  }
+  if (done < numel) {
+    const int blocks = launch_blocks(numel - done, 256, 16);
+    if (out_dtype == USAF_F16)
+      dequant_generic_kernel<USAF_F16><<<blocks, 256, 0, st>>>((const uint8_t*)packed, scale_f16, zero_f16,
+                                                               (uint16_t*)out, done, numel, eff_gs);
+    else
+      dequant_generic_kernel<USAF_BF16><<<blocks, 256, 0, st>>>((const uint8_t*)packed, scale_f16, zero_f16,
+                                                                (uint16_t*)out, done, numel, eff_gs);
+    return check_launch("dequant_q4");
+  }
+  return clear_error();
+}
+
+extern "C" int usaf_hip_quantize_q4(const void* x, int32_t x_dtype, int64_t numel, int64_t group_size,
+                                    int8_t* packed, uint16_t* scale_f16, uint16_t* zero_f16, void* stream) {
+  if (numel <= 0) return set_error(USAF_ERR_INVALID, "quantize_q4: Scalar tensors cannot be quantized; numel must be > 0");
+  if (group_size <= 0) return set_error(USAF_ERR_INVALID, "quantize_q4: group_size must be positive");
+  if (!x || !packed || !scale_f16 || !zero_f16) return set_error(USAF_ERR_INVALID, "quantize_q4: null pointer");
+  const int64_t eff_gs = group_size < numel ? group_size : numel;
+  const int64_t n_groups = (numel + eff_gs - 1) / eff_gs;
+  hipStream_t st = as_stream(stream);
+  const int64_t blocks = (n_groups + 3) / 4;  // 4 wavefronts (groups) per 256-thread block
+  if (blocks > 0x7fffffffLL) return set_error(USAF_ERR_INVALID, "quantize_q4: too many groups");
+  USAF_DISPATCH_DT(x_dtype, DT,
+                   quantize_kernel<DT><<<(unsigned)blocks, 256, 0, st>>>(x, numel, eff_gs, n_groups,
+                                                                        (uint8_t*)packed, scale_f16, zero_f16));
+  return check_launch("quantize_q4");
+}

@@ -1,0 +1,95 @@
+// Shared helpers for the usaf_hip C-ABI library (gfx950 / CDNA4).
+//
+// Every exported entry point validates its arguments on the host, launches on
+// the caller's stream and returns a status code; it never throws across the
+// ABI.  The message for the last failure on the calling thread is kept in a
+// thread-local buffer read back through usaf_hip_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+
+#include "../../include/usaf_hip.h"
+
+namespace usaf {
+
+// Records a formatted message as the calling thread's last error; returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Clears the calling thread's last error; returns USAF_OK.
+int clear_error();
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// 16-bit float types used in device code.
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Checks the launch that was just issued; returns a status code.
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(USAF_ERR_RUNTIME, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return clear_error();
+}
+
+// ---- device-side conversions -------------------------------------------------
+
+// fp32 -> bf16 with round-to-nearest-even (NaN stays NaN).  Bit-level form so
+// the result does not depend on the compiler's choice of instruction.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Load one element of a 16-bit or 32-bit float array as fp32.
+template <int DT>
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
+  if constexpr (DT == USAF_F32) return reinterpret_cast<const float*>(p)[i];
+  else if constexpr (DT == USAF_F16) return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  else return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+// Store an fp32 value into a float array of type DT with round-to-nearest-even.
+template <int DT>
+__device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v) {
+  if constexpr (DT == USAF_F32) reinterpret_cast<float*>(p)[i] = v;
+  else if constexpr (DT == USAF_F16) reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);
+  else reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+}
+// Round an fp32 value to the storage type DT and back (models a tensor of type DT).
+template <int DT>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (DT == USAF_F32) return v;
+  else if constexpr (DT == USAF_F16) return (float)(_Float16)v;
+  else return bf16_bits_to_f32(f32_to_bf16_bits(v));
+}
+
+}  // namespace usaf
+
+// Dispatch a runtime dtype code onto a template parameter.
+#define USAF_DISPATCH_DT(dt, DTNAME, ...)                                        \
+  switch (dt) {                                                                \
+    case USAF_F32: { constexpr int DTNAME = USAF_F32; __VA_ARGS__; } break;    \
+    case USAF_F16: { constexpr int DTNAME = USAF_F16; __VA_ARGS__; } break;    \
+    case USAF_BF16: { constexpr int DTNAME = USAF_BF16; __VA_ARGS__; } break;  \
+    default: return usaf::set_error(USAF_ERR_INVALID, "unknown dtype code %d", (int)(dt)); \
+  }
