@@ -4,10 +4,10 @@
 //   nibble i of the flat code bytes (low nibble first)  -> q in [0, 15]
 //   x = fp16( fp16(q * scale) + zero )                    (two fp16 roundings)
 // The fast kernel serves the production layout (group_size 128 -> 64 code
-// bytes per group): each lane loads 16 code bytes (one 128-bit load = 32
-// elements of one group), unpacks nibbles in registers with the 0x6400 magic
-// (fp16 1024 + q), runs packed fp16 mul and add, and writes four 128-bit
-// stores.  Contraction is disabled so mul+add never fuse into an FMA (an FMA
+// bytes per group): each lane turns one 32-bit code word into 8 outputs,
+// unpacking nibbles in registers with the 0x6400 magic (fp16 1024 + q),
+// running packed fp16 mul and add and writing one 128-bit store; a wave's
+// loads and stores are contiguous across lanes.  Contraction is disabled so mul+add never fuse into an FMA (an FMA
 // rounds once and would not match the reference's two roundings).
 #include "common.h"
 
@@ -43,8 +43,9 @@ __device__ __forceinline__ void dequant_word_f16(uint32_t w, f16x2 s2, f16x2 z2,
   out[3] = (u2 >> 16) | (u3 & 0xFFFF0000u);
 }
 
-// fp16 pair (as bits) -> bf16 pair (as bits), round-to-nearest-even.  NaN
-// inputs are handled by the caller's slow path (see group_is_finite).
+// fp16 pair (as bits) -> bf16 pair (as bits), round-to-nearest-even.  Only
+// called for finite scale/zero (no NaN can arise then); NaN-capable groups
+// take f16bits_to_bf16bits.
 __device__ __forceinline__ uint32_t f16pair_to_bf16pair(uint32_t h2) {
   f16x2 h = __builtin_bit_cast(f16x2, h2);
   f32x2 f = {(float)h.x, (float)h.y};
@@ -69,54 +70,68 @@ __device__ __forceinline__ uint16_t dequant_one_f16(uint32_t q, uint16_t s_bits,
   return __builtin_bit_cast(uint16_t, r);
 }
 
-// Fast path: group_size 128, 64 code bytes per group, 16-byte aligned codes
-// and output.  Chunk c = code bytes [16c, 16c+16) = elements [32c, 32c+32),
-// all in group c/4.  `n_chunks` counts only chunks lying fully inside numel.
-template <int OUT_DT>
-__global__ __launch_bounds__(256) void dequant_g128_kernel(const u32x4* __restrict__ packed,
+// Fast path: group_size 128 (64 code bytes per group), 16-byte aligned output.
+// Work is cut into wave tiles of 2048 elements (1 KiB of codes, 16 groups).
+// Lane l of a wave owns the 8-element units u = l + 64k (k = 0..3) of its
+// tile: one 32-bit code word in, one 128-bit store out, so every load and
+// store instruction of the wave touches one contiguous 256 B / 1 KiB span.
+// UNR tiles are loaded before any is converted to keep more bytes in flight.
+template <int OUT_DT, int UNR>
+__global__ __launch_bounds__(256) void dequant_g128_kernel(const uint32_t* __restrict__ packed,
                                                            const uint16_t* __restrict__ scale,
                                                            const uint16_t* __restrict__ zero,
-                                                           u32x4* __restrict__ out, int64_t n_chunks) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < n_chunks; c += stride) {
-    const u32x4 w = __builtin_nontemporal_load(packed + c);
-    const int64_t g = c >> 2;
-    const uint16_t sb = scale[g];
-    const uint16_t zb = zero[g];
-    const f16 s = __builtin_bit_cast(f16, sb);
-    const f16 z = __builtin_bit_cast(f16, zb);
-    const f16x2 s2 = {s, s};
-    const f16x2 z2 = {z, z};
-    uint32_t h[16];
-    dequant_word_f16(w.x, s2, z2, h + 0);
-    dequant_word_f16(w.y, s2, z2, h + 4);
-    dequant_word_f16(w.z, s2, z2, h + 8);
-    dequant_word_f16(w.w, s2, z2, h + 12);
-    u32x4* dst = out + c * 4;
-    if constexpr (OUT_DT == USAF_F16) {
+                                                           u32x4* __restrict__ out, int64_t n_tiles) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t t0 = wave * UNR; t0 < n_tiles; t0 += n_waves * UNR) {
+    uint32_t w[UNR][4];
+    uint16_t sb[UNR][4], zb[UNR][4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        u32x4 v = {h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]};
-        __builtin_nontemporal_store(v, dst + k);
+    for (int r = 0; r < UNR; ++r) {
+      if (t0 + r < n_tiles) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int64_t u = (t0 + r) * 256 + lane + 64 * k;
+          w[r][k] = __builtin_nontemporal_load(packed + u);
+          sb[r][k] = scale[u >> 4];
+          zb[r][k] = zero[u >> 4];
+        }
       }
-    } else {
-      // Non-finite scale or zero can produce NaN; those groups take the
-      // scalar conversion that yields torch's canonical bf16 NaN.
-      const bool finite = ((sb & 0x7C00u) != 0x7C00u) && ((zb & 0x7C00u) != 0x7C00u);
-      uint32_t b[16];
-      if (finite) {
+    }
 #pragma unroll
-        for (int k = 0; k < 16; ++k) b[k] = f16pair_to_bf16pair(h[k]);
-      } else {
+    for (int r = 0; r < UNR; ++r) {
+      if (t0 + r < n_tiles) {
 #pragma unroll
-        for (int k = 0; k < 16; ++k)
-          b[k] = (uint32_t)f16bits_to_bf16bits((uint16_t)(h[k] & 0xFFFFu)) |
-                 ((uint32_t)f16bits_to_bf16bits((uint16_t)(h[k] >> 16)) << 16);
-      }
+        for (int k = 0; k < 4; ++k) {
+          const int64_t u = (t0 + r) * 256 + lane + 64 * k;
+          const f16 s = __builtin_bit_cast(f16, sb[r][k]);
+          const f16 z = __builtin_bit_cast(f16, zb[r][k]);
+          const f16x2 s2 = {s, s};
+          const f16x2 z2 = {z, z};
+          uint32_t h[4];
+          dequant_word_f16(w[r][k], s2, z2, h);
+          u32x4 v;
+          if constexpr (OUT_DT == USAF_F16) {
+            v = u32x4{h[0], h[1], h[2], h[3]};
+          } else {
+            // Non-finite scale or zero can produce NaN; those groups take the
+            // scalar conversion that yields torch's canonical bf16 NaN.
+            const bool finite = ((sb[r][k] & 0x7C00u) != 0x7C00u) && ((zb[r][k] & 0x7C00u) != 0x7C00u);
+            if (finite) {
+              v = u32x4{f16pair_to_bf16pair(h[0]), f16pair_to_bf16pair(h[1]), f16pair_to_bf16pair(h[2]),
+                        f16pair_to_bf16pair(h[3])};
+            } else {
+              uint32_t b[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        u32x4 v = {b[4 * k], b[4 * k + 1], b[4 * k + 2], b[4 * k + 3]};
-        __builtin_nontemporal_store(v, dst + k);
+              for (int j = 0; j < 4; ++j)
+                b[j] = (uint32_t)f16bits_to_bf16bits((uint16_t)(h[j] & 0xFFFFu)) |
+                       ((uint32_t)f16bits_to_bf16bits((uint16_t)(h[j] >> 16)) << 16);
+              v = u32x4{b[0], b[1], b[2], b[3]};
+            }
+          }
+          __builtin_nontemporal_store(v, out + u);
+        }
       }
     }
   }
@@ -234,22 +249,24 @@ extern "C" int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f
   hipStream_t st = as_stream(stream);
 
   int64_t done = 0;
-  const bool fast = eff_gs == 128 && packed_cols == 64 && (((uintptr_t)packed & 15) == 0) &&
+  const bool fast = eff_gs == 128 && packed_cols == 64 && (((uintptr_t)packed & 3) == 0) &&
                     (((uintptr_t)out & 15) == 0);
   if (fast) {
-    const int64_t n_chunks = numel / 32;
-    if (n_chunks > 0) {
-      const int blocks = launch_blocks(n_chunks, 256, 16);
+    constexpr int UNR = 2;
+    const int64_t n_tiles = numel / 2048;
+    if (n_tiles > 0) {
+      int64_t blocks = (n_tiles + 4 * UNR - 1) / (4 * UNR);  // 4 waves per block, UNR tiles per wave
+      if (blocks > 65536) blocks = 65536;
       if (out_dtype == USAF_F16)
-        dequant_g128_kernel<USAF_F16><<<blocks, 256, 0, st>>>((const u32x4*)packed, scale_f16, zero_f16,
-                                                              (u32x4*)out, n_chunks);
+        dequant_g128_kernel<USAF_F16, UNR><<<(unsigned)blocks, 256, 0, st>>>(
+            (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles);
       else
-        dequant_g128_kernel<USAF_BF16><<<blocks, 256, 0, st>>>((const u32x4*)packed, scale_f16, zero_f16,
-                                                               (u32x4*)out, n_chunks);
+        dequant_g128_kernel<USAF_BF16, UNR><<<(unsigned)blocks, 256, 0, st>>>(
+            (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles);
       int rc = check_launch("dequant_q4");
       if (rc) return rc;
     }
-    done = n_chunks * 32;
+    done = n_tiles * 2048;
   }
   if (done < numel) {
     const int blocks = launch_blocks(numel - done, 256, 16);
