@@ -74,6 +74,143 @@ int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f16, const u
 int usaf_hip_quantize_q4(const void* x, int32_t x_dtype, int64_t numel, int64_t group_size,
                          int8_t* packed, uint16_t* scale_f16, uint16_t* zero_f16, void* stream);
 
+/* ---- routing and bucketing ------------------------------------------------ */
+
+/*
+ * Router softmax + top-k threshold mask.
+ * Replaces usaf/qwen3moe_dml.py:73-83 (dml_qwen3_moe_block_forward's routing).
+ *   logits   [T, E] fp32/fp16/bf16 (the router F.linear output)
+ *   weights  [T, E] out, weights_dtype: p * (p >= kth_largest(p)) (ties may select
+ *            more than top_k experts), divided by max(sum, 1e-9) if norm_topk_prob
+ *   probs    [T, E] fp32 out (optional, NULL to skip): p = softmax(logits) in fp32
+ * 0 < E <= 1024, 0 < top_k <= E.
+ */
+int usaf_hip_route_topk(const void* logits, int32_t logits_dtype, int64_t T, int64_t E, int64_t top_k,
+                        int32_t norm_topk_prob, void* weights, int32_t weights_dtype, float* probs, void* stream);
+
+/*
+ * Backward of usaf_hip_route_topk (autograd of qwen3moe_dml.py:74-83):
+ * dlogits [T, E] (logits_dtype) from dweights [T, E] and the forward's probs.
+ */
+int usaf_hip_route_topk_bwd(const void* dweights, int32_t weights_dtype, const float* probs, int64_t T, int64_t E,
+                            int64_t top_k, int32_t norm_topk_prob, void* dlogits, int32_t logits_dtype,
+                            void* stream);
+
+/* int32 workspace entries usaf_hip_bucket_by_expert needs for T tokens, E experts. */
+int64_t usaf_hip_bucket_workspace_ints(int64_t T, int64_t E);
+
+/*
+ * Bucket routed (token, expert) pairs by expert -- the histogram + prefix sum +
+ * stable scatter that replaces benchmarks/kaggle_t4_bench.py:293-306
+ * (nonzero -> bincount -> argsort(stable) -> cumsum).
+ *   weights    [T, E] routing weights; a pair is routed iff its weight != 0
+ *   counts     [E] int32 out; offsets [E+1] int32 out (offsets[E] = S, the pair count)
+ *   token_idx  [capacity] int32 out: slot s -> token, tokens ascending within each expert
+ *   slot_w     [capacity] fp32 out: fp32 of the routing weight of slot s
+ *   pair_slot  [T, E] int32 out: slot of (t, e), -1 if not routed
+ * Pairs beyond `capacity` are counted in offsets but not stored; callers size
+ * capacity >= T*E or check offsets[E] <= capacity.
+ */
+int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dtype, int64_t T, int64_t E, int32_t* workspace,
+                              int32_t* counts, int32_t* offsets, int32_t* token_idx, float* slot_w,
+                              int32_t* pair_slot, int64_t capacity, void* stream);
+
+/*
+ * Expert-ordered combine.  Replaces usaf/qwen3moe_dml.py:62-64:
+ *   out[t] = dtype( sum_{e ascending, routed} fp32(y[slot(t,e)]) * fp32(w[t,e]) )
+ * accumulated in fp32 with each product rounded before the add, as the
+ * reference's `final = final + cur.float() * w.float()`.  weights == NULL: the
+ * unweighted sum (used for the grad-input accumulation over experts).
+ *   y_slots [S, H], weights [T, E], out [T, H]; dtype fp16 or bf16.
+ */
+int usaf_hip_moe_combine(const void* y_slots, const void* weights, const int32_t* pair_slot, int64_t T, int64_t E,
+                         int64_t H, int32_t dtype, void* out, void* stream);
+
+/*
+ * Backward of the weighted combine (autograd of qwen3moe_dml.py:62-64):
+ *   dcur[s]          = dtype(fp32(dout[t]) * w_s)                 [S, H]
+ *   dweights[t, e]   = dtype(sum_h fp32(dout[t,h]) * fp32(y[s,h])) (routed pairs only;
+ *                      other entries are left untouched -- callers zero them)
+ */
+int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_t* token_idx, const float* slot_w,
+                             const int32_t* offsets, int64_t S, int64_t E, int64_t H, int32_t dtype, void* dcur,
+                             void* dweights, void* stream);
+
+/* ---- fused 4-bit dequant grouped GEMMs (MFMA) ----------------------------- */
+/*
+ * Weights are whole [E, rows, cols] tensors in the codec format above
+ * (packed int8 [E*rows*cols/128, 64], fp16 scale/zero [E*rows*cols/128]);
+ * expert e owns slots offsets[e] .. offsets[e+1]-1.  Activations are fp16 or
+ * bf16 (`dtype`); with bf16 the weight operand is the bf16 rounding of the
+ * fp16 dequantized value.  Accumulation is fp32 on MFMA.  When `w16` is not
+ * NULL the weight is instead that dense [E, rows, cols] tensor of `dtype` (the
+ * reference's dense expert weights) and wq/ws/wz may be NULL.  Weight pointers
+ * must be 16-byte aligned.
+ */
+
+/* Replaces qwen3moe_dml.py:58-60 per routed slot: gu[s] = x[token_idx[s]] @ W_gate_up[e]^T
+ * ([S, 2I], dtype-rounded), act[s] = dtype(dtype(silu(gate)) * up) ([S, I]).
+ * W_gate_up [E, 2I, H]; needs H % 128 == 0, I % 64 == 0. */
+int usaf_hip_moe_gate_up_fwd(const void* x, int64_t H, const int32_t* token_idx, const int32_t* offsets, int64_t S,
+                             int64_t E, int64_t I, const int8_t* wq, const uint16_t* ws, const uint16_t* wz,
+                             const void* w16, int32_t dtype, void* gu, void* act, void* stream);
+
+/* Replaces qwen3moe_dml.py:61: y[s] = act[s] @ W_down[e]^T ([S, H]).  W_down [E, H, I];
+ * needs I % 128 == 0, H % 128 == 0. */
+int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
+                          const int8_t* wq, const uint16_t* ws, const uint16_t* wz, const void* w16, int32_t dtype, void* y,
+                          void* stream);
+
+/* Autograd of qwen3moe_dml.py:60-61: dact = dcur @ W_down[e] through the SwiGLU
+ * (saved gu) -> dgu [S, 2I] (gate half, up half).  Needs I % 128 == 0, H % 64 == 0. */
+int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S, int64_t E,
+                          int64_t I, const int8_t* wq, const uint16_t* ws, const uint16_t* wz, const void* w16, int32_t dtype,
+                          void* dgu, void* stream);
+
+/* Autograd of qwen3moe_dml.py:58 (grad-input): dx_slots[s] = dgu[s] @ W_gate_up[e]
+ * ([S, H]); sum per token with usaf_hip_moe_combine(weights=NULL).
+ * Needs H % 128 == 0, 2I % 64 == 0. */
+int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
+                             const int8_t* wq, const uint16_t* ws, const uint16_t* wz, const void* w16, int32_t dtype, void* dx_slots,
+                             void* stream);
+
+/* ---- sparse gradient path and optimizer ----------------------------------- */
+
+/* out[c, s] = in[rows ? rows[s] : s, c] for 16-bit [.., C] -> [C, S] (slot-major operands). */
+int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const int32_t* rows, int64_t S, int64_t C, void* out,
+                              int64_t ld_out, void* stream);
+
+/*
+ * Sampled weight gradient at the active positions only.  Replaces the dense
+ * per-expert F.linear weight grad + SparseGradStore.add gather
+ * (usaf/qwen3moe_dml.py:44-56, usaf/moe_loader.py:564-578):
+ *   compact[pos(p)] += fp32(dtype( sum_{s in expert e} rowT[o, s] * colT[i, s] ))
+ * for each active position p = (e, o, i) of a [E, R, C] weight, given as CSR over
+ * the E*R rows (row_ptr [E*R+1] int64, col_idx [nnz] int32) and pos_map [nnz]
+ * (compact index of CSR entry p; NULL = identity).  rowT, colT are slot-major
+ * [*, ldT] 16-bit operands (dtype).
+ */
+int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t ldT, const int32_t* offsets, int64_t E,
+                          int64_t R, const int64_t* row_ptr, const int32_t* col_idx, const int64_t* pos_map,
+                          int32_t dtype, float* compact, void* stream);
+
+/*
+ * One SparseAdam step on compact fp32 vectors (usaf/sparse_optim.py:94-130,
+ * compact_params=True): p, m, v updated in place from grad; `step` >= 1 is the
+ * step count after increment.  Scalars are the reference's Python floats.
+ */
+int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, float* v, int64_t n, double lr, double beta1,
+                              double beta2, double eps, double weight_decay, int64_t step, void* stream);
+
+/* out = in / denom (fp32) and *finite_flag = 0 if any result is inf/NaN (train.py:661-663);
+ * the caller sets *finite_flag = 1 beforehand. */
+int usaf_hip_scale_check(const float* in, float* out, int64_t n, float denom, int32_t* finite_flag, void* stream);
+
+/* base.flat[idx[j]] = dtype(vals[j]) (usaf/moe_loader.py:218-221, 411-443); out-of-range
+ * indices are skipped and set *bad_flag = 1. */
+int usaf_hip_overlay_scatter(void* base, int32_t dtype, int64_t numel, const int64_t* idx, const float* vals,
+                             int64_t n, int32_t* bad_flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,125 @@
+"""TEST INFRASTRUCTURE ONLY: the reference's routed-expert path restated in
+torch CPU ops (the parity checker and bench.py's CPU baseline; never shipped).
+
+Each function follows the cited reference lines op for op, in the same dtypes.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def route(logits: torch.Tensor, top_k: int, norm_topk_prob: bool, act_dtype: torch.dtype):
+    """usaf/qwen3moe_dml.py:73-83 -> (weights [T,E] act_dtype, probs fp32, mask fp32)."""
+    probs = F.softmax(logits, dtype=torch.float, dim=-1)                 # :74
+    top_val, _ = torch.topk(probs, top_k, dim=-1)                       # :77
+    thresh = top_val[:, -1:].clone()                                     # :78
+    mask = (probs >= thresh).to(probs.dtype)                             # :79
+    weights = probs * mask                                               # :80
+    if norm_topk_prob:                                                   # :81
+        weights = weights / weights.sum(dim=-1, keepdim=True).clamp_min(1e-9)  # :82
+    return weights.to(act_dtype), probs, mask                            # :83
+
+
+def bucket(weights: torch.Tensor):
+    """benchmarks/kaggle_t4_bench.py:293-306: nonzero pairs, bincount, stable
+    argsort by expert.  Returns (counts [E], offsets [E+1], token_idx [S], slot
+    weight (fp32 of the act-dtype weight) [S])."""
+    E = weights.shape[1]
+    tok_idx, exp_idx = torch.nonzero(weights, as_tuple=True)            # :293
+    counts = torch.bincount(exp_idx, minlength=E)                        # :296
+    order = torch.argsort(exp_idx, stable=True)                          # :298
+    exp_s, tok_s = exp_idx[order], tok_idx[order]                        # :299
+    offsets = torch.zeros(E + 1, dtype=torch.long)
+    offsets[1:] = torch.cumsum(counts, 0)                                # :300-301
+    return counts, offsets, tok_s, weights[tok_s, exp_s].float()
+
+
+def experts_dense_masked(hs, weights, w_gate_up, w_down):
+    """usaf/qwen3moe_dml.py:24-64 without grad capture: every expert on every
+    token, scaled by a router weight that is zero outside the top-k."""
+    final = torch.zeros(hs.shape, dtype=torch.float32)                  # :26
+    weights_t = weights.t().contiguous()                                 # :27
+    for ei in range(w_gate_up.shape[0]):                                 # :49
+        gu = F.linear(hs, w_gate_up[ei])                                 # :58
+        gate, up = gu.chunk(2, dim=-1)                                   # :59
+        cur = F.silu(gate) * up                                          # :60
+        cur = F.linear(cur, w_down[ei])                                  # :61
+        final = final + cur.float() * weights_t[ei].float().unsqueeze(-1)  # :62
+    return final.to(hs.dtype)                                            # :64
+
+
+def experts_routed(hs, weights, w_gate_up, w_down, return_slots: bool = False):
+    """benchmarks/kaggle_t4_bench.py:253-282: the same products restricted to
+    each expert's routed tokens; fp32 accumulation in expert order (equal to
+    the dense-masked sum: non-routed experts add exact zeros)."""
+    N, H = hs.shape
+    final = torch.zeros(N, H, dtype=torch.float32)
+    slots = {}
+    for ei in range(w_gate_up.shape[0]):
+        w_col = weights[:, ei]
+        idx = torch.nonzero(w_col, as_tuple=False).reshape(-1)          # :266
+        if idx.numel() == 0:
+            continue
+        x_e = hs.index_select(0, idx)                                    # :268
+        gu = F.linear(x_e, w_gate_up[ei])                                # :276
+        gate, up = gu.chunk(2, dim=-1)
+        act = F.silu(gate) * up
+        cur = F.linear(act, w_down[ei])                                  # :279
+        if return_slots:
+            slots[ei] = dict(idx=idx, gu=gu, act=act, y=cur)
+        cur = cur.float() * w_col.index_select(0, idx).float().unsqueeze(-1)  # :280
+        final = final.index_add(0, idx, cur)                             # :281
+    out = final.to(hs.dtype)
+    return (out, slots) if return_slots else out
+
+
+def experts_routed_autograd(hs, weights, w_gate_up, w_down, dout):
+    """Backward of the routed expert forward by torch autograd in the act
+    dtype (the reference obtains its gradients the same way, through
+    F.linear/silu/mul backward).  Returns (dhs, dweights, dW_gate_up, dW_down)
+    with dense per-expert weight gradients in the weight dtype."""
+    hs = hs.detach().clone().requires_grad_(True)
+    w = weights.detach().clone().requires_grad_(True)
+    wg = w_gate_up.detach().clone().requires_grad_(True)
+    wd = w_down.detach().clone().requires_grad_(True)
+    out = experts_routed(hs, w, wg, wd)
+    out.backward(dout)
+    return hs.grad, w.grad, wg.grad, wd.grad
+
+
+def gather_compact(dense_grad: torch.Tensor, active_idx: torch.Tensor) -> torch.Tensor:
+    """SparseGradStore.add (usaf/moe_loader.py:564-578) for one microbatch:
+    the active flat positions of the dense grad, as fp32."""
+    return dense_grad.reshape(-1).gather(0, active_idx.reshape(-1).long()).float()
+
+
+def sparse_adam_step(p, g, m, v, step, lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0):
+    """usaf/sparse_optim.py:94-130 (compact_params=True) on fp32 CPU vectors, in place."""
+    beta1, beta2 = betas
+    bias1 = 1 - beta1 ** step                                            # :96
+    bias2 = 1 - beta2 ** step                                            # :97
+    grad = g.clone()
+    if weight_decay > 0:                                                 # :113
+        grad = grad + weight_decay * p                                   # :119
+    m.mul_(beta1).add_(grad, alpha=1 - beta1)                            # :123
+    v.mul_(beta2).addcmul_(grad, grad, value=1 - beta2)                  # :124
+    update = (m / bias1) / ((v / bias2).sqrt() + eps)                    # :126
+    p.add_(-lr * update)                                                 # :127-130
+    return p, m, v
+
+
+def combine_slots(y_slots: torch.Tensor, offsets, token_idx: torch.Tensor, weights: torch.Tensor):
+    """usaf/qwen3moe_dml.py:62-64 given each routed slot's expert output
+    (slots grouped by expert in `offsets`): fp32 accumulation over experts in
+    ascending order, each product cur.float() * w.float() rounded before the add."""
+    T, E = weights.shape
+    final = torch.zeros(T, y_slots.shape[1], dtype=torch.float32)
+    offs = [int(o) for o in offsets]
+    for e in range(E):
+        s0, s1 = offs[e], offs[e + 1]
+        if s0 == s1:
+            continue
+        idx = token_idx[s0:s1].long()
+        final = final.index_add(0, idx, y_slots[s0:s1].float() * weights[idx, e].float().unsqueeze(-1))
+    return final.to(weights.dtype)

@@ -1,0 +1,333 @@
+"""GPU parity of routing, bucketing, the fused expert GEMMs, the backward and
+the sparse optimizer path against the CPU oracle (oracle/moe.py).
+
+Bars: routing masks, bucket order and slot maps bit-exact; the combine
+bit-exact given identical inputs; floating-point outputs within
+rel = max|got - ref| / max|ref| <= 1e-2 (bf16) or 2e-3 (fp16).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as M
+from oracle.codec_torch import dequant_opseq
+from usaf_amd import moe as G
+from usaf_amd.moe_loader import SparseGradStore, overlay_scatter
+from usaf_amd.sparse_optim import SparseAdam
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def rel_err(got, ref):
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+def make_layer(dev, E, H, I, T, k, dtype, seed=0, norm=False, dense=False):
+    g = torch.Generator().manual_seed(seed)
+    w_gu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).half()
+    w_dn = (torch.randn(E, H, I, generator=g) * 0.02).half()
+    qg = G.Q4Tensor.quantize(w_gu.to(dev))
+    qd = G.Q4Tensor.quantize(w_dn.to(dev))
+    # oracle weights: the reference's CPU dequant of the same codes, in the activation dtype
+    deq_g = dequant_opseq(qg.q.cpu(), qg.s.cpu(), qg.z.cpu(), qg.shape).to(dtype)
+    deq_d = dequant_opseq(qd.q.cpu(), qd.s.cpu(), qd.z.cpu(), qd.shape).to(dtype)
+    hs = torch.randn(T, H, generator=g).to(dtype)
+    logits = torch.randn(T, E, generator=g)
+    w_ref, _, _ = M.route(logits, k, norm, dtype)
+    if dense:
+        ew = G.ExpertWeights(deq_g.to(dev), deq_d.to(dev))
+    else:
+        ew = G.ExpertWeights(qg, qd)
+    return dict(hs=hs, logits=logits, w=w_ref, deq_g=deq_g, deq_d=deq_d, ew=ew)
+
+
+# ---- routing -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("ldt", [torch.float32, torch.bfloat16])
+def test_route_cfg1(gpu_device, norm, ldt):
+    _say(f"route T=4096 E=128 k=8 norm={norm} logits={ldt}")
+    g = torch.Generator().manual_seed(7)
+    logits = torch.randn(4096, 128, generator=g).to(ldt)
+    w_ref, p_ref, mask_ref = M.route(logits, 8, norm, torch.bfloat16)
+    w, p = G.route_topk(logits.to(gpu_device), 8, norm, torch.bfloat16)
+    torch.cuda.synchronize()
+    w, p = w.cpu(), p.cpu()
+    assert torch.equal(w != 0, mask_ref != 0), "routing mask differs"
+    assert torch.allclose(p, p_ref, rtol=2e-6, atol=1e-9)
+    # bf16 weights: equal except for rare one-ulp rounding differences of the fp32 probs
+    diff = (w.float() - w_ref.float()).abs()
+    assert float(diff.max()) <= 2.0 ** -8 * float(w_ref.float().abs().max())
+    if ldt == torch.bfloat16:  # bf16 logits tie often: more than k selected on some tokens
+        assert int((mask_ref != 0).sum(-1).max()) >= 8
+
+
+def test_route_ties_brute(gpu_device):
+    _say("route with forced ties")
+    logits = torch.zeros(8, 16)
+    logits[0, :6] = 3.0
+    logits[1] = torch.arange(16.0)
+    logits[2, [1, 5, 9]] = 2.0
+    w_ref, _, mask_ref = M.route(logits, 4, False, torch.float32)
+    w, _ = G.route_topk(logits.to(gpu_device), 4, False, torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(w.cpu() != 0, mask_ref != 0)
+    assert int((w.cpu()[0] != 0).sum()) == 6
+
+
+def test_bucket_cfg1(gpu_device):
+    _say("bucket T=4096 E=128")
+    g = torch.Generator().manual_seed(8)
+    w_ref, _, _ = M.route(torch.randn(4096, 128, generator=g), 8, False, torch.bfloat16)
+    counts, offsets, tok, sw = M.bucket(w_ref)
+    b = G.bucket_by_expert(w_ref.to(gpu_device))
+    torch.cuda.synchronize()
+    assert b.n_slots == int(offsets[-1])
+    assert torch.equal(b.counts.cpu().long(), counts)
+    assert torch.equal(b.offsets.cpu().long(), offsets)
+    assert torch.equal(b.token_idx.cpu().long(), tok)
+    assert torch.equal(b.slot_w.cpu(), sw)
+    ps = b.pair_slot.cpu()
+    assert torch.equal(ps >= 0, w_ref != 0)
+    sel = ps[ps >= 0].long()
+    assert torch.equal(torch.sort(sel).values, torch.arange(b.n_slots))
+
+
+def test_bucket_empty_and_ragged(gpu_device):
+    _say("bucket: empty experts, single token, no routed pairs")
+    w = torch.zeros(5, 12, dtype=torch.bfloat16)
+    w[0, 3] = 0.5
+    w[4, 3] = 0.25
+    w[2, 11] = 1.0
+    b = G.bucket_by_expert(w.to(gpu_device))
+    torch.cuda.synchronize()
+    assert b.n_slots == 3 and b.token_idx.cpu().tolist() == [0, 4, 2]
+    assert b.offsets.cpu().tolist() == [0, 0, 0, 0, 2, 2, 2, 2, 2, 2, 2, 2, 3]
+    b0 = G.bucket_by_expert(torch.zeros(3, 4, dtype=torch.bfloat16, device=gpu_device))
+    assert b0.n_slots == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_combine_bit_exact(gpu_device, dtype):
+    _say(f"combine bit-exact {dtype}")
+    g = torch.Generator().manual_seed(9)
+    T, E, H = 512, 32, 384
+    w_ref, _, _ = M.route(torch.randn(T, E, generator=g), 4, False, dtype)
+    counts, offsets, tok, sw = M.bucket(w_ref)
+    y = torch.randn(int(offsets[-1]), H, generator=g).to(dtype)
+    ref = M.combine_slots(y, offsets, tok, w_ref)
+    b = G.bucket_by_expert(w_ref.to(gpu_device))
+    out = G.combine(y.to(gpu_device), w_ref.to(gpu_device), b.pair_slot, dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+# ---- forward ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dense", [False, True])
+def test_experts_forward_small(gpu_device, dtype, dense):
+    _say(f"experts fwd E=8 H=256 I=128 T=300 k=2 {dtype} dense={dense}")
+    L = make_layer(gpu_device, 8, 256, 128, 300, 2, dtype, seed=1, dense=dense)
+    ref = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"])
+    out = G.routed_experts(L["hs"].to(gpu_device), L["w"].to(gpu_device), L["ew"])
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) <= TOL[dtype]
+
+
+def test_experts_forward_intermediates(gpu_device):
+    # per-slot gate_up / SwiGLU / down outputs against the oracle's per-expert tensors
+    _say("experts fwd intermediates E=8 H=256 I=128 bf16")
+    dt = torch.bfloat16
+    L = make_layer(gpu_device, 8, 256, 128, 300, 2, dt, seed=2)
+    _, slots = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"], return_slots=True)
+    b = G.bucket_by_expert(L["w"].to(gpu_device))
+    ew = L["ew"]
+    S, I, H = b.n_slots, ew.I, ew.H
+    gu = torch.empty(S, 2 * I, dtype=dt, device=gpu_device)
+    act = torch.empty(S, I, dtype=dt, device=gpu_device)
+    y = torch.empty(S, H, dtype=dt, device=gpu_device)
+    from usaf_amd import _native as N
+    st = N.stream_ptr(gpu_device)
+    q, s, z, w16 = ew._ptrs("gate_up", dt)
+    N.call("usaf_hip_moe_gate_up_fwd", L["hs"].to(gpu_device).data_ptr(), H, b.token_idx.data_ptr(),
+           b.offsets.data_ptr(), S, ew.E, I, q, s, z, w16, N.BF16, gu.data_ptr(), act.data_ptr(), st)
+    q, s, z, w16 = ew._ptrs("down", dt)
+    N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, ew.E, H, q, s, z, w16, N.BF16,
+           y.data_ptr(), st)
+    torch.cuda.synchronize()
+    offs = b.offsets.cpu().tolist()
+    for e, sl in slots.items():
+        s0, s1 = offs[e], offs[e + 1]
+        assert torch.equal(b.token_idx[s0:s1].cpu().long(), sl["idx"])
+        assert rel_err(gu[s0:s1], sl["gu"]) <= 1e-2
+        assert rel_err(act[s0:s1], sl["act"]) <= 1e-2
+        assert rel_err(y[s0:s1], sl["y"]) <= 1e-2
+
+
+def test_experts_forward_cfg1(gpu_device):
+    _say("experts fwd cfg1 Qwen3-30B-A3B: T=4096 H=2048 I=768 E=128 k=8 bf16 q4")
+    dt = torch.bfloat16
+    L = make_layer(gpu_device, 128, 2048, 768, 4096, 8, dt, seed=11)
+    out = G.routed_experts(L["hs"].to(gpu_device), L["w"].to(gpu_device), L["ew"])
+    torch.cuda.synchronize()
+    torch.set_num_threads(16)
+    ref = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"])
+    assert rel_err(out, ref) <= TOL[dt]
+
+
+def test_experts_forward_mixtral_shape(gpu_device):
+    _say("experts fwd cfg3 Mixtral shapes E=8 H=4096 I=14336 k=2 (T=192) bf16 q4")
+    dt = torch.bfloat16
+    L = make_layer(gpu_device, 8, 4096, 14336, 192, 2, dt, seed=12)
+    out = G.routed_experts(L["hs"].to(gpu_device), L["w"].to(gpu_device), L["ew"])
+    torch.cuda.synchronize()
+    torch.set_num_threads(16)
+    ref = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"])
+    assert rel_err(out, ref) <= TOL[dt]
+
+
+# ---- backward -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dense", [False, True])
+def test_experts_backward_small(gpu_device, dtype, dense):
+    _say(f"experts bwd E=8 H=256 I=128 T=300 k=2 {dtype} dense={dense}")
+    E, H, I, T = 8, 256, 128, 300
+    L = make_layer(gpu_device, E, H, I, T, 2, dtype, seed=3, dense=dense)
+    g = torch.Generator().manual_seed(30)
+    dout = torch.randn(T, H, generator=g).to(dtype)
+    dhs_r, dw_r, dwg_r, dwd_r = M.experts_routed_autograd(L["hs"], L["w"], L["deq_g"], L["deq_d"], dout)
+    # random 0.5 % active positions per tensor, as the bench's cfg2 mask
+    nG, nD = E * 2 * I * H, E * H * I
+    act_g = torch.randperm(nG, generator=g)[: max(1, nG // 200)].sort().values
+    act_d = torch.randperm(nD, generator=g)[: max(1, nD // 200)]          # unsorted: exercises pos_map
+    store = SparseGradStore({"L.gate_up_proj": act_g, "L.down_proj": act_d},
+                            {"L.gate_up_proj": (E, 2 * I, H), "L.down_proj": (E, H, I)}, device=gpu_device)
+    hs = L["hs"].to(gpu_device).requires_grad_(True)
+    w = L["w"].to(gpu_device).requires_grad_(True)
+    out = G.routed_experts(hs, w, L["ew"], capture=(store, "L"))
+    out.backward(dout.to(gpu_device))
+    torch.cuda.synchronize()
+    tol = TOL[dtype]
+    assert rel_err(hs.grad, dhs_r) <= tol
+    routed = L["w"] != 0
+    assert torch.all(w.grad.cpu()[~routed] == 0)
+    assert rel_err(w.grad.cpu()[routed], dw_r[routed]) <= tol
+    cg = M.gather_compact(dwg_r, act_g)
+    cd = M.gather_compact(dwd_r, act_d)
+    assert rel_err(store.compact["L.gate_up_proj"], cg) <= tol
+    assert rel_err(store.compact["L.down_proj"], cd) <= tol
+
+
+def test_dict_capture_dense_grads(gpu_device):
+    _say("experts bwd with dict grad store (dense per-expert grads)")
+    E, H, I, T = 4, 256, 128, 96
+    dt = torch.bfloat16
+    L = make_layer(gpu_device, E, H, I, T, 2, dt, seed=4)
+    dout = torch.randn(T, H, generator=torch.Generator().manual_seed(40)).to(dt)
+    _, _, dwg_r, dwd_r = M.experts_routed_autograd(L["hs"], L["w"], L["deq_g"], L["deq_d"], dout)
+    store = {}
+    out = G.routed_experts(L["hs"].to(gpu_device).requires_grad_(True), L["w"].to(gpu_device), L["ew"],
+                           capture=(store, "L"))
+    out.backward(dout.to(gpu_device))
+    torch.cuda.synchronize()
+    assert store["L.gate_up_proj"].dtype == torch.float16 and store["L.gate_up_proj"].shape == (E, 2 * I, H)
+    assert rel_err(store["L.gate_up_proj"], dwg_r) <= 1e-2
+    assert rel_err(store["L.down_proj"], dwd_r) <= 1e-2
+
+
+def test_moe_block_router_backward(gpu_device):
+    _say("moe block fwd+bwd incl. router softmax/top-k backward, bf16")
+    E, H, I, T, k = 16, 256, 128, 200, 4
+    dt = torch.bfloat16
+    L = make_layer(gpu_device, E, H, I, T, k, dt, seed=5)
+    g = torch.Generator().manual_seed(50)
+    wr = (torch.randn(E, H, generator=g) / H ** 0.5).to(dt)
+    dout = torch.randn(T, H, generator=g).to(dt)
+    # oracle: the reference block on CPU with autograd
+    x = L["hs"].clone().requires_grad_(True)
+    wr_c = wr.clone().requires_grad_(True)
+    logits = torch.nn.functional.linear(x, wr_c)
+    weights, _, _ = M.route(logits, k, True, dt)
+    ref = M.experts_routed(x, weights, L["deq_g"], L["deq_d"])
+    ref.backward(dout)
+    # GPU
+    xg = L["hs"].to(gpu_device).requires_grad_(True)
+    wg = wr.to(gpu_device).requires_grad_(True)
+    out = G.moe_block(xg, wg, k, True, L["ew"])
+    out.backward(dout.to(gpu_device))
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) <= 1e-2
+    assert rel_err(xg.grad, x.grad) <= 1e-2
+    assert rel_err(wg.grad, wr_c.grad) <= 1e-2
+
+
+# ---- optimizer path ------------------------------------------------------------------
+
+def test_sparse_adam_vs_oracle(gpu_device):
+    _say("SparseAdam 3 steps, 3,019,897 elements")
+    n = 3_019_897
+    g = torch.Generator().manual_seed(6)
+    p0 = torch.randn(n, generator=g) * 0.02
+    p_ref, m_ref, v_ref = p0.clone(), torch.zeros(n), torch.zeros(n)
+    master = torch.nn.Parameter(p0.clone().to(gpu_device), requires_grad=False)
+    opt = SparseAdam({"w": master}, active_idx={"w": torch.arange(n)}, lr=2e-4, weight_decay=0.005,
+                     compact_params=True)
+    for step in range(1, 4):
+        grad = torch.randn(n, generator=g) * 1e-3
+        M.sparse_adam_step(p_ref, grad, m_ref, v_ref, step, 2e-4, weight_decay=0.005)
+        opt.step(compact_grads={"w": grad.to(gpu_device)})
+    torch.cuda.synchronize()
+    # fp32 elementwise: a few ulps at most (torch's scalar tail may round differently)
+    assert rel_err(master, p_ref) <= 1e-6
+    assert rel_err(opt._m["w"], m_ref) <= 1e-6
+    assert rel_err(opt._v["w"], v_ref) <= 1e-6
+
+
+def test_sparse_adam_full_params(gpu_device):
+    _say("SparseAdam compact_params=False")
+    p = torch.nn.Parameter(torch.ones(10, device=gpu_device))
+    opt = SparseAdam({"w": p}, active_idx={"w": torch.tensor([0, 1, 2, 3, 4])}, lr=1.0)
+    p.grad = torch.ones(10, device=gpu_device)
+    opt.step()
+    torch.cuda.synchronize()
+    assert float(p[0]) < 1.0 and float(p[5]) == 1.0
+
+
+def test_overlay_scatter_bit_exact(gpu_device):
+    _say("overlay scatter fp16")
+    g = torch.Generator().manual_seed(7)
+    base = torch.randn(100_000, generator=g).half()
+    idx = torch.randperm(100_000, generator=g)[:500]
+    vals = torch.randn(500, generator=g)
+    ref = base.clone()
+    ref.reshape(-1).scatter_(0, idx, vals.to(torch.float16))
+    b = base.to(gpu_device)
+    overlay_scatter(b, idx, vals)
+    torch.cuda.synchronize()
+    assert torch.equal(b.cpu().view(torch.int16), ref.view(torch.int16))
+    with pytest.raises(IndexError):
+        overlay_scatter(b, torch.tensor([100_000]), torch.tensor([1.0]))
+
+
+def test_scale_check(gpu_device):
+    _say("scale + finite check")
+    from usaf_amd import _native as N
+    x = torch.randn(10000, device=gpu_device)
+    out = torch.empty_like(x)
+    flag = torch.ones(1, dtype=torch.int32, device=gpu_device)
+    N.call("usaf_hip_scale_check", x.data_ptr(), out.data_ptr(), x.numel(), 4096.0, flag.data_ptr(),
+           N.stream_ptr(gpu_device))
+    assert int(flag.item()) == 1 and torch.equal(out, x / 4096.0)
+    x[123] = float("inf")
+    N.call("usaf_hip_scale_check", x.data_ptr(), out.data_ptr(), x.numel(), 4096.0, flag.data_ptr(),
+           N.stream_ptr(gpu_device))
+    assert int(flag.item()) == 0

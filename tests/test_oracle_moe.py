@@ -1,0 +1,150 @@
+"""Pins the MoE part of the oracle (oracle/moe.py) on the CPU.
+
+Checks: brute force on tiny inputs (routing threshold with ties, stable
+bucketing), the reference's claim that the routed and dense-masked forwards
+agree (benchmarks/kaggle_t4_bench.py:245-250), the float64 closed form of the
+expert layer, closed-form Adam steps, and the reference's own qualitative
+SparseAdam tests (tests/test_sparse_optim.py:21-49).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import moe as M
+
+
+def test_route_threshold_brute_force_with_ties():
+    g = torch.Generator().manual_seed(0)
+    T, E, k = 64, 16, 4
+    logits = torch.randn(T, E, generator=g)
+    logits[0, :6] = 2.5          # six-way tie at the top: all six selected
+    logits[1, 3] = logits[1, 7] = logits[1].max() + 1  # tie among the top two
+    logits = logits.bfloat16().float()  # bf16-valued logits produce more ties
+    w, probs, mask = M.route(logits, k, False, torch.float32)
+    for t in range(T):
+        p = probs[t].tolist()
+        thr = sorted(p, reverse=True)[k - 1]
+        sel = [e for e in range(E) if p[e] >= thr]
+        assert mask[t].nonzero().reshape(-1).tolist() == sel
+        assert len(sel) >= k
+    assert int(mask[0].sum()) == 6
+    # softmax against float64 closed form
+    ref = torch.softmax(logits.double(), -1)
+    assert torch.allclose(probs.double(), ref, rtol=1e-6, atol=1e-9)
+
+
+def test_route_renorm_sums_to_one():
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn(32, 128, generator=g)
+    w, _, mask = M.route(logits, 8, True, torch.float32)
+    assert torch.allclose(w.sum(-1), torch.ones(32), atol=1e-6)
+    assert torch.all((w != 0) == (mask != 0))
+
+
+def test_bucket_brute_force():
+    g = torch.Generator().manual_seed(2)
+    T, E = 50, 7
+    w = (torch.rand(T, E, generator=g) < 0.3).float() * torch.rand(T, E, generator=g)
+    counts, offsets, tok, sw = M.bucket(w)
+    exp_tok = []
+    exp_w = []
+    for e in range(E):
+        for t in range(T):
+            if w[t, e] != 0:
+                exp_tok.append(t)
+                exp_w.append(float(w[t, e]))
+        assert int(counts[e]) == sum(1 for t in range(T) if w[t, e] != 0)
+    assert tok.tolist() == exp_tok
+    assert sw.tolist() == pytest.approx(exp_w)
+    assert offsets[-1] == len(exp_tok) and offsets[0] == 0
+
+
+def _layer(E=8, H=128, I=64, T=40, k=2, dtype=torch.bfloat16, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    hs = torch.randn(T, H, generator=g).to(dtype)
+    wg = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(dtype)
+    wd = (torch.randn(E, H, I, generator=g) * 0.05).to(dtype)
+    logits = torch.randn(T, E, generator=g)
+    w, _, _ = M.route(logits, k, False, dtype)
+    return hs, w, wg, wd
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_routed_equals_dense_masked(dtype):
+    hs, w, wg, wd = _layer(dtype=dtype)
+    a = M.experts_dense_masked(hs, w, wg, wd)
+    b = M.experts_routed(hs, w, wg, wd)
+    rel = (a.float() - b.float()).abs().max() / a.float().abs().max()
+    assert rel <= (1e-2 if dtype == torch.bfloat16 else 2e-3)
+
+
+def test_expert_layer_vs_float64_closed_form():
+    hs, w, wg, wd = _layer(dtype=torch.float32)
+    out = M.experts_routed(hs, w, wg, wd).double()
+    x, W, G, D = hs.double(), w.double(), wg.double(), wd.double()
+    ref = torch.zeros_like(x)
+    for e in range(G.shape[0]):
+        gu = x @ G[e].t()
+        I = D.shape[2]
+        a = F.silu(gu[:, :I]) * gu[:, I:]
+        ref += (a @ D[e].t()) * W[:, e:e + 1]
+    assert torch.allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_backward_dweights_closed_form():
+    hs, w, wg, wd = _layer(dtype=torch.float32)
+    g = torch.Generator().manual_seed(9)
+    dout = torch.randn(hs.shape, generator=g)
+    dhs, dw, dwg, dwd = M.experts_routed_autograd(hs, w, wg, wd, dout)
+    _, slots = M.experts_routed(hs, w, wg, wd, return_slots=True)
+    for e, s in slots.items():
+        exp = (dout[s["idx"]] * s["y"]).sum(-1)
+        assert torch.allclose(dw[s["idx"], e], exp, rtol=1e-5, atol=1e-6)
+        # dW_down = dcur^T act, dcur = dout * w
+        dcur = dout[s["idx"]] * w[s["idx"], e:e + 1]
+        assert torch.allclose(dwd[e], dcur.t() @ s["act"], rtol=1e-4, atol=1e-6)
+
+
+def test_gather_compact_brute_force():
+    g = torch.Generator().manual_seed(4)
+    dense = torch.randn(3, 5, 7, generator=g).half()
+    idx = torch.tensor([0, 9, 50, 104])
+    out = M.gather_compact(dense, idx)
+    flat = dense.reshape(-1)
+    assert out.tolist() == [float(flat[i]) for i in idx.tolist()]
+
+
+def test_sparse_adam_closed_form_first_steps():
+    g = torch.Generator().manual_seed(5)
+    p = torch.randn(1000, generator=g)
+    grad = torch.randn(1000, generator=g)
+    m = torch.zeros(1000)
+    v = torch.zeros(1000)
+    lr, wd, eps = 1e-2, 0.005, 1e-8
+    p0 = p.clone()
+    M.sparse_adam_step(p, grad, m, v, 1, lr, weight_decay=wd, eps=eps)
+    gg = grad.double() + wd * p0.double()
+    # step 1: m_hat = g, v_hat = g^2 -> update = g / (|g| + eps)
+    exp = p0.double() - lr * gg / (gg.abs() + eps)
+    assert torch.allclose(p.double(), exp, rtol=0, atol=1e-6)
+    # step 2 closed form
+    p1 = p.clone()
+    grad2 = torch.randn(1000, generator=g)
+    M.sparse_adam_step(p, grad2, m, v, 2, lr, weight_decay=wd, eps=eps)
+    g2 = grad2.double() + wd * p1.double()
+    m2 = 0.9 * 0.1 * gg + 0.1 * g2
+    v2 = 0.999 * 0.001 * gg ** 2 + 0.001 * g2 ** 2
+    upd = (m2 / (1 - 0.9 ** 2)) / ((v2 / (1 - 0.999 ** 2)).sqrt() + eps)
+    assert torch.allclose(p.double(), p1.double() - lr * upd, rtol=0, atol=2e-6)
+
+
+def test_sparse_adam_reference_qualitative():
+    # tests/test_sparse_optim.py:41-49 pattern: active params decrease under positive grads
+    p = torch.ones(3)
+    m, v = torch.zeros(3), torch.zeros(3)
+    M.sparse_adam_step(p, torch.ones(3), m, v, 1, 1.0)
+    assert bool((p < 1.0).all())
+    assert math.isclose(float(p[0]), 0.0, abs_tol=1e-6)  # 1 - 1.0 * 1/(1+1e-8)

@@ -29,9 +29,32 @@ _c_f32 = ctypes.c_float
 _c_p = ctypes.c_void_p
 
 # name -> argument types (all return int status)
+_c_d = ctypes.c_double
+
 _SIGNATURES: dict[str, list] = {
     "usaf_hip_dequant_q4": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i32, _c_p],
     "usaf_hip_quantize_q4": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],
+    "usaf_hip_route_topk": [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p, _c_p],
+    "usaf_hip_route_topk_bwd": [_c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p],
+    "usaf_hip_bucket_by_expert": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p],
+    "usaf_hip_moe_combine": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p],
+    "usaf_hip_moe_combine_bwd": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p],
+    "usaf_hip_moe_gate_up_fwd": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i32,
+                                 _c_p, _c_p, _c_p],
+    "usaf_hip_moe_down_fwd": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p],
+    "usaf_hip_moe_down_bwd": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p,
+                              _c_p],
+    "usaf_hip_moe_gate_up_bwd": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p,
+                                 _c_p],
+    "usaf_hip_gather_transpose": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    "usaf_hip_sddmm_masked": [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p],
+    "usaf_hip_sparse_adam_step": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_d, _c_d, _c_d, _c_d, _c_i64, _c_p],
+    "usaf_hip_scale_check": [_c_p, _c_p, _c_i64, _c_f32, _c_p, _c_p],
+    "usaf_hip_overlay_scatter": [_c_p, _c_i32, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p],
+}
+# entry points that return a value instead of a status
+_VALUE_FUNCS: dict[str, tuple] = {
+    "usaf_hip_bucket_workspace_ints": (_c_i64, [_c_i64, _c_i64]),
 }
 
 _lock = threading.Lock()
@@ -40,7 +63,7 @@ _lib: ctypes.CDLL | None = None
 
 def exported_symbols() -> list[str]:
     """Names of the status-returning entry points this binding declares."""
-    return list(_SIGNATURES) + ["usaf_hip_abi_version", "usaf_hip_last_error"]
+    return list(_SIGNATURES) + list(_VALUE_FUNCS) + ["usaf_hip_abi_version", "usaf_hip_last_error"]
 
 
 def load() -> ctypes.CDLL:
@@ -63,6 +86,10 @@ def load() -> ctypes.CDLL:
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        for name, (restype, argtypes) in _VALUE_FUNCS.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
             fn.argtypes = argtypes
         _lib = lib
     return _lib

@@ -1,0 +1,451 @@
+// Routing (softmax + top-k threshold), bucketing of tokens by expert, and the
+// expert-ordered combine, with their backward passes.
+//
+//  route_topk        usaf/qwen3moe_dml.py:73-83
+//  bucket_by_expert  benchmarks/kaggle_t4_bench.py:293-306 (nonzero -> bincount
+//                    -> stable argsort by expert -> offsets)
+//  moe_combine       usaf/qwen3moe_dml.py:62-64 (fp32 accumulation in expert order)
+#include "common.h"
+
+namespace usaf {
+namespace {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// k-th largest value (counting repeats, as torch.topk(...).values[:, -1]) of
+// the valid entries held by the wave: VPL values per lane, element e = lane + 64*j.
+template <int VPL>
+__device__ __forceinline__ float kth_largest(const float (&p)[VPL], const bool (&valid)[VPL], int k, int lane) {
+  bool taken[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) taken[j] = !valid[j];
+  float thr = -INFINITY;
+  for (int r = 0; r < k; ++r) {
+    // lane-local best (largest value, lowest element index on ties)
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = lane + kWave * j;
+      if (!taken[j] && (p[j] > bv || (p[j] == bv && e < bi))) { bv = p[j]; bi = e; }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, kWave);
+      const int oi = __shfl_xor(bi, off, kWave);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    thr = bv;
+    if (bi == 0x7fffffff) break;  // fewer valid entries than k
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (lane + kWave * j == bi) taken[j] = true;
+  }
+  return thr;
+}
+
+// Softmax over the row (fp32), as F.softmax(logits, dtype=float).
+template <int VPL>
+__device__ __forceinline__ void row_softmax(float (&p)[VPL], const bool (&valid)[VPL]) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) if (valid[j]) m = fmaxf(m, p[j]);
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    p[j] = valid[j] ? expf(p[j] - m) : 0.f;
+    s += p[j];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) p[j] = p[j] / s;
+}
+
+// One wavefront per token.
+template <int VPL, int LDT, int WDT>
+__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int64_t T, int E, int k,
+                                                         int norm, void* __restrict__ weights,
+                                                         float* __restrict__ probs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float p[VPL];
+  bool valid[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + kWave * j;
+    valid[j] = e < E;
+    p[j] = valid[j] ? load_as_f32<LDT>(logits, t * E + e) : -INFINITY;
+  }
+  row_softmax<VPL>(p, valid);
+  const float thr = kth_largest<VPL>(p, valid, k, lane);
+  float w[VPL];
+  float ws = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    w[j] = (valid[j] && p[j] >= thr) ? p[j] : 0.f;  // probs * mask
+    ws += w[j];
+  }
+  if (norm) {
+    ws = fmaxf(wave_sum(ws), 1e-9f);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) w[j] = w[j] / ws;
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    if (!valid[j]) continue;
+    const int64_t i = t * E + lane + kWave * j;
+    store_from_f32<WDT>(weights, i, w[j]);
+    if (probs) probs[i] = p[j];
+  }
+}
+
+// Backward of route_topk: d(weights) -> d(logits) through the mask, the
+// optional renormalisation and the fp32 softmax (probs saved by the forward).
+template <int VPL, int WDT, int LDT>
+__global__ __launch_bounds__(256) void route_topk_bwd_kernel(const void* __restrict__ dweights,
+                                                             const float* __restrict__ probs, int64_t T, int E, int k,
+                                                             int norm, void* __restrict__ dlogits) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float p[VPL], g[VPL];
+  bool valid[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + kWave * j;
+    valid[j] = e < E;
+    p[j] = valid[j] ? probs[t * E + e] : -INFINITY;
+    g[j] = valid[j] ? load_as_f32<WDT>(dweights, t * E + e) : 0.f;
+  }
+  const float thr = kth_largest<VPL>(p, valid, k, lane);
+  bool sel[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) sel[j] = valid[j] && p[j] >= thr;
+  if (norm) {
+    // w = w0 / s, s = max(sum(w0), 1e-9), w0 = p * mask
+    float s = 0.f, gw = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) if (sel[j]) s += p[j];
+    s = wave_sum(s);
+    const bool clamped = s < 1e-9f;
+    const float sc = clamped ? 1e-9f : s;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) if (sel[j]) gw += g[j] * p[j];
+    gw = wave_sum(gw);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) g[j] = clamped ? g[j] / sc : g[j] / sc - gw / (sc * sc);
+  }
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    g[j] = sel[j] ? g[j] : 0.f;  // d(probs) = d(w0) * mask
+    if (valid[j]) dot += g[j] * p[j];
+  }
+  dot = wave_sum(dot);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (valid[j]) store_from_f32<LDT>(dlogits, t * E + lane + kWave * j, p[j] * (g[j] - dot));
+}
+
+// ---- bucketing ------------------------------------------------------------------
+// Three passes over the [T, E] routing weights, chunked by kChunk tokens:
+//  count: per (chunk, expert) number of nonzero weights
+//  scan : per-expert totals -> counts, offsets; per (chunk, expert) base slot
+//  fill : token ids in ascending order within each expert (a stable sort by
+//         expert), slot weights, and the [T, E] token/expert -> slot map.
+constexpr int kChunk = 64;
+
+template <int WDT>
+__global__ __launch_bounds__(256) void bucket_count_kernel(const void* __restrict__ w, int64_t T, int E,
+                                                           int32_t* __restrict__ chunk_cnt) {
+  const int64_t c = blockIdx.x;
+  const int64_t t0 = c * kChunk;
+  const int64_t t1 = (t0 + kChunk < T) ? t0 + kChunk : T;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int n = 0;
+    for (int64_t t = t0; t < t1; ++t) n += load_as_f32<WDT>(w, t * E + e) != 0.f;
+    chunk_cnt[c * E + e] = n;
+  }
+}
+
+// Single block of 1024 threads; E <= 1024.
+__global__ __launch_bounds__(1024) void bucket_scan_kernel(int32_t* __restrict__ chunk_cnt, int64_t n_chunks, int E,
+                                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
+  __shared__ int32_t s_tot[1024];
+  const int e = threadIdx.x;
+  int tot = 0;
+  if (e < E) {
+    for (int64_t c = 0; c < n_chunks; ++c) {
+      const int v = chunk_cnt[c * E + e];
+      chunk_cnt[c * E + e] = tot;  // exclusive within expert
+      tot += v;
+    }
+    counts[e] = tot;
+  }
+  s_tot[e] = (e < E) ? tot : 0;
+  __syncthreads();
+  // inclusive Hillis-Steele scan over 1024 entries
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int v = (e >= off) ? s_tot[e - off] : 0;
+    __syncthreads();
+    s_tot[e] += v;
+    __syncthreads();
+  }
+  const int base = s_tot[e] - ((e < E) ? tot : 0);  // exclusive
+  if (e < E) {
+    offsets[e] = base;
+    for (int64_t c = 0; c < n_chunks; ++c) chunk_cnt[c * E + e] += base;
+  }
+  if (e == E - 1) offsets[E] = s_tot[e];
+}
+
+template <int WDT>
+__global__ __launch_bounds__(256) void bucket_fill_kernel(const void* __restrict__ w, int64_t T, int E,
+                                                          const int32_t* __restrict__ chunk_base,
+                                                          int64_t capacity, int32_t* __restrict__ token_idx,
+                                                          float* __restrict__ slot_w, int32_t* __restrict__ pair_slot) {
+  const int64_t c = blockIdx.x;
+  const int64_t t0 = c * kChunk;
+  const int64_t t1 = (t0 + kChunk < T) ? t0 + kChunk : T;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int64_t pos = chunk_base[c * E + e];
+    for (int64_t t = t0; t < t1; ++t) {
+      const float v = load_as_f32<WDT>(w, t * E + e);
+      int32_t s = -1;
+      if (v != 0.f) {
+        if (pos < capacity) {
+          token_idx[pos] = (int32_t)t;
+          slot_w[pos] = v;
+          s = (int32_t)pos;
+        }
+        ++pos;
+      }
+      pair_slot[t * E + e] = s;
+    }
+  }
+}
+
+// ---- combine ---------------------------------------------------------------------
+// out[t] = dtype( sum over experts e ascending of float(y[slot(t,e)]) * float(w[t,e]) )
+// with the sum in fp32 and each product rounded before it is added (no FMA),
+// which is the reference's `final = final + cur.float() * w.float()` sequence.
+// w == nullptr: unweighted sum (the backward's gradient accumulation over experts).
+template <int DT>
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y, const void* __restrict__ w,
+                                                      const int32_t* __restrict__ pair_slot, int64_t T, int E,
+                                                      int64_t H, uint16_t* __restrict__ out) {
+#pragma clang fp contract(off)
+  const int64_t t = blockIdx.x;
+  // 8 consecutive features per thread per pass (one 128-bit load of y)
+  for (int64_t h0 = (int64_t)threadIdx.x * 8; h0 < H; h0 += (int64_t)blockDim.x * 8) {
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    const bool full = h0 + 8 <= H;
+    for (int e = 0; e < E; ++e) {
+      const int32_t s = pair_slot[t * E + e];
+      if (s < 0) continue;
+      const float we = w ? load_as_f32<DT>(w, t * E + e) : 1.0f;
+      const uint16_t* yr = y + (int64_t)s * H + h0;
+      uint16_t v[8];
+      if (full && (((uintptr_t)yr & 15) == 0)) {
+        const uint4 q = *reinterpret_cast<const uint4*>(yr);
+        v[0] = q.x & 0xFFFF; v[1] = q.x >> 16; v[2] = q.y & 0xFFFF; v[3] = q.y >> 16;
+        v[4] = q.z & 0xFFFF; v[5] = q.z >> 16; v[6] = q.w & 0xFFFF; v[7] = q.w >> 16;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (h0 + j < H) ? yr[j] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float yv = load_as_f32<DT>(v, j);
+        const float prod = w ? yv * we : yv;
+        acc[j] = acc[j] + prod;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (h0 + j < H) store_from_f32<DT>(out, t * H + h0 + j, acc[j]);
+  }
+}
+
+// Backward of the weighted combine, one block per slot m (token t = token_idx[m],
+// expert e): dcur[m] = dtype(float(dout[t]) * w_m) and
+// dweights[t, e] = dtype(sum_h float(dout[t,h]) * float(y[m,h])).
+template <int DT>
+__global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __restrict__ dout,
+                                                          const uint16_t* __restrict__ y,
+                                                          const int32_t* __restrict__ token_idx,
+                                                          const float* __restrict__ slot_w,
+                                                          const int32_t* __restrict__ offsets, int E, int64_t H,
+                                                          uint16_t* __restrict__ dcur, void* __restrict__ dweights) {
+#pragma clang fp contract(off)
+  __shared__ float s_part[4];
+  const int64_t m = blockIdx.x;
+  const int64_t t = token_idx[m];
+  const float wm = slot_w[m];
+  float part = 0.f;
+  for (int64_t h = threadIdx.x; h < H; h += blockDim.x) {
+    const float g = load_as_f32<DT>(dout, t * H + h);
+    store_from_f32<DT>(dcur, m * H + h, g * wm);
+    part += g * load_as_f32<DT>(y, m * H + h);
+  }
+  part = wave_sum(part);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float tot = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += s_part[i];
+    // expert of slot m: largest e with offsets[e] <= m (offsets ascending)
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (offsets[mid] <= m) lo = mid; else hi = mid - 1;
+    }
+    store_from_f32<DT>(dweights, t * E + lo, tot);
+  }
+}
+
+template <int VPL>
+int launch_route(const void* logits, int ldt, int64_t T, int E, int k, int norm, void* weights, int wdt, float* probs,
+                 hipStream_t st) {
+  const unsigned blocks = (unsigned)((T + 3) / 4);
+  USAF_DISPATCH_DT(ldt, LDT, USAF_DISPATCH_DT(wdt, WDT, route_topk_kernel<VPL, LDT, WDT><<<blocks, 256, 0, st>>>(
+                                                            logits, T, E, k, norm, weights, probs)));
+  return check_launch("route_topk");
+}
+
+template <int VPL>
+int launch_route_bwd(const void* dw, int wdt, const float* probs, int64_t T, int E, int k, int norm, void* dlogits,
+                     int ldt, hipStream_t st) {
+  const unsigned blocks = (unsigned)((T + 3) / 4);
+  USAF_DISPATCH_DT(wdt, WDT, USAF_DISPATCH_DT(ldt, LDT, route_topk_bwd_kernel<VPL, WDT, LDT><<<blocks, 256, 0, st>>>(
+                                                            dw, probs, T, E, k, norm, dlogits)));
+  return check_launch("route_topk_bwd");
+}
+
+int check_route_args(const char* what, int64_t T, int64_t E, int64_t k) {
+  if (T < 0 || E <= 0 || E > 1024) return set_error(USAF_ERR_INVALID, "%s: need 0 < E <= 1024, got E=%lld", what, (long long)E);
+  if (k <= 0 || k > E) return set_error(USAF_ERR_INVALID, "%s: need 0 < top_k <= E, got top_k=%lld", what, (long long)k);
+  if (T > (int64_t)0x7fffffff * 4) return set_error(USAF_ERR_INVALID, "%s: too many tokens", what);
+  return USAF_OK;
+}
+
+}  // namespace
+}  // namespace usaf
+
+using namespace usaf;
+
+extern "C" int usaf_hip_route_topk(const void* logits, int32_t logits_dtype, int64_t T, int64_t E, int64_t top_k,
+                                   int32_t norm_topk_prob, void* weights, int32_t weights_dtype, float* probs,
+                                   void* stream) {
+  if (int rc = check_route_args("route_topk", T, E, top_k)) return rc;
+  if (T == 0) return clear_error();
+  if (!logits || !weights) return set_error(USAF_ERR_INVALID, "route_topk: null pointer");
+  hipStream_t st = as_stream(stream);
+  const int e = (int)E, k = (int)top_k, n = norm_topk_prob ? 1 : 0;
+  if (E <= 64) return launch_route<1>(logits, logits_dtype, T, e, k, n, weights, weights_dtype, probs, st);
+  if (E <= 128) return launch_route<2>(logits, logits_dtype, T, e, k, n, weights, weights_dtype, probs, st);
+  if (E <= 256) return launch_route<4>(logits, logits_dtype, T, e, k, n, weights, weights_dtype, probs, st);
+  if (E <= 512) return launch_route<8>(logits, logits_dtype, T, e, k, n, weights, weights_dtype, probs, st);
+  return launch_route<16>(logits, logits_dtype, T, e, k, n, weights, weights_dtype, probs, st);
+}
+
+extern "C" int usaf_hip_route_topk_bwd(const void* dweights, int32_t weights_dtype, const float* probs, int64_t T,
+                                       int64_t E, int64_t top_k, int32_t norm_topk_prob, void* dlogits,
+                                       int32_t logits_dtype, void* stream) {
+  if (int rc = check_route_args("route_topk_bwd", T, E, top_k)) return rc;
+  if (T == 0) return clear_error();
+  if (!dweights || !probs || !dlogits) return set_error(USAF_ERR_INVALID, "route_topk_bwd: null pointer");
+  hipStream_t st = as_stream(stream);
+  const int e = (int)E, k = (int)top_k, n = norm_topk_prob ? 1 : 0;
+  if (E <= 64) return launch_route_bwd<1>(dweights, weights_dtype, probs, T, e, k, n, dlogits, logits_dtype, st);
+  if (E <= 128) return launch_route_bwd<2>(dweights, weights_dtype, probs, T, e, k, n, dlogits, logits_dtype, st);
+  if (E <= 256) return launch_route_bwd<4>(dweights, weights_dtype, probs, T, e, k, n, dlogits, logits_dtype, st);
+  if (E <= 512) return launch_route_bwd<8>(dweights, weights_dtype, probs, T, e, k, n, dlogits, logits_dtype, st);
+  return launch_route_bwd<16>(dweights, weights_dtype, probs, T, e, k, n, dlogits, logits_dtype, st);
+}
+
+extern "C" int64_t usaf_hip_bucket_workspace_ints(int64_t T, int64_t E) {
+  if (T < 0 || E < 0) return -1;
+  return ((T + kChunk - 1) / kChunk) * E;
+}
+
+extern "C" int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dtype, int64_t T, int64_t E,
+                                         int32_t* workspace, int32_t* counts, int32_t* offsets, int32_t* token_idx,
+                                         float* slot_w, int32_t* pair_slot, int64_t capacity, void* stream) {
+  if (T < 0 || E <= 0 || E > 1024) return set_error(USAF_ERR_INVALID, "bucket_by_expert: need 0 < E <= 1024");
+  if (T > 0x7fffffff) return set_error(USAF_ERR_INVALID, "bucket_by_expert: token ids must fit int32");
+  if (!counts || !offsets) return set_error(USAF_ERR_INVALID, "bucket_by_expert: null counts/offsets");
+  if (T > 0 && (!weights || !workspace || !pair_slot || (capacity > 0 && (!token_idx || !slot_w))))
+    return set_error(USAF_ERR_INVALID, "bucket_by_expert: null pointer");
+  hipStream_t st = as_stream(stream);
+  const int64_t n_chunks = (T + kChunk - 1) / kChunk;
+  const int e = (int)E;
+  if (n_chunks > 0) {
+    USAF_DISPATCH_DT(weights_dtype, WDT,
+                     bucket_count_kernel<WDT><<<(unsigned)n_chunks, 256, 0, st>>>(weights, T, e, workspace));
+    if (int rc = check_launch("bucket_by_expert/count")) return rc;
+  }
+  bucket_scan_kernel<<<1, 1024, 0, st>>>(workspace, n_chunks, e, counts, offsets);
+  if (int rc = check_launch("bucket_by_expert/scan")) return rc;
+  if (n_chunks > 0) {
+    USAF_DISPATCH_DT(weights_dtype, WDT,
+                     bucket_fill_kernel<WDT><<<(unsigned)n_chunks, 256, 0, st>>>(
+                         weights, T, e, workspace, capacity, token_idx, slot_w, pair_slot));
+    if (int rc = check_launch("bucket_by_expert/fill")) return rc;
+  }
+  return clear_error();
+}
+
+extern "C" int usaf_hip_moe_combine(const void* y_slots, const void* weights, const int32_t* pair_slot, int64_t T,
+                                    int64_t E, int64_t H, int32_t dtype, void* out, void* stream) {
+  if (T < 0 || E <= 0 || H <= 0) return set_error(USAF_ERR_INVALID, "moe_combine: bad sizes");
+  if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "moe_combine: dtype must be fp16/bf16");
+  if (T == 0) return clear_error();
+  if (!y_slots || !pair_slot || !out) return set_error(USAF_ERR_INVALID, "moe_combine: null pointer");
+  if (T > 0x7fffffff) return set_error(USAF_ERR_INVALID, "moe_combine: too many tokens");
+  hipStream_t st = as_stream(stream);
+  if (dtype == USAF_F16)
+    combine_kernel<USAF_F16><<<(unsigned)T, 256, 0, st>>>((const uint16_t*)y_slots, weights, pair_slot, T, (int)E, H,
+                                                         (uint16_t*)out);
+  else
+    combine_kernel<USAF_BF16><<<(unsigned)T, 256, 0, st>>>((const uint16_t*)y_slots, weights, pair_slot, T, (int)E, H,
+                                                          (uint16_t*)out);
+  return check_launch("moe_combine");
+}
+
+extern "C" int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_t* token_idx,
+                                        const float* slot_w, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
+                                        int32_t dtype, void* dcur, void* dweights, void* stream) {
+  if (S < 0 || E <= 0 || H <= 0) return set_error(USAF_ERR_INVALID, "moe_combine_bwd: bad sizes");
+  if (dtype != USAF_F16 && dtype != USAF_BF16)
+    return set_error(USAF_ERR_INVALID, "moe_combine_bwd: dtype must be fp16/bf16");
+  if (S == 0) return clear_error();
+  if (!dout || !y_slots || !token_idx || !slot_w || !offsets || !dcur || !dweights)
+    return set_error(USAF_ERR_INVALID, "moe_combine_bwd: null pointer");
+  if (S > 0x7fffffff) return set_error(USAF_ERR_INVALID, "moe_combine_bwd: too many slots");
+  hipStream_t st = as_stream(stream);
+  if (dtype == USAF_F16)
+    combine_bwd_kernel<USAF_F16><<<(unsigned)S, 256, 0, st>>>((const uint16_t*)dout, (const uint16_t*)y_slots,
+                                                             token_idx, slot_w, offsets, (int)E, H, (uint16_t*)dcur,
+                                                             dweights);
+  else
+    combine_bwd_kernel<USAF_BF16><<<(unsigned)S, 256, 0, st>>>((const uint16_t*)dout, (const uint16_t*)y_slots,
+                                                              token_idx, slot_w, offsets, (int)E, H, (uint16_t*)dcur,
+                                                              dweights);
+  return check_launch("moe_combine_bwd");
+}

@@ -1,0 +1,339 @@
+"""Routed MoE expert layer on the GPU: routing, bucketing, fused 4-bit
+dequant-GEMMs, combine, and their backward, as torch autograd Functions over
+the C-ABI kernels.
+
+Numerics follow the reference's dense-masked forward
+(usaf/qwen3moe_dml.py:24-86) restricted to routed tokens
+(benchmarks/kaggle_t4_bench.py:253-328): activations in the layer dtype
+(bf16/fp16) with each op's output rounded to it, fp32 accumulation on MFMA,
+and an fp32 combine over experts in ascending expert order.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Optional
+
+import torch
+
+from . import _native as N
+
+
+# ---------------------------------------------------------------------------
+# 4-bit expert tensors
+# ---------------------------------------------------------------------------
+
+@dataclass
+class Q4Tensor:
+    """An HBM-resident tensor in the reference's 4-bit format (quantization.py:21-85)."""
+    q: torch.Tensor        # int8 [groups, ceil(gs/2)]
+    s: torch.Tensor        # fp16 [groups]
+    z: torch.Tensor        # fp16 [groups]
+    shape: torch.Size
+    group_size: int = 128
+
+    @classmethod
+    def from_entry(cls, entry: Any, device=None, group_size: int = 128) -> "Q4Tensor":
+        """Accepts a quantize_state_dict entry ({"q","s","z","shape"[,"group_size"]})
+        or a (q, s, z, shape) tuple (moe_loader.py:203-212)."""
+        if isinstance(entry, Q4Tensor):
+            q, s, z, shape, gs = entry.q, entry.s, entry.z, entry.shape, entry.group_size
+        elif isinstance(entry, dict) and "q" in entry:
+            q, s, z, shape = entry["q"], entry["s"], entry["z"], entry["shape"]
+            gs = entry.get("group_size", group_size)
+        elif isinstance(entry, (tuple, list)) and len(entry) == 4:
+            q, s, z, shape = entry
+            gs = group_size
+        else:
+            raise TypeError(f"not a 4-bit entry: {type(entry).__name__}")
+        dev = torch.device(device) if device is not None else (q.device if q.is_cuda else N.default_device())
+        return cls(N.on_device(q, dev, torch.int8) if q.dtype != torch.uint8 else N.on_device(q.view(torch.int8), dev),
+                   N.on_device(s, dev, torch.float16), N.on_device(z, dev, torch.float16),
+                   torch.Size(shape), int(gs))
+
+    @classmethod
+    def quantize(cls, tensor: torch.Tensor, group_size: int = 128, device=None) -> "Q4Tensor":
+        from .quantization import quantize_4bit
+        q, s, z, shape = quantize_4bit(tensor, group_size, device=device)
+        return cls(q, s, z, shape, group_size)
+
+    @property
+    def device(self) -> torch.device:
+        return self.q.device
+
+    def numel(self) -> int:
+        n = 1
+        for d in self.shape:
+            n *= int(d)
+        return n
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.q, self.s, self.z))
+
+    def dequantize(self, out_dtype: torch.dtype = torch.float16, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        from .quantization import dequantize_4bit
+        return dequantize_4bit(self.q, self.s, self.z, self.shape, self.group_size, out_dtype=out_dtype, out=out)
+
+    def fused_ok(self) -> bool:
+        """True when the layout is the one the fused GEMMs read directly:
+        group size 128 along whole rows (last dim % 128 == 0)."""
+        return self.group_size == 128 and len(self.shape) == 3 and int(self.shape[-1]) % 128 == 0 \
+            and self.q.shape[1] == 64
+
+
+class ExpertWeights:
+    """The two fused expert tensors of one MoE layer, either 4-bit (Q4Tensor)
+    or dense 16-bit tensors of the activation dtype:
+    gate_up [E, 2I, H] and down [E, H, I] (transformers' fused layout)."""
+
+    def __init__(self, gate_up, down):
+        self.gate_up = gate_up
+        self.down = down
+        gs = gate_up.shape
+        ds = down.shape
+        if len(gs) != 3 or len(ds) != 3 or gs[0] != ds[0] or gs[2] != ds[1] or gs[1] != 2 * ds[2]:
+            raise ValueError(f"expert shapes do not form gate_up [E,2I,H] / down [E,H,I]: {tuple(gs)}, {tuple(ds)}")
+        self.E, self.H, self.I = int(gs[0]), int(gs[2]), int(ds[2])
+
+    @property
+    def is_q4(self) -> bool:
+        return isinstance(self.gate_up, Q4Tensor)
+
+    def _ptrs(self, which, dtype: torch.dtype):
+        w = self.gate_up if which == "gate_up" else self.down
+        if isinstance(w, Q4Tensor):
+            if not w.fused_ok():
+                raise NotImplementedError(
+                    f"fused 4-bit GEMM needs group_size 128 along whole rows (shape {tuple(w.shape)}, "
+                    f"group_size {w.group_size})")
+            return w.q.data_ptr(), w.s.data_ptr(), w.z.data_ptr(), None
+        if w.dtype != dtype:
+            raise TypeError(f"dense expert weight dtype {w.dtype} must match the activations ({dtype})")
+        if not w.is_contiguous():
+            raise ValueError("dense expert weights must be contiguous")
+        return None, None, None, w.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# routing and bucketing
+# ---------------------------------------------------------------------------
+
+def route_topk(logits: torch.Tensor, top_k: int, norm_topk_prob: bool, out_dtype: torch.dtype,
+               with_probs: bool = True):
+    """qwen3moe_dml.py:73-83 on the GPU: (weights [T,E] out_dtype, probs fp32 [T,E] or None)."""
+    if logits.dim() != 2:
+        raise ValueError("logits must be [T, E]")
+    logits = logits.contiguous()
+    T, E = logits.shape
+    dev = logits.device
+    weights = torch.empty(T, E, dtype=out_dtype, device=dev)
+    probs = torch.empty(T, E, dtype=torch.float32, device=dev) if with_probs else None
+    N.call("usaf_hip_route_topk", logits.data_ptr(), N.dtype_code(logits.dtype), T, E, int(top_k),
+           1 if norm_topk_prob else 0, weights.data_ptr(), N.dtype_code(out_dtype), N.ptr(probs), N.stream_ptr(dev))
+    return weights, probs
+
+
+@dataclass
+class Buckets:
+    counts: torch.Tensor     # int32 [E]
+    offsets: torch.Tensor    # int32 [E+1]
+    token_idx: torch.Tensor  # int32 [S]
+    slot_w: torch.Tensor     # fp32 [S]
+    pair_slot: torch.Tensor  # int32 [T, E]
+    n_slots: int
+
+
+def bucket_by_expert(weights: torch.Tensor) -> Buckets:
+    """Stable bucketing of routed pairs by expert (kaggle_t4_bench.py:293-306).
+
+    Reads back the slot count once (the reference's batched path also syncs,
+    on `counts.max().item()`) to size the slot buffers.
+    """
+    weights = weights.contiguous()
+    T, E = weights.shape
+    dev = weights.device
+    lib = N.load()
+    ws = torch.empty(max(1, int(lib.usaf_hip_bucket_workspace_ints(T, E))), dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    cap = T * E
+    token_idx = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    slot_w = torch.empty(max(cap, 1), dtype=torch.float32, device=dev)
+    pair_slot = torch.empty(T, E, dtype=torch.int32, device=dev)
+    N.call("usaf_hip_bucket_by_expert", weights.data_ptr(), N.dtype_code(weights.dtype), T, E, ws.data_ptr(),
+           counts.data_ptr(), offsets.data_ptr(), token_idx.data_ptr(), slot_w.data_ptr(), pair_slot.data_ptr(),
+           cap, N.stream_ptr(dev))
+    S = int(offsets[E].item())
+    return Buckets(counts, offsets, token_idx[:S], slot_w[:S], pair_slot, S)
+
+
+def combine(y_slots: torch.Tensor, weights: Optional[torch.Tensor], pair_slot: torch.Tensor, dtype: torch.dtype):
+    T, E = pair_slot.shape
+    H = y_slots.shape[1]
+    out = torch.empty(T, H, dtype=dtype, device=pair_slot.device)
+    N.call("usaf_hip_moe_combine", y_slots.data_ptr(), N.ptr(weights), pair_slot.data_ptr(), T, E, H,
+           N.dtype_code(dtype), out.data_ptr(), N.stream_ptr(pair_slot.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# grad capture (usaf/qwen3moe_dml.py:30-56 protocol)
+# ---------------------------------------------------------------------------
+
+def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Optional[torch.Tensor],
+             b: "Buckets", full_shape, dtype) -> None:
+    """Deliver the weight gradient of ``{prefix}.{which}`` (dW_e = dy_e^T @ x_e over
+    expert e's slots; x_e = x[x_rows] when x_rows is given) to the capture store.
+
+    SparseGradStore (``add_sampled``): only the active positions, by the
+    sampled-product kernel.  Other stores get dense per-expert gradients in
+    the activation dtype, as F.linear's weight grad in the reference:
+    ``store.add(name, ei, g)`` or, for a dict store, accumulation into
+    per-tensor fp16 CPU buffers (usaf/qwen3moe_dml.py:34-47).
+    """
+    store, prefix = capture
+    name = f"{prefix}.{which}"
+    if hasattr(store, "add_sampled"):
+        store.add_sampled(name, slot_major(dy), slot_major(x, rows=x_rows), b.offsets, dtype)
+        return
+    offs = b.offsets.tolist()
+    for ei in range(len(offs) - 1):
+        s0, s1 = offs[ei], offs[ei + 1]
+        if s0 == s1:
+            continue
+        xe = x.index_select(0, x_rows[s0:s1].long()) if x_rows is not None else x[s0:s1]
+        g = torch.mm(dy[s0:s1].t(), xe)  # library GEMM, dtype output as F.linear's weight grad
+        if isinstance(store, dict):
+            buf = store.get(name)
+            if buf is None:
+                buf = torch.zeros(tuple(full_shape), dtype=torch.float16, device="cpu")
+                store[name] = buf
+            buf[ei] += g.detach().to(device="cpu", dtype=torch.float16)
+        else:
+            store.add(name, ei, g)
+
+
+# ---------------------------------------------------------------------------
+# the routed expert layer
+# ---------------------------------------------------------------------------
+
+def _gemm_call(name, *args):
+    N.call(name, *args)
+
+
+class RoutedExpertsFn(torch.autograd.Function):
+    """out = sum_e w[:, e] * down_e(silu(gate_e(x)) * up_e(x)) over routed pairs."""
+
+    @staticmethod
+    def forward(ctx, hs: torch.Tensor, weights: torch.Tensor, ew: ExpertWeights, capture):
+        dt = hs.dtype
+        if dt not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"activations must be fp16 or bf16, got {dt}")
+        hs = hs.contiguous()
+        weights = weights.to(dt).contiguous()
+        T, H = hs.shape
+        E, I = ew.E, ew.I
+        if H != ew.H or weights.shape != (T, E):
+            raise ValueError(f"shape mismatch: hs {tuple(hs.shape)}, weights {tuple(weights.shape)}, "
+                             f"experts E={E} H={ew.H} I={I}")
+        dev = hs.device
+        st = N.stream_ptr(dev)
+        code = N.dtype_code(dt)
+        b = bucket_by_expert(weights)
+        S = b.n_slots
+        gu = torch.empty(S, 2 * I, dtype=dt, device=dev)
+        act = torch.empty(S, I, dtype=dt, device=dev)
+        y = torch.empty(S, H, dtype=dt, device=dev)
+        if S > 0:
+            q, s, z, w16 = ew._ptrs("gate_up", dt)
+            _gemm_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
+                       S, E, I, q, s, z, w16, code, gu.data_ptr(), act.data_ptr(), st)
+            q, s, z, w16 = ew._ptrs("down", dt)
+            _gemm_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, s, z, w16,
+                       code, y.data_ptr(), st)
+        out = combine(y, weights, b.pair_slot, dt)
+        ctx.ew = ew
+        ctx.capture = capture
+        ctx.b = b
+        ctx.save_for_backward(hs, gu, act, y)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout: torch.Tensor):
+        hs, gu, act, y = ctx.saved_tensors
+        ew, b, capture = ctx.ew, ctx.b, ctx.capture
+        dt = hs.dtype
+        dout = dout.to(dt).contiguous()
+        T, H = hs.shape
+        E, I = ew.E, ew.I
+        S = b.n_slots
+        dev = hs.device
+        st = N.stream_ptr(dev)
+        code = N.dtype_code(dt)
+        dweights = torch.zeros(T, E, dtype=dt, device=dev)
+        if S == 0:
+            return torch.zeros_like(hs), dweights, None, None
+        dcur = torch.empty(S, H, dtype=dt, device=dev)
+        N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
+               b.slot_w.data_ptr(), b.offsets.data_ptr(), S, E, H, code, dcur.data_ptr(), dweights.data_ptr(), st)
+        dgu = torch.empty(S, 2 * I, dtype=dt, device=dev)
+        q, s, z, w16 = ew._ptrs("down", dt)
+        _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
+                   q, s, z, w16, code, dgu.data_ptr(), st)
+        if capture is not None:
+            _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt)
+        dx_slots = torch.empty(S, H, dtype=dt, device=dev)
+        q, s, z, w16 = ew._ptrs("gate_up", dt)
+        _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, s, z, w16,
+                   code, dx_slots.data_ptr(), st)
+        if capture is not None:
+            _capture(capture, "gate_up_proj", dgu, hs, b.token_idx, b, (E, 2 * I, H), dt)
+        dhs = combine(dx_slots, None, b.pair_slot, dt)
+        return dhs, dweights, None, None
+
+
+def slot_major(x: torch.Tensor, rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """[S or T, C] -> [C, S] (rows gathered by `rows` when given)."""
+    C = x.shape[1]
+    S = rows.numel() if rows is not None else x.shape[0]
+    out = torch.empty(C, S, dtype=x.dtype, device=x.device)
+    N.call("usaf_hip_gather_transpose", x.data_ptr(), x.stride(0), N.ptr(rows), S, C, out.data_ptr(), S,
+           N.stream_ptr(x.device))
+    return out
+
+
+def routed_experts(hs: torch.Tensor, weights: torch.Tensor, experts: ExpertWeights, capture=None) -> torch.Tensor:
+    """Experts forward with the reference signature's data: hs [T, H], weights [T, E]."""
+    return RoutedExpertsFn.apply(hs, weights, experts, capture)
+
+
+class RouteTopKFn(torch.autograd.Function):
+    """Router softmax + threshold mask (+ renorm) with the kernel backward."""
+
+    @staticmethod
+    def forward(ctx, logits: torch.Tensor, top_k: int, norm: bool, out_dtype: torch.dtype):
+        weights, probs = route_topk(logits, top_k, norm, out_dtype)
+        ctx.top_k, ctx.norm, ctx.ldt = top_k, norm, logits.dtype
+        ctx.save_for_backward(probs)
+        return weights
+
+    @staticmethod
+    def backward(ctx, dweights: torch.Tensor):
+        (probs,) = ctx.saved_tensors
+        T, E = probs.shape
+        dweights = dweights.contiguous()
+        dlogits = torch.empty(T, E, dtype=ctx.ldt, device=probs.device)
+        N.call("usaf_hip_route_topk_bwd", dweights.data_ptr(), N.dtype_code(dweights.dtype), probs.data_ptr(), T, E,
+               ctx.top_k, 1 if ctx.norm else 0, dlogits.data_ptr(), N.dtype_code(ctx.ldt), N.stream_ptr(probs.device))
+        return dlogits, None, None, None
+
+
+def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_topk_prob: bool,
+              experts: ExpertWeights, capture=None) -> torch.Tensor:
+    """qwen3moe_dml.py:67-86: router F.linear (library GEMM), routing kernel,
+    routed experts; hs [B, S, H] or [T, H]."""
+    shape = hs.shape
+    x = hs.reshape(-1, shape[-1])
+    logits = torch.nn.functional.linear(x, router_weight)
+    weights = RouteTopKFn.apply(logits, top_k, norm_topk_prob, x.dtype)
+    out = routed_experts(x, weights, experts, capture)
+    return out.view(shape)

@@ -1,0 +1,540 @@
+"""HBM-resident quantized expert cache and sparse gradient stores.
+
+Drop-in for usaf/moe_loader.py.  Differences of placement, not of interface:
+
+* ``QuantizedExpertCache`` keeps every 4-bit entry in HBM (the reference keeps
+  them in CPU RAM) and fills its LRU of fp16 expert copies with the dequant
+  kernel instead of a CPU dequant + PCIe copy.  ``get_q4`` additionally hands
+  the 4-bit tensors to the fused expert GEMMs.  Resident copies of trainable
+  layers and their overlays also live in HBM.
+* ``SparseGradStore`` keeps its compact fp32 gradients in HBM and accepts
+  sampled gradients straight from the fused backward (``add_sampled``) besides
+  the reference's dense per-expert ``add``.
+"""
+from __future__ import annotations
+
+import fnmatch
+from collections import OrderedDict
+from typing import Any, Dict, List, Optional, Tuple, Union
+
+import torch
+import torch.nn as nn
+
+from . import _native as N
+from .moe import Q4Tensor
+from .quantization import dequantize_4bit
+
+
+def save_quantized_state_dict(q_dict: Dict[str, Any], path: str, *, _use_new_zipfile_serialization: bool = True
+                              ) -> None:
+    """moe_loader.py:25-37: torch.save of the quantized dict (tensors moved to CPU first)."""
+    def cpu(x):
+        if isinstance(x, torch.Tensor):
+            return x.detach().cpu()
+        if isinstance(x, dict):
+            return {k: cpu(v) for k, v in x.items()}
+        if isinstance(x, tuple):
+            return tuple(cpu(v) for v in x)
+        return x
+    torch.save(cpu(q_dict), path, _use_new_zipfile_serialization=_use_new_zipfile_serialization)
+
+
+def load_quantized_state_dict(path: str, map_location: Union[str, torch.device] = "cpu") -> Dict[str, Any]:
+    """moe_loader.py:40-57 (weights_only load; raises TypeError if not a dict)."""
+    loaded = torch.load(path, map_location=map_location, weights_only=True)
+    if not isinstance(loaded, dict):
+        raise TypeError(f"Expected quantized state dict (dict), got {type(loaded).__name__}")
+    return loaded
+
+
+def _is_q4_entry(entry) -> bool:
+    return isinstance(entry, Q4Tensor) or (isinstance(entry, dict) and "q" in entry) or \
+        (isinstance(entry, tuple) and len(entry) == 4)
+
+
+class QuantizedExpertCache:
+    """LRU of dequantized fp16 expert modules over an HBM-resident 4-bit store.
+
+    Mirrors moe_loader.py:60-524.  Keys are expert module names
+    (``model.layers.L.mlp.experts``); each holds that module's parameters
+    (``gate_up_proj``, ``down_proj``).
+
+    Args:
+        quantized_dict: output of ``quantize_state_dict`` (dict or tuple entries);
+                        moved to ``device`` once.
+        device:         GPU holding the 4-bit store and the fp16 copies.
+        max_cached:     LRU size in expert modules.
+        group_size:     group size of the 4-bit entries.
+        max_cached_bytes: optional byte cap on the fp16 LRU (checked with max_cached).
+        dtype:          dtype of the dequantized copies (fp16 as the reference, or bf16).
+    """
+
+    def __init__(self, quantized_dict: Dict[str, Any], device: torch.device, max_cached: int = 2,
+                 group_size: int = 128, *, max_cached_bytes: Optional[int] = None,
+                 dtype: torch.dtype = torch.float16) -> None:
+        N.require_gpu()
+        self._device = torch.device(device)
+        if self._device.type != "cuda":
+            raise ValueError("QuantizedExpertCache holds its store in GPU memory; pass a cuda device")
+        self._max_cached = max(max_cached, 1)
+        self._max_bytes = max_cached_bytes
+        self._group_size = group_size
+        self._dtype = dtype
+        self._q_dict: Dict[str, Any] = {}
+        for name, entry in quantized_dict.items():
+            if _is_q4_entry(entry):
+                self._q_dict[name] = Q4Tensor.from_entry(entry, self._device, group_size)
+            elif isinstance(entry, torch.Tensor):
+                self._q_dict[name] = entry.detach().to(self._device)
+            else:
+                self._q_dict[name] = entry
+        self._cache: "OrderedDict[str, Dict[str, torch.Tensor]]" = OrderedDict()
+        self.overlays: Dict[str, Tuple[torch.Tensor, torch.Tensor]] = {}
+        self._prefetched: Dict[str, Tuple[Dict[str, torch.Tensor], torch.cuda.Event]] = {}
+        self._prefetch_stream: Optional[torch.cuda.Stream] = None
+        self._prefetch_disabled = False
+        self._expert_to_params: Dict[str, List[Tuple[str, str]]] = {}
+        self._build_index()
+        self._resident: Dict[str, Dict[str, torch.Tensor]] = {}
+        self._resident_active = False
+        self.hits = 0
+        self.misses = 0
+
+    # ---- indexing -----------------------------------------------------------------
+
+    def _build_index(self) -> None:
+        """moe_loader.py:111-128: group keys by expert module name."""
+        e2p: Dict[str, List[Tuple[str, str]]] = {}
+        for full_name in self._q_dict:
+            parts = full_name.rsplit(".", 1)
+            if len(parts) != 2:
+                continue
+            e2p.setdefault(parts[0], []).append((full_name, parts[1]))
+        self._expert_to_params = e2p
+
+    # ---- 4-bit access for the fused path --------------------------------------------
+
+    def get_q4(self, expert_module_name: str) -> Dict[str, Any]:
+        """The HBM 4-bit tensors (Q4Tensor) or dense entries of a module, by local name."""
+        out = {}
+        for full_name, local in self._expert_to_params.get(expert_module_name, []):
+            entry = self._q_dict.get(full_name)
+            if entry is not None:
+                out[local] = entry
+        return out
+
+    # ---- dequantized copies --------------------------------------------------------
+
+    def _nbytes(self, params: Dict[str, torch.Tensor]) -> int:
+        return sum(t.numel() * t.element_size() for t in params.values())
+
+    def _dequant(self, expert_module_name: str, stream=None) -> Dict[str, torch.Tensor]:
+        """HBM dequant of a module's params with overlays applied (moe_loader.py:183-224)."""
+        out: Dict[str, torch.Tensor] = {}
+        ctx = torch.cuda.stream(stream) if stream is not None else torch.cuda.device(self._device)
+        with ctx:
+            for full_name, local in self._expert_to_params.get(expert_module_name, []):
+                entry = self._q_dict.get(full_name)
+                if isinstance(entry, Q4Tensor):
+                    t = entry.dequantize(self._dtype)
+                elif isinstance(entry, torch.Tensor):
+                    t = entry.to(self._dtype).clone()
+                else:
+                    continue
+                ov = self.overlays.get(full_name)
+                if ov is not None:
+                    overlay_scatter(t, ov[0], ov[1])
+                out[local] = t
+        return out
+
+    # the reference's name for the same step (it ran on the CPU there)
+    _dequant_cpu = _dequant
+
+    def _get_resident(self, expert_module_name: str) -> Dict[str, torch.Tensor]:
+        """moe_loader.py:226-247: resident base with overlays applied (a fresh copy)."""
+        out = {}
+        for local, base in self._resident[expert_module_name].items():
+            t = base.clone()
+            ov = self.overlays.get(f"{expert_module_name}.{local}")
+            if ov is not None:
+                overlay_scatter(t, ov[0], ov[1])
+            out[local] = t
+        return out
+
+    def _evict_for(self, incoming_bytes: int) -> None:
+        while self._cache and (len(self._cache) >= self._max_cached or (
+                self._max_bytes is not None and
+                sum(self._nbytes(p) for p in self._cache.values()) + incoming_bytes > self._max_bytes)):
+            self._cache.popitem(last=False)
+
+    def get_expert_weights(self, expert_module_name: str) -> Dict[str, torch.nn.Parameter]:
+        """moe_loader.py:130-181: fp16 Parameters of a module on the GPU (LRU)."""
+        if expert_module_name in self._cache:
+            self.hits += 1
+            self._cache.move_to_end(expert_module_name)
+            cached = self._cache[expert_module_name]
+            return {p: torch.nn.Parameter(t, requires_grad=t.requires_grad) for p, t in cached.items()}
+        self.misses += 1
+        if expert_module_name in self._resident:
+            params = self._get_resident(expert_module_name)
+            for k, v in self._dequant(expert_module_name).items():
+                params.setdefault(k, v)
+        else:
+            pending = self._prefetched.pop(expert_module_name, None)
+            if pending is not None:
+                params, ev = pending
+                torch.cuda.current_stream(self._device).wait_event(ev)
+                for t in params.values():
+                    t.record_stream(torch.cuda.current_stream(self._device))
+            else:
+                params = self._dequant(expert_module_name)
+        self._evict_for(self._nbytes(params))
+        self._cache[expert_module_name] = params
+        return {p: torch.nn.Parameter(t, requires_grad=True) for p, t in params.items()}
+
+    def free_frozen(self, detach_at: int) -> None:
+        """moe_loader.py:249-261: drop 4-bit entries of layers 0..detach_at."""
+        for li in range(detach_at + 1):
+            prefix = f"model.layers.{li}."
+            for key in list(self._q_dict.keys()):
+                if key.startswith(prefix):
+                    del self._q_dict[key]
+            name = f"model.layers.{li}.mlp.experts"
+            self._expert_to_params.pop(name, None)
+            self._prefetched.pop(name, None)
+
+    def make_resident(self, train_layers, dequant_batch: int = 8, only_params=None) -> None:
+        """moe_loader.py:263-299: dequantize trainable layers once into HBM fp16."""
+        self._resident_active = False
+        for li in sorted(train_layers):
+            name = f"model.layers.{li}.mlp.experts"
+            entries = self._expert_to_params.get(name)
+            if not entries:
+                continue
+            res: Dict[str, torch.Tensor] = {}
+            for full_name, local in entries:
+                if only_params is not None and local not in only_params:
+                    continue
+                entry = self._q_dict.get(full_name)
+                if isinstance(entry, Q4Tensor):
+                    res[local] = entry.dequantize(self._dtype)
+                elif isinstance(entry, torch.Tensor):
+                    res[local] = entry.to(self._dtype).clone()
+            self._resident[name] = res
+        self._resident_active = True
+
+    def setup_vk_dequant(self, train_layers) -> None:
+        """moe_loader.py:301-350 uploaded codes to Vulkan buffers; the codes already
+        live in HBM here and the dequant kernel always runs on the GPU."""
+        return None
+
+    def setup_vk_streaming(self, max_layers: int = 999) -> None:
+        """moe_loader.py:352-409 counterpart; nothing to upload (see setup_vk_dequant)."""
+        return None
+
+    def apply_resident_overlays(self, active_idx, masters) -> None:
+        """moe_loader.py:411-423: scatter master values into the resident copies."""
+        self._scatter_masters(active_idx, masters)
+
+    def sync_resident(self, active_idx, masters) -> None:
+        """moe_loader.py:425-443: propagate optimizer masters into the resident copies."""
+        if not self._resident_active:
+            return
+        self._scatter_masters(active_idx, masters)
+
+    def _scatter_masters(self, active_idx, masters) -> None:
+        for fname, aidx in active_idx.items():
+            parts = fname.rsplit(".", 1)
+            if len(parts) != 2:
+                continue
+            name, local = parts
+            if name not in self._resident or local not in self._resident[name]:
+                continue
+            overlay_scatter(self._resident[name][local], aidx, masters[fname].data)
+
+    def prefetch(self, expert_module_name: str) -> None:
+        """moe_loader.py:445-471: dequantize ahead on a side stream."""
+        if self._prefetch_disabled:
+            return
+        if (expert_module_name in self._cache or expert_module_name in self._prefetched
+                or expert_module_name not in self._expert_to_params or expert_module_name in self._resident):
+            return
+        if self._prefetch_stream is None:
+            self._prefetch_stream = torch.cuda.Stream(device=self._device)
+        self._prefetch_stream.wait_stream(torch.cuda.current_stream(self._device))
+        params = self._dequant(expert_module_name, stream=self._prefetch_stream)
+        ev = torch.cuda.Event()
+        ev.record(self._prefetch_stream)
+        self._prefetched[expert_module_name] = (params, ev)
+
+    def clear_prefetch(self) -> None:
+        """moe_loader.py:473-486: drop pending prefetches (waiting for them)."""
+        for _, ev in self._prefetched.values():
+            ev.synchronize()
+        self._prefetched.clear()
+
+    def evict(self, expert_module_name: str) -> None:
+        self._cache.pop(expert_module_name, None)
+
+    def evict_all(self) -> None:
+        self._cache.clear()
+
+    @property
+    def cached_experts(self) -> List[str]:
+        return list(reversed(self._cache.keys()))
+
+    @property
+    def device(self) -> torch.device:
+        return self._device
+
+    def estimate_vram_mb(self) -> float:
+        """MiB held by the fp16 LRU (moe_loader.py:506-512)."""
+        return sum(self._nbytes(p) for p in self._cache.values()) / (1024 * 1024)
+
+    def estimate_cpu_mb(self) -> float:
+        """MiB of the 4-bit store (moe_loader.py:514-524; it sits in HBM here)."""
+        total = 0
+        for entry in self._q_dict.values():
+            if isinstance(entry, Q4Tensor):
+                total += entry.nbytes()
+            elif isinstance(entry, torch.Tensor):
+                total += entry.numel() * entry.element_size()
+        return total / (1024 * 1024)
+
+
+def overlay_scatter(base: torch.Tensor, idx: torch.Tensor, vals: torch.Tensor) -> None:
+    """base.flat[idx] = base.dtype(vals) on the GPU (moe_loader.py:218-221)."""
+    if not base.is_contiguous():
+        raise ValueError("overlay target must be contiguous")
+    dev = base.device
+    idx = idx.reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
+    vals = vals.detach().reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    if idx.numel() != vals.numel():
+        raise ValueError(f"overlay has {idx.numel()} indices and {vals.numel()} values")
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    N.call("usaf_hip_overlay_scatter", base.data_ptr(), N.dtype_code(base.dtype), base.numel(), idx.data_ptr(),
+           vals.data_ptr(), idx.numel(), bad.data_ptr(), N.stream_ptr(dev))
+    if bool(bad.item()):
+        raise IndexError("overlay index out of range")
+
+
+class SparseGradStore:
+    """Compact fp32 gradients at the active positions of each expert tensor, in HBM.
+
+    Mirrors moe_loader.py:527-581 (``compact``, ``zero_``, ``add``,
+    ``n_captured``).  ``add_sampled`` is the fused path: it receives the
+    slot-major operands of a weight gradient from the expert backward and
+    computes only the active entries (usaf_hip_sddmm_masked).
+    """
+
+    def __init__(self, active_idx: Dict[str, torch.Tensor], shapes: Dict[str, Any], device=None) -> None:
+        dev = torch.device(device) if device is not None else N.default_device()
+        self.device = dev
+        self.compact: Dict[str, torch.Tensor] = {}
+        self._csr: Dict[str, tuple] = {}
+        self._maps: Dict[str, Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = {}
+        for name, idx in active_idx.items():
+            idx = idx.reshape(-1).to(device=dev, dtype=torch.long)
+            shape = [int(s) for s in shapes[name]]
+            self.compact[name] = torch.zeros(idx.numel(), dtype=torch.float32, device=dev)
+            if len(shape) < 2:
+                raise ValueError(f"{name}: expert tensors are [E, rows, ...], got shape {shape}")
+            E, R = shape[0], shape[1]
+            C = 1
+            for s in shape[2:]:
+                C *= s
+            order = torch.argsort(idx, stable=True)
+            sidx = idx[order]
+            identity = bool(torch.equal(order, torch.arange(idx.numel(), device=dev)))
+            rows = torch.div(sidx, C, rounding_mode="floor")
+            cols = (sidx - rows * C).to(torch.int32)
+            row_ptr = torch.zeros(E * R + 1, dtype=torch.int64, device=dev)
+            if idx.numel():
+                if int(sidx[0]) < 0 or int(sidx[-1]) >= E * R * C:
+                    raise IndexError(f"{name}: active index out of range for shape {shape}")
+                row_ptr[1:] = torch.cumsum(torch.bincount(rows, minlength=E * R), 0)
+            self._csr[name] = (row_ptr, cols.contiguous(), None if identity else order.contiguous(), E, R, C)
+
+    def zero_(self) -> None:
+        for v in self.compact.values():
+            v.zero_()
+
+    def add_sampled(self, full_name: str, rowT: torch.Tensor, colT: torch.Tensor, offsets: torch.Tensor,
+                    dtype: torch.dtype) -> None:
+        """compact[name] += dtype(rowT[o, slots_e] . colT[i, slots_e]) at each active (e, o, i)."""
+        csr = self._csr.get(full_name)
+        if csr is None:
+            return
+        row_ptr, cols, pos_map, E, R, C = csr
+        if rowT.shape[0] != R or colT.shape[0] != C or rowT.shape[1] != colT.shape[1]:
+            raise ValueError(f"{full_name}: operands {tuple(rowT.shape)} / {tuple(colT.shape)} do not match "
+                             f"the weight rows {R} x cols {C}")
+        if not (rowT.is_contiguous() and colT.is_contiguous()):
+            raise ValueError("slot-major operands must be contiguous")
+        N.call("usaf_hip_sddmm_masked", rowT.data_ptr(), colT.data_ptr(), rowT.shape[1], offsets.data_ptr(), E, R,
+               row_ptr.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
+               self.compact[full_name].data_ptr(), N.stream_ptr(self.device))
+
+    def add(self, full_name: str, ei: int, g: torch.Tensor) -> None:
+        """Reference protocol (moe_loader.py:564-578): dense grad of expert ei."""
+        csr = self._csr.get(full_name)
+        if csr is None:
+            return
+        row_ptr, cols, pos_map, E, R, C = csr
+        ei = int(ei)
+        p0, p1 = int(row_ptr[ei * R]), int(row_ptr[(ei + 1) * R])
+        if p0 == p1:
+            return
+        rows = torch.searchsorted(row_ptr, torch.arange(p0, p1, device=row_ptr.device), right=True) - 1
+        local = (rows - ei * R) * C + cols[p0:p1].long()
+        pos = pos_map[p0:p1] if pos_map is not None else torch.arange(p0, p1, device=row_ptr.device)
+        vals = g.detach().to(self.device).reshape(-1).gather(0, local).float()
+        self.compact[full_name].index_add_(0, pos, vals)
+
+    def n_captured(self) -> int:
+        return len(self.compact)
+
+
+class TopKImportanceStore:
+    """moe_loader.py:584-631: per-expert top |grad| candidates, global top-k in
+    ``select`` (torch ops on the GPU over dense per-expert gradients)."""
+
+    def __init__(self, shapes: Dict[str, Any], frac: float, cand_mult: float = 2.0) -> None:
+        self._shapes = shapes
+        self._frac = frac
+        self._cand = cand_mult
+        self._vals: Dict[str, Dict[int, torch.Tensor]] = {n: {} for n in shapes}
+        self._idx: Dict[str, Dict[int, torch.Tensor]] = {n: {} for n in shapes}
+
+    def zero_(self) -> None:
+        for n in self._vals:
+            self._vals[n].clear()
+            self._idx[n].clear()
+
+    def add(self, full_name: str, ei: int, g: torch.Tensor) -> None:
+        if full_name not in self._vals:
+            return
+        flat = g.detach().float().reshape(-1).abs()
+        k = max(1, int(flat.numel() * self._frac * self._cand))
+        v, i = torch.topk(flat, min(k, flat.numel()))
+        self._vals[full_name][int(ei)] = v
+        self._idx[full_name][int(ei)] = i.to(torch.long) + int(ei) * flat.numel()
+
+    def select(self, frac: float | None = None) -> Dict[str, torch.Tensor]:
+        frac = self._frac if frac is None else frac
+        out: Dict[str, torch.Tensor] = {}
+        for name, shape in self._shapes.items():
+            if not self._vals[name]:
+                continue
+            vals = torch.cat(list(self._vals[name].values()))
+            idxs = torch.cat(list(self._idx[name].values()))
+            numel = 1
+            for s in shape:
+                numel *= int(s)
+            k = min(max(1, int(numel * frac)), vals.numel())
+            out[name] = idxs[torch.topk(vals, k).indices]
+        return out
+
+    def n_captured(self) -> int:
+        return sum(len(d) for d in self._vals.values())
+
+
+def _move_module_tensors_to(module: nn.Module, target: torch.device) -> None:
+    for pname, p in list(module._parameters.items()):
+        if p is None or p.device == target:
+            continue
+        new = torch.nn.Parameter(p.detach().to(target), requires_grad=p.requires_grad)
+        if p.grad is not None:
+            new.grad = p.grad.to(target)
+        module._parameters[pname] = new
+    for bname, b in list(module._buffers.items()):
+        if b is None or b.device == target:
+            continue
+        module._buffers[bname] = b.to(target)
+
+
+def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], device: torch.device, *,
+                              max_cached_experts: int = 2, group_size: int = 128,
+                              expert_pattern: str = "*.mlp.experts", verbose: bool = True,
+                              fused: bool = True) -> nn.Module:
+    """moe_loader.py:650-769.  Non-expert params go to the GPU; expert modules get
+    a pre-hook that attaches their HBM 4-bit tensors (``module._usaf_q4``, read
+    by the fused forward) -- or, with ``fused=False``, dequantized fp16
+    Parameters from the LRU as the reference does -- and a post-hook that
+    detaches them again."""
+    cache = QuantizedExpertCache(quantized_dict, device=device, max_cached=max_cached_experts,
+                                 group_size=group_size)
+    expert_names: List[str] = []
+    n_gpu = bytes_gpu = 0
+    for mname, mod in model.named_modules():
+        if fnmatch.fnmatch(mname, expert_pattern):
+            expert_names.append(mname)
+            mod._parameters.clear()
+            continue
+        for p in mod._parameters.values():
+            if p is not None:
+                n_gpu += 1
+                bytes_gpu += p.numel() * p.element_size()
+        _move_module_tensors_to(mod, torch.device(device))
+    if verbose:
+        print(f"  GPU (resident): {n_gpu} tensors, {bytes_gpu / 1e9:.2f}GB")
+        print(f"  HBM (4-bit):    {len(quantized_dict)} entries, ~{cache.estimate_cpu_mb() / 1024:.2f}GiB")
+    state: Dict[str, int] = {"resident": 0, "max": 0}
+    model._expert_grads = {}
+    grad_store = model._expert_grads
+
+    def make_pre_hook(mod_name: str):
+        def pre_hook(module: nn.Module, _args) -> None:
+            if fused:
+                module._usaf_q4 = cache.get_q4(mod_name)
+            else:
+                for pname, param in cache.get_expert_weights(mod_name).items():
+                    module._parameters[pname] = param
+                    full = f"{mod_name}.{pname}"
+
+                    def _cap(p, _full=full):
+                        if p.grad is not None:
+                            grad_store[_full] = p.grad.detach()
+                    param.register_post_accumulate_grad_hook(_cap)
+            state["resident"] += 1
+            state["max"] = max(state["max"], state["resident"])
+        return pre_hook
+
+    def post_hook(module: nn.Module, _args, output):
+        module._parameters.clear()
+        module._usaf_q4 = None
+        state["resident"] -= 1
+        return output
+
+    model._stream_state = state
+    for name, mod in model.named_modules():
+        if name in expert_names:
+            mod.register_forward_pre_hook(make_pre_hook(name))
+            mod.register_forward_hook(post_hook)
+    model._quantized_cache = cache
+    return model
+
+
+def get_quantized_cache(model: nn.Module) -> Optional[QuantizedExpertCache]:
+    return getattr(model, "_quantized_cache", None)
+
+
+def apply_captured_expert_grads(model: nn.Module, scale: float = 1.0) -> int:
+    """moe_loader.py:778-802: captured expert grads -> canonical Parameters."""
+    store: Dict[str, torch.Tensor] = getattr(model, "_expert_grads", {})
+    if not store:
+        return 0
+    params = dict(model.named_parameters())
+    applied = 0
+    for full, g in store.items():
+        p = params.get(full)
+        if p is not None:
+            p.grad = (g.detach().float() * scale).to(device=p.device, dtype=p.dtype)
+            applied += 1
+    store.clear()
+    return applied
+
+
+def load_and_stream(model: nn.Module, quantized_path: str, device: torch.device, **stream_kwargs: Any) -> nn.Module:
+    """moe_loader.py:805-824."""
+    return setup_quantized_streaming(model, load_quantized_state_dict(quantized_path), device, **stream_kwargs)

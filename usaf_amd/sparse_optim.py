@@ -1,0 +1,169 @@
+"""SparseAdam over the active elements, with state in HBM.
+
+Drop-in for usaf/sparse_optim.py (same constructor, step/refresh/reselect/
+state_dict surface).  The update itself is one HIP kernel per parameter
+(``usaf_hip_sparse_adam_step``) over the compact fp32 vectors; the m/v state
+lives on the parameter's device instead of the CPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+
+class SparseAdam:
+    """Adam (L2 weight decay folded into the gradient) on flat active indices.
+
+    ``compact_params=True``: each named parameter is itself the compact fp32
+    vector aligned with ``active_idx`` (the training script's masters).
+    ``compact_params=False``: parameters are full tensors; the active elements
+    are gathered, updated and scattered back.
+    """
+
+    def __init__(
+        self,
+        named_params: dict[str, torch.nn.Parameter],
+        active_mask: dict[str, torch.Tensor] | None = None,
+        active_idx: dict[str, torch.Tensor] | None = None,
+        lr: float = 1e-4,
+        betas: tuple = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 0.01,
+        compact_params: bool = False,
+    ):
+        self.compact_params = compact_params
+        self.lr = lr
+        self.betas = betas
+        self.eps = eps
+        self.weight_decay = weight_decay
+        self._named: dict[str, torch.nn.Parameter] = dict(named_params)
+        self._step = 0
+        self._active_ids: list[str] = []
+        self._idx: dict[str, torch.Tensor] = {}
+        self._m: dict[str, torch.Tensor] = {}
+        self._v: dict[str, torch.Tensor] = {}
+        if active_idx is not None:
+            self._build_state_from_idx(active_idx)
+        else:
+            self._build_state(active_mask or {})
+
+    def _device_of(self, name: str) -> torch.device:
+        p = self._named[name]
+        return p.device if p.is_cuda else N.default_device()
+
+    def _init_slot(self, name: str, idx: torch.Tensor) -> None:
+        dev = self._device_of(name)
+        self._active_ids.append(name)
+        self._idx[name] = idx.to(dev)
+        self._m[name] = torch.zeros(idx.numel(), device=dev, dtype=torch.float32)
+        self._v[name] = torch.zeros(idx.numel(), device=dev, dtype=torch.float32)
+
+    def _build_state_from_idx(self, active_idx: dict[str, torch.Tensor]):
+        """sparse_optim.py:43-53."""
+        self._active_ids, self._idx, self._m, self._v = [], {}, {}, {}
+        for name, idx in active_idx.items():
+            if name not in self._named or idx is None or idx.numel() == 0:
+                continue
+            self._init_slot(name, idx.reshape(-1).to(dtype=torch.long))
+
+    def _build_state(self, active_mask: dict[str, torch.Tensor]):
+        """sparse_optim.py:55-68."""
+        self._active_ids, self._idx, self._m, self._v = [], {}, {}, {}
+        for name in self._named:
+            mask = active_mask.get(name)
+            if mask is None:
+                continue
+            idx = mask.reshape(-1).to(dtype=torch.bool).nonzero(as_tuple=False).reshape(-1)
+            if idx.numel() == 0:
+                continue
+            self._init_slot(name, idx)
+
+    def zero_grad(self, set_to_none: bool = False):
+        for name in self._active_ids:
+            param = self._named[name]
+            if param.grad is not None:
+                if set_to_none:
+                    param.grad = None
+                else:
+                    param.grad.zero_()
+
+    def step(self, compact_grads: dict[str, torch.Tensor] | None = None):
+        """One Adam step over the active elements (sparse_optim.py:86-134).
+
+        compact_grads: optional name -> 1-D gradient aligned with ``active_idx``
+        (e.g. ``SparseGradStore.compact``), used instead of ``param.grad``.
+        """
+        self._step += 1
+        beta1, beta2 = self.betas
+        for name in self._active_ids:
+            param = self._named[name]
+            if compact_grads is None and param.grad is None:
+                continue
+            dev = param.device
+            if not param.is_cuda:
+                raise RuntimeError(f"SparseAdam: parameter {name} must live on the GPU")
+            if compact_grads is not None:
+                g = compact_grads.get(name)
+                if g is None:
+                    continue
+                grad = g.detach().to(device=dev, dtype=torch.float32).contiguous()
+            else:
+                grad = param.grad.detach().reshape(-1).index_select(0, self._idx[name]).float().contiguous()
+            if self.compact_params:
+                if param.dtype != torch.float32 or not param.is_contiguous():
+                    raise TypeError("compact_params=True needs contiguous fp32 parameters (the masters)")
+                target = param.data
+            else:
+                target = param.data.reshape(-1).index_select(0, self._idx[name]).float().contiguous()
+            if grad.numel() != target.numel():
+                raise ValueError(f"SparseAdam: gradient for {name} has {grad.numel()} entries, expected "
+                                 f"{target.numel()}")
+            N.call("usaf_hip_sparse_adam_step", target.data_ptr(), grad.data_ptr(), self._m[name].data_ptr(),
+                   self._v[name].data_ptr(), target.numel(), float(self.lr), float(beta1), float(beta2),
+                   float(self.eps), float(self.weight_decay), self._step, N.stream_ptr(dev))
+            if not self.compact_params:
+                flat = param.data.reshape(-1)
+                flat.scatter_(0, self._idx[name], target.to(param.dtype))
+
+    def refresh(self, model):
+        """Re-bind current model Parameters by name (sparse_optim.py:136-150)."""
+        current = dict(model.named_parameters())
+        for name in self._active_ids:
+            if name not in current:
+                continue
+            if current[name].numel() != self._named[name].numel():
+                continue
+            self._named[name] = current[name]
+
+    def reselect(self, named_params: dict[str, torch.nn.Parameter], new_active_mask: dict[str, torch.Tensor]):
+        self._named = dict(named_params)
+        self._build_state(new_active_mask)
+
+    def state_dict(self) -> dict:
+        """m/v/step for checkpoints (CPU copies, as the reference stores them)."""
+        return {
+            "step": self._step,
+            "m": {n: t.detach().cpu().clone() for n, t in self._m.items()},
+            "v": {n: t.detach().cpu().clone() for n, t in self._v.items()},
+        }
+
+    def load_state_dict(self, sd: dict) -> None:
+        self._step = int(sd["step"])
+        for n, t in sd["m"].items():
+            if n in self._m and t.numel() == self._m[n].numel():
+                self._m[n] = t.detach().to(self._m[n].device, torch.float32).clone()
+        for n, t in sd["v"].items():
+            if n in self._v and t.numel() == self._v[n].numel():
+                self._v[n] = t.detach().to(self._v[n].device, torch.float32).clone()
+
+    @property
+    def num_active_params(self) -> int:
+        return sum(idx.numel() for idx in self._idx.values())
+
+    @property
+    def optimizer_memory_mb(self) -> float:
+        total = 0
+        for name in self._active_ids:
+            total += self._m[name].numel() * 4 + self._v[name].numel() * 4
+        return total / (1024 * 1024)
