@@ -229,7 +229,7 @@ def bench_moe_kernels(L, reps: int) -> dict:
     qg = ew._ptrs("gate_up", dt)
     qd = ew._ptrs("down", dt)
     calls = {
-        "gate_up_fwd": lambda: N.call("usaf_hip_moe_gate_up_fwd", x.data_ptr(), H, b.token_idx.data_ptr(),
+        "gate_up_fwd": lambda: N.call("usaf_hip_moe_gate_up_fwd", x.data_ptr(), T, H, b.token_idx.data_ptr(),
                                       b.offsets.data_ptr(), S, E, I, *qg, code, gu.data_ptr(), act.data_ptr(), st),
         "down_fwd": lambda: N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *qd,
                                    code, y.data_ptr(), st),

@@ -150,8 +150,8 @@ int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_
 
 /* Replaces qwen3moe_dml.py:58-60 per routed slot: gu[s] = x[token_idx[s]] @ W_gate_up[e]^T
  * ([S, 2I], dtype-rounded), act[s] = dtype(dtype(silu(gate)) * up) ([S, I]).
- * W_gate_up [E, 2I, H]; needs H % 128 == 0, I % 64 == 0. */
-int usaf_hip_moe_gate_up_fwd(const void* x, int64_t H, const int32_t* token_idx, const int32_t* offsets, int64_t S,
+ * x [T, H] (token_idx values < T); W_gate_up [E, 2I, H]; needs H % 128 == 0, I % 64 == 0. */
+int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T, int64_t H, const int32_t* token_idx, const int32_t* offsets, int64_t S,
                              int64_t E, int64_t I, const int8_t* wq, const uint16_t* ws, const uint16_t* wz,
                              const void* w16, int32_t dtype, void* gu, void* act, void* stream);
 

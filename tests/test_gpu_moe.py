@@ -142,6 +142,28 @@ def test_experts_forward_small(gpu_device, dtype, dense):
     assert rel_err(out, ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("E,T,k", [(4, 1, 1), (2, 700, 2), (16, 37, 3), (3, 333, 3)])
+def test_experts_edge_shapes(gpu_device, E, T, k):
+    # one token; experts with more slots than one m-tile (700 x 2 over 2 experts);
+    # experts with no tokens; every expert selected (k == E)
+    _say(f"experts fwd+bwd edge E={E} T={T} k={k} bf16")
+    dt = torch.bfloat16
+    L = make_layer(gpu_device, E, 256, 128, T, k, dt, seed=13)
+    g = torch.Generator().manual_seed(31)
+    dout = torch.randn(T, 256, generator=g).to(dt)
+    dhs_r, dw_r, _, _ = M.experts_routed_autograd(L["hs"], L["w"], L["deq_g"], L["deq_d"], dout)
+    ref = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"])
+    hs = L["hs"].to(gpu_device).requires_grad_(True)
+    w = L["w"].to(gpu_device).requires_grad_(True)
+    out = G.routed_experts(hs, w, L["ew"])
+    out.backward(dout.to(gpu_device))
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) <= 1e-2
+    assert rel_err(hs.grad, dhs_r) <= 1e-2
+    routed = L["w"] != 0
+    assert rel_err(w.grad.cpu()[routed], dw_r[routed]) <= 1e-2
+
+
 def test_experts_forward_intermediates(gpu_device):
     # per-slot gate_up / SwiGLU / down outputs against the oracle's per-expert tensors
     _say("experts fwd intermediates E=8 H=256 I=128 bf16")
@@ -157,7 +179,7 @@ def test_experts_forward_intermediates(gpu_device):
     from usaf_amd import _native as N
     st = N.stream_ptr(gpu_device)
     q, s, z, w16 = ew._ptrs("gate_up", dt)
-    N.call("usaf_hip_moe_gate_up_fwd", L["hs"].to(gpu_device).data_ptr(), H, b.token_idx.data_ptr(),
+    N.call("usaf_hip_moe_gate_up_fwd", L["hs"].to(gpu_device).data_ptr(), L["hs"].shape[0], H, b.token_idx.data_ptr(),
            b.offsets.data_ptr(), S, ew.E, I, q, s, z, w16, N.BF16, gu.data_ptr(), act.data_ptr(), st)
     q, s, z, w16 = ew._ptrs("down", dt)
     N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, ew.E, H, q, s, z, w16, N.BF16,

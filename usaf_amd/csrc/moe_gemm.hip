@@ -25,18 +25,37 @@
 //   SWIGLU_BWD  acc = d(act); with the saved gu: d(up) = dtype(dact * silu(g)),
 //               d(gate) = dtype(dtype(dact * u) * silu'(g)) -> dgu[m, n], dgu[m, I+n]
 //
-// Block: 256 threads = 4 waves in a 2x2 grid, tile BM x BN x BK = 128 x 128 x 64,
-// each wave 64 x 64 (2 x 2 MFMA 32x32 tiles), two LDS stages.  The grid is
-// persistent: block b walks tiles b, b + gridDim.x, ... of the device-side
-// tile list (m-tiles of every expert x n-tiles), so no host sync is needed.
+// Block: 512 threads, one block per CU, warp-specialised: 4 multiply waves
+// (2 (M) x 2 (N) over the tile, LDS fragments -> MFMA only) and 4 producer
+// waves (global loads, 4-bit dequant, LDS stores), one of each per SIMD, so
+// the dequant and memory work overlaps the matrix cores instead of
+// serialising with them in one instruction stream.
+// Tile: up to BM = 320 slots of one expert x BN = 128 columns x BK = 64, so a
+// typical expert (~256 routed tokens of 4096 x top-8 over 128 experts) is one
+// m-tile and each dequantized weight tile feeds all of its tokens.  Each
+// multiply wave owns 5 x 2 MFMA 32x32 accumulators (160 registers).  Two LDS
+// stages (129 KB); the producers load two k-tiles ahead.
+// The grid is persistent: tiles (expert m-tile x n-tile) come from a
+// device-side list, walked per die so one expert's n-tiles share an L2; no
+// host sync is needed.
 #include "common.h"
+
+#include <type_traits>
 
 namespace usaf {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64;
+// Tile: up to BM slots of one expert (10 MFMA row blocks of 32; empty blocks
+// are skipped) x BN output columns x BK contraction per LDS stage.
+constexpr int BM = 320, BN = 128, BK = 64;
+constexpr int WM_SUB = BM / 32 / 2;    // 32-row blocks per M-wave (2 M-waves x 2 N-waves)
+constexpr int kThreads = 512;                // 4 multiply waves + 4 producer waves
+constexpr int A_CHUNKS = BM * BK / 8 / 256;  // 16-byte A chunks per producer thread per k-tile
 constexpr int LDSW = BK + 8;  // LDS row stride in 16-bit elements (16 B pad: conflict-free 128-bit reads)
+constexpr int LDSC = BN + 8; // epilogue tile row stride (16-bit elements)
 constexpr int MAX_E = 1024;
+constexpr int kXcds = 8;      // MI355X: 8 accelerator dies, blocks dispatched round-robin over them
+constexpr size_t kSmemBytes = (size_t)2 * (BM + BN) * LDSW * 2 + (MAX_E + 1 + kThreads) * 4;
 
 enum { BMODE_NK = 0, BMODE_KN = 1 };
 enum { BQ_Q4 = 0, BQ_DENSE16 = 1 };
@@ -107,6 +126,18 @@ __device__ __forceinline__ void dequant32(const u32x4 w, uint16_t sb, uint16_t z
 
 // ---- small helpers -------------------------------------------------------------
 
+// fp32 -> 16-bit bits of dtype DT (round to nearest even) and back.
+template <int DT>
+__device__ __forceinline__ uint16_t round_bits(float v) {
+  if constexpr (DT == USAF_F16) return f32_to_f16_bits(v);
+  else return f32_to_bf16_bits(v);
+}
+template <int DT>
+__device__ __forceinline__ float bits_to_f32(uint16_t b) {
+  if constexpr (DT == USAF_F16) return f16_bits_to_f32(b);
+  else return bf16_bits_to_f32(b);
+}
+
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
 template <int DT>
@@ -131,21 +162,281 @@ __device__ __forceinline__ int64_t nk_weight_row(int b, int64_t n0, int64_t inte
   }
 }
 
+// ---- producer waves: global -> registers -> LDS, 4-bit B dequantized on the way ----
+// Called by the 256 threads of waves 4-7 for one tile; executes exactly the
+// barriers the multiply waves do (one after the prologue, one per k-tile, one
+// after the accumulators are parked).
 template <int BMODE, int EPI, int BQ, int DT>
-__global__ __launch_bounds__(256, 2) void moe_gemm_kernel(const GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDSW];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDSW];
-  __shared__ int32_t s_mt[MAX_E + 1];   // m-tile prefix over experts
-  __shared__ int32_t s_part[256];
+__device__ __forceinline__ void produce_tile(const GemmArgs& g, uint16_t* sA0, uint16_t* sB0, const int ptid,
+                                             const int e, const int64_t m_beg, const int valid, const int64_t n0,
+                                             const int nk) {
+  const int64_t w_base = (int64_t)e * g.w_rows * g.w_cols;  // element offset of expert e
+  // A: chunks c = ptid + 256*i (i < A_CHUNKS) of 16 B: row c>>3, 8-element k block c&7.
+  // Rows past the expert's last slot re-read its first row into LDS rows that
+  // are never used: loads and stores stay unconditional, which keeps the
+  // producer loop one basic block and its memory waits precise.
+  int32_t a_off[A_CHUNKS];
+#pragma unroll
+  for (int i = 0; i < A_CHUNKS; ++i) {
+    const int c = ptid + 256 * i;
+    const int row = c >> 3;
+    const int64_t m = m_beg + (row < valid ? row : 0);
+    const int64_t arow = g.a_rows ? (int64_t)g.a_rows[m] : m;
+    a_off[i] = (int32_t)(arow * g.lda + (c & 7) * 8);
+  }
+  // B (4-bit NK): 16 code bytes (32 elements of one group) of tile row ptid>>1.
+  // B (4-bit KN): 4 contraction rows 4*(ptid&15)+r, 8 columns 8*(ptid>>4): one code word per row.
+  // B (dense NK): 4 chunks of 8 elements; (dense KN): 4 rows x 8 columns.
+  int64_t b_off[4] = {0, 0, 0, 0};
+  int64_t b_kstep;
+  if constexpr (BMODE == BMODE_NK) {
+    b_kstep = BK;
+    if constexpr (BQ == BQ_Q4) {
+      b_off[0] = w_base + nk_weight_row<EPI>(ptid >> 1, n0, g.inter) * g.w_cols + (ptid & 1) * 32;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = ptid + 256 * i;
+        b_off[i] = w_base + nk_weight_row<EPI>(c >> 3, n0, g.inter) * g.w_cols + (c & 7) * 8;
+      }
+    }
+  } else {
+    b_kstep = (int64_t)BK * g.w_cols;
+    const int kb = ptid & 15, nb = ptid >> 4;
+    b_off[0] = w_base + (int64_t)(4 * kb) * g.w_cols + n0 + nb * 8;  // row r adds r * w_cols
+  }
+
+  // Register ring: tile kt lives in slot kt % RING; with RING = 3 loads are
+  // issued two k-tiles before their LDS store, covering L2/HBM latency (the
+  // dense-weight and transposed-weight variants need more registers per tile
+  // and use RING = 2).
+  constexpr int RING = (BQ == BQ_Q4 && BMODE == BMODE_NK) ? 3 : 2;
+  u32x4 ra[RING][A_CHUNKS];
+  u32x4 rb4[RING][(BQ == BQ_Q4) ? 1 : 4];
+  uint32_t rw[RING][4];
+  uint32_t rsz[RING][4];  // scale | zero << 16 of each row's group
+  auto load_tile = [&](auto slot_c, int kt) {
+    constexpr int S = decltype(slot_c)::value;
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) ra[S][i] = *reinterpret_cast<const u32x4*>(g.A + a_off[i] + kt * BK);
+    const int64_t ks = (int64_t)kt * b_kstep;
+    if constexpr (BQ == BQ_Q4) {
+      if constexpr (BMODE == BMODE_NK) {
+        const int64_t el = b_off[0] + ks;
+        rb4[S][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g.wq + (el >> 1)));
+        rsz[S][0] = (uint32_t)g.ws[el >> 7] | ((uint32_t)g.wz[el >> 7] << 16);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t el = b_off[0] + r * g.w_cols + ks;
+          rw[S][r] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(g.wq + (el >> 1)));
+          rsz[S][r] = (uint32_t)g.ws[el >> 7] | ((uint32_t)g.wz[el >> 7] << 16);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t off = (BMODE == BMODE_NK) ? b_off[r] : b_off[0] + r * g.w_cols;
+        rb4[S][r] = *reinterpret_cast<const u32x4*>(g.w16 + off + ks);
+      }
+    }
+  };
+  auto store_tile = [&](auto slot_c, int st) {
+    constexpr int S = decltype(slot_c)::value;
+    uint16_t* sA = sA0 + st * (BM * LDSW);
+    uint16_t* sB = sB0 + st * (BN * LDSW);
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int c = ptid + 256 * i;
+      *reinterpret_cast<u32x4*>(&sA[(c >> 3) * LDSW + (c & 7) * 8]) = ra[S][i];
+    }
+    if constexpr (BMODE == BMODE_NK) {
+      if constexpr (BQ == BQ_Q4) {
+        uint32_t o[16];
+        dequant32<DT>(rb4[S][0], (uint16_t)(rsz[S][0] & 0xFFFFu), (uint16_t)(rsz[S][0] >> 16), o);
+        u32x4* dst = reinterpret_cast<u32x4*>(&sB[(ptid >> 1) * LDSW + (ptid & 1) * 32]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dst[j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = ptid + 256 * i;
+          *reinterpret_cast<u32x4*>(&sB[(c >> 3) * LDSW + (c & 7) * 8]) = rb4[S][i];
+        }
+      }
+    } else {
+      // rows r = 0..3 hold 8 consecutive columns each as 4 pairs (col 2p, 2p+1);
+      // write column-major: 4 consecutive contraction values per column (8 bytes)
+      uint32_t v[4][4];
+      if constexpr (BQ == BQ_Q4) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const f16 sv = __builtin_bit_cast(f16, (uint16_t)(rsz[S][r] & 0xFFFFu));
+          const f16 zv = __builtin_bit_cast(f16, (uint16_t)(rsz[S][r] >> 16));
+          const f16x2 s2 = {sv, sv}, z2 = {zv, zv};
+          dq_word(rw[S][r], s2, z2, v[r]);
+          if constexpr (DT == USAF_BF16) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) v[r][p] = h2_to_bf2(v[r][p]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[r][0] = rb4[S][r].x; v[r][1] = rb4[S][r].y; v[r][2] = rb4[S][r].z; v[r][3] = rb4[S][r].w;
+        }
+      }
+      const int kb = ptid & 15, nb = ptid >> 4;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        uint2 even, odd;
+        even.x = __builtin_amdgcn_perm(v[1][p], v[0][p], 0x05040100u);  // lo halves of rows 0,1
+        even.y = __builtin_amdgcn_perm(v[3][p], v[2][p], 0x05040100u);  // lo halves of rows 2,3
+        odd.x = __builtin_amdgcn_perm(v[1][p], v[0][p], 0x07060302u);   // hi halves of rows 0,1
+        odd.y = __builtin_amdgcn_perm(v[3][p], v[2][p], 0x07060302u);
+        *reinterpret_cast<uint2*>(&sB[(nb * 8 + 2 * p) * LDSW + 4 * kb]) = even;
+        *reinterpret_cast<uint2*>(&sB[(nb * 8 + 2 * p + 1) * LDSW + 4 * kb]) = odd;
+      }
+    }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+
+  // Steady-state loops are branch-free (every store and load of a step exists);
+  // the guarded tail finishes the remaining steps.  One barrier per step k
+  // (store tile k+1 into stage (k+1)&1, load tile k+RING into the slot tile k left).
+  if constexpr (RING == 3) {
+    load_tile(S0{}, 0);
+    if (nk > 1) load_tile(S1{}, 1);
+    if (nk > 2) load_tile(S2{}, 2);
+    store_tile(S0{}, 0);
+    __syncthreads();
+    int k = 0;
+    for (; k + 5 < nk; k += 3) {
+      store_tile(S1{}, (k + 1) & 1); load_tile(S0{}, k + 3); __syncthreads();
+      store_tile(S2{}, (k + 2) & 1); load_tile(S1{}, k + 4); __syncthreads();
+      store_tile(S0{}, (k + 3) & 1); load_tile(S2{}, k + 5); __syncthreads();
+    }
+    auto step = [&](auto store_c, auto load_c, int kk) {
+      if (kk + 1 < nk) store_tile(store_c, (kk + 1) & 1);
+      if (kk + 3 < nk) load_tile(load_c, kk + 3);
+      __syncthreads();
+    };
+    for (; k < nk; k += 3) {
+      step(S1{}, S0{}, k);
+      if (k + 1 < nk) step(S2{}, S1{}, k + 1);
+      if (k + 2 < nk) step(S0{}, S2{}, k + 2);
+    }
+  } else {
+    load_tile(S0{}, 0);
+    if (nk > 1) load_tile(S1{}, 1);
+    store_tile(S0{}, 0);
+    __syncthreads();
+    int k = 0;
+    for (; k + 3 < nk; k += 2) {
+      store_tile(S1{}, (k + 1) & 1); load_tile(S0{}, k + 2); __syncthreads();
+      store_tile(S0{}, (k + 2) & 1); load_tile(S1{}, k + 3); __syncthreads();
+    }
+    auto step = [&](auto store_c, auto load_c, int kk) {
+      if (kk + 1 < nk) store_tile(store_c, (kk + 1) & 1);
+      if (kk + 2 < nk) load_tile(load_c, kk + 2);
+      __syncthreads();
+    };
+    for (; k < nk; k += 2) {
+      step(S1{}, S0{}, k);
+      if (k + 1 < nk) step(S0{}, S1{}, k + 1);
+    }
+  }
+  __syncthreads();  // the multiply waves park their accumulators
+}
+
+// ---- multiply waves: LDS fragments -> MFMA, accumulators parked in LDS ----
+// Waves 0-3 as 2 (M) x 2 (N); each owns WM_SUB x 2 MFMA 32x32 accumulators.
+// A fragments are re-read one k16 step ahead and B fragments double-buffered
+// so LDS latency hides behind the MFMAs.  Row blocks past the expert's last
+// slot multiply stale rows whose results are never stored.
+template <int DT>
+__device__ __forceinline__ void consume_tile(const uint16_t* sA0, const uint16_t* sB0, const int lane, const int wm,
+                                             const int wn, const int nk, const int nrb, uint16_t* sC) {
+  f32x16 acc[WM_SUB][2];
+#pragma unroll
+  for (int i = 0; i < WM_SUB; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  auto frag_a = [&](int st, int i, int kk) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(
+        &sA0[st * (BM * LDSW) + ((wm * WM_SUB + i) * 32 + (lane & 31)) * LDSW + kk * 16 + (lane >> 5) * 8]);
+  };
+  auto frag_b = [&](int st, int j, int kk) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(
+        &sB0[st * (BN * LDSW) + (wn * 64 + j * 32 + (lane & 31)) * LDSW + kk * 16 + (lane >> 5) * 8]);
+  };
+  __syncthreads();  // stage 0 filled
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    u32x4 fa[WM_SUB], fb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[j] = frag_b(cur, j, 0);
+#pragma unroll
+    for (int i = 0; i < WM_SUB; ++i) fa[i] = frag_a(cur, i, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      u32x4 fbn[2];
+      if (kk + 1 < BK / 16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fbn[j] = frag_b(cur, j, kk + 1);
+      }
+#pragma unroll
+      for (int i = 0; i < WM_SUB; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<DT>(fa[i], fb[j], acc[i][j]);
+        if (kk + 1 < BK / 16) fa[i] = frag_a(cur, i, kk + 1);
+      }
+      if (kk + 1 < BK / 16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fb[j] = fbn[j];
+      }
+    }
+    __syncthreads();
+  }
+  // park dtype(acc) as the [BM][BN] tile; acc[i][j][r] is tile row
+  // 32*(wm*WM_SUB+i) + 8*(r/4) + 4*(lane/32) + r%4, column wn*64 + j*32 + lane%32
+  if (wm * WM_SUB < nrb) {
+#pragma unroll
+    for (int i = 0; i < WM_SUB; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * (wm * WM_SUB + i) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int col = wn * 64 + j * 32 + (lane & 31);
+          sC[row * LDSC + col] = round_bits<DT>(acc[i][j][r]);
+        }
+  }
+  __syncthreads();
+}
+
+template <int BMODE, int EPI, int BQ, int DT>
+__global__ __launch_bounds__(kThreads) void moe_gemm_kernel(const GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* const sA0 = smem;                      // [2][BM * LDSW]
+  uint16_t* const sB0 = smem + 2 * BM * LDSW;      // [2][BN * LDSW]
+  int32_t* const s_mt = reinterpret_cast<int32_t*>(smem + 2 * (BM + BN) * LDSW);  // [MAX_E + 1]
+  int32_t* const s_part = s_mt + MAX_E + 1;                                        // [kThreads]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  // Waves 0-3 multiply (2 x 2 over the tile), waves 4-7 feed the LDS stages.
+  // Waves are placed round-robin on the 4 SIMDs, so every SIMD runs one of each.
+  const bool producer = wave >= 4;
+  const int ptid = tid - 256;  // producer thread index 0..255
+  const int wm = (wave & 3) >> 1, wn = wave & 1;
   const int E = g.E;
 
-  // m-tile prefix: each thread owns a run of experts, then a block scan of the runs
+  // m-tile prefix over experts: each thread owns a run of experts, then a block scan
   {
-    const int per = (E + 255) / 256;
+    const int per = (E + kThreads - 1) / kThreads;
     const int e0 = tid * per;
     int local = 0;
     for (int i = 0; i < per; ++i) {
@@ -154,7 +445,7 @@ __global__ __launch_bounds__(256, 2) void moe_gemm_kernel(const GemmArgs g) {
     }
     s_part[tid] = local;
     __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
+    for (int off = 1; off < kThreads; off <<= 1) {
       const int v = (tid >= off) ? s_part[tid - off] : 0;
       __syncthreads();
       s_part[tid] += v;
@@ -168,19 +459,29 @@ __global__ __launch_bounds__(256, 2) void moe_gemm_kernel(const GemmArgs g) {
         run += (g.offsets[e + 1] - g.offsets[e] + BM - 1) / BM;
       }
     }
-    if (tid == 255) s_mt[E] = s_part[255];
+    if (tid == kThreads - 1) s_mt[E] = s_part[kThreads - 1];
     __syncthreads();
   }
   const int64_t n_mt = s_mt[E];
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? g.N / 64 : g.N / BN;
   const int64_t n_tiles = n_mt * n_nt;
   const int nk = (int)(g.K / BK);
-  const int64_t groups_per_row = g.w_cols / 128;
 
-  for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+  // XCD-aware walk: blocks are dispatched round-robin over kXcds dies, so
+  // block b runs on die b % kXcds.  Each die takes one contiguous slice of the
+  // (expert, m-tile, n-tile) list, so the n-tiles of an expert -- which share
+  // the expert's activation rows -- run on one die and share its L2.
+  // With fewer blocks than dies, every block is its own slice.
+  const int64_t nblk = gridDim.x;
+  const int dies = nblk < kXcds ? (int)nblk : kXcds;
+  const int xcd = (int)(blockIdx.x % dies);
+  const int64_t per_xcd = (nblk + dies - 1 - xcd) / dies;  // blocks on this die (>= 1)
+  const int64_t local_b = blockIdx.x / dies;
+  const int64_t t_beg = n_tiles * xcd / dies, t_end = n_tiles * (xcd + 1) / dies;
+
+  for (int64_t tile = t_beg + local_b; tile < t_end; tile += per_xcd) {
     const int64_t mt = tile / n_nt, nt = tile % n_nt;
-    // expert of m-tile mt: largest e with s_mt[e] <= mt
-    int lo = 0, hi = E - 1;
+    int lo = 0, hi = E - 1;  // expert of m-tile mt: largest e with s_mt[e] <= mt
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (s_mt[mid] <= mt) lo = mid; else hi = mid - 1;
@@ -188,204 +489,120 @@ __global__ __launch_bounds__(256, 2) void moe_gemm_kernel(const GemmArgs g) {
     const int e = lo;
     const int64_t m_beg = g.offsets[e] + (mt - s_mt[e]) * BM;
     const int64_t m_end = g.offsets[e + 1];
+    const int valid = (int)((m_end - m_beg < BM) ? (m_end - m_beg) : BM);
+    const int nrb = (valid + 31) >> 5;  // 32-row blocks holding slots
     const int64_t n0 = (EPI == EPI_SWIGLU_FWD) ? nt * 64 : nt * BN;
-    const int64_t w_base = (int64_t)e * g.w_rows * g.w_cols;  // element offset of expert e
 
-    // ---- per-thread global load coordinates ----
-    // A: chunks c = tid + 256*i (i < 4) of 16 B: row c>>3, 8-element column block c&7
-    const uint16_t* a_src[4];
-    bool a_ok[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int64_t m = m_beg + (c >> 3);
-      a_ok[i] = m < m_end;
-      const int64_t row = a_ok[i] ? (g.a_rows ? (int64_t)g.a_rows[m] : m) : 0;
-      a_src[i] = g.A + row * g.lda + (c & 7) * 8;
-    }
-    // B (4-bit): one 16-byte code load per thread per k-tile, 32 codes of one group.
-    // B (dense 16-bit): four 16-byte loads per thread per k-tile.
-    int64_t b_elem = 0;   // element offset (within the whole tensor) of the thread's first B element at k0 = 0
-    int64_t b_kstep = 0;  // element offset advance per k-tile
-    if constexpr (BQ == BQ_Q4) {
-      if constexpr (BMODE == BMODE_NK) {
-        const int b = tid >> 1, half = tid & 1;
-        const int64_t r = nk_weight_row<EPI>(b, n0, g.inter);
-        b_elem = w_base + r * g.w_cols + half * 32;
-        b_kstep = BK;
-      } else {
-        b_elem = w_base + (int64_t)lane * g.w_cols + n0 + wave * 32;
-        b_kstep = (int64_t)BK * g.w_cols;
-      }
-    }
-    const uint16_t* d_src[4];
-    if constexpr (BQ == BQ_DENSE16) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = tid + 256 * i;
-        if constexpr (BMODE == BMODE_NK) {  // tile row c>>3 (weight row), 8-element k block c&7
-          const int64_t r = nk_weight_row<EPI>(c >> 3, n0, g.inter);
-          d_src[i] = g.w16 + w_base + r * g.w_cols + (c & 7) * 8;
-        } else {  // contraction row c>>4, 8-element n block c&15
-          d_src[i] = g.w16 + w_base + (int64_t)(c >> 4) * g.w_cols + n0 + (c & 15) * 8;
-        }
-      }
-      b_kstep = (BMODE == BMODE_NK) ? (int64_t)BK : (int64_t)BK * g.w_cols;
+    if (producer) {
+      produce_tile<BMODE, EPI, BQ, DT>(g, sA0, sB0, ptid, e, m_beg, valid, n0, nk);
+    } else {
+      consume_tile<DT>(sA0, sB0, lane, wm, wn, nk, nrb, sA0);
     }
 
-    u32x4 ra[4];
-    u32x4 rb;
-    u32x4 rd[4];
-    uint16_t rs = 0, rz = 0;
-    auto load_tile = [&](int kt) {
+    // ---- epilogue: all waves walk the valid rows in 8-column chunks of the
+    //      [BM][BN] dtype tile the multiply waves parked in LDS (sA0) ----
+    const uint16_t* sC = sA0;
+    constexpr int CPR = (EPI == EPI_SWIGLU_FWD) ? 8 : 16;  // 8-column chunks per row
+    for (int c = tid; c < valid * CPR; c += kThreads) {
+      const int row = c / CPR, ch = c % CPR;
+      const int64_t m = m_beg + row;
+      if constexpr (EPI == EPI_STORE) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&sC[row * LDSC + ch * 8]);
+        *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n0 + ch * 8) = v;
+      } else if constexpr (EPI == EPI_SWIGLU_FWD) {
+        // output columns o..o+7 (o = 8*ch): gate at tile column (o/32)*64 + o%32, up 32 further
+        const int o = ch * 8;
+        const int cg = (o >> 5) * 64 + (o & 31);
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(&sC[row * LDSC + cg]);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(&sC[row * LDSC + cg + 32]);
+        const int64_t n = n0 + o;
+        *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + n) = gv;
+        *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + g.inter + n) = uv;
+        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+        uint32_t aw[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (a_ok[i]) ra[i] = *reinterpret_cast<const u32x4*>(a_src[i] + (int64_t)kt * BK);
-        else ra[i] = u32x4{0, 0, 0, 0};
-      }
-      if constexpr (BQ == BQ_Q4) {
-        const int64_t el = b_elem + (int64_t)kt * b_kstep;
-        rb = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g.wq + (el >> 1)));
-        const int64_t grp = el >> 7;  // groups are 128 consecutive elements of the flat tensor
-        rs = g.ws[grp];
-        rz = g.wz[grp];
-      } else {
+        for (int q = 0; q < 4; ++q) {
+          uint32_t h2 = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rd[i] = *reinterpret_cast<const u32x4*>(d_src[i] + (int64_t)kt * b_kstep);
-      }
-    };
-    auto store_tile = [&](int st) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = tid + 256 * i;
-        *reinterpret_cast<u32x4*>(&sA[st][(c >> 3) * LDSW + (c & 7) * 8]) = ra[i];
-      }
-      if constexpr (BQ == BQ_Q4) {
-        uint32_t o[16];
-        dequant32<DT>(rb, rs, rz, o);
-        if constexpr (BMODE == BMODE_NK) {
-          const int b = tid >> 1, half = tid & 1;
-          u32x4* dst = reinterpret_cast<u32x4*>(&sB[st][b * LDSW + half * 32]);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) dst[j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
-        } else {
-          // transpose: code j of this thread is column wave*32 + j, contraction index lane
-          uint16_t* dst = &sB[st][(wave * 32) * LDSW + lane];
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            dst[(2 * j) * LDSW] = (uint16_t)(o[j] & 0xFFFFu);
-            dst[(2 * j + 1) * LDSW] = (uint16_t)(o[j] >> 16);
+          for (int h = 0; h < 2; ++h) {
+            const float gt = bits_to_f32<DT>((uint16_t)(gw[q] >> (16 * h)));
+            const float up = bits_to_f32<DT>((uint16_t)(uw[q] >> (16 * h)));
+            const float sg = round_to<DT>(silu_f(gt));
+            h2 |= (uint32_t)round_bits<DT>(sg * up) << (16 * h);
           }
+          aw[q] = h2;
         }
-      } else {
+        *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n) = u32x4{aw[0], aw[1], aw[2], aw[3]};
+      } else {  // EPI_SWIGLU_BWD
+        const int64_t n = n0 + ch * 8;
+        const u32x4 dv = *reinterpret_cast<const u32x4*>(&sC[row * LDSC + ch * 8]);
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(g.aux + m * g.ld_aux + n);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(g.aux + m * g.ld_aux + g.inter + n);
+        const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w},
+                       uw[4] = {uv.x, uv.y, uv.z, uv.w};
+        uint32_t dg_w[4], du_w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int c = tid + 256 * i;
-          if constexpr (BMODE == BMODE_NK) {
-            *reinterpret_cast<u32x4*>(&sB[st][(c >> 3) * LDSW + (c & 7) * 8]) = rd[i];
-          } else {
-            uint16_t* dst = &sB[st][((c & 15) * 8) * LDSW + (c >> 4)];
-            const uint32_t w4[4] = {rd[i].x, rd[i].y, rd[i].z, rd[i].w};
+        for (int q = 0; q < 4; ++q) {
+          uint32_t a = 0, b = 0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              dst[(2 * j) * LDSW] = (uint16_t)(w4[j] & 0xFFFFu);
-              dst[(2 * j + 1) * LDSW] = (uint16_t)(w4[j] >> 16);
-            }
-          }
-        }
-      }
-    };
-
-    f32x16 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) load_tile(kt + 1);
-#pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        u32x4 fa[2], fb[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          fa[i] = *reinterpret_cast<const u32x4*>(
-              &sA[cur][(wm * 64 + i * 32 + (lane & 31)) * LDSW + kk * 16 + (lane >> 5) * 8]);
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          fb[j] = *reinterpret_cast<const u32x4*>(
-              &sB[cur][(wn * 64 + j * 32 + (lane & 31)) * LDSW + kk * 16 + (lane >> 5) * 8]);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = mfma32<DT>(fa[i], fb[j], acc[i][j]);
-      }
-      if (kt + 1 < nk) store_tile(cur ^ 1);
-      __syncthreads();
-    }
-
-    // ---- epilogue: acc[i][j][r] is row wm*64 + i*32 + 8*(r/4) + 4*(lane/32) + r%4,
-    //      column wn*64 + j*32 + lane%32 of the tile ----
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m_beg + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m >= m_end) continue;
-        if constexpr (EPI == EPI_STORE) {
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
-            store_from_f32<DT>(g.out, m * g.ldo + n, acc[i][j][r]);
-          }
-        } else if constexpr (EPI == EPI_SWIGLU_FWD) {
-          const int64_t n = n0 + wn * 32 + (lane & 31);
-          const float gt = round_to<DT>(acc[i][0][r]);
-          const float up = round_to<DT>(acc[i][1][r]);
-          store_from_f32<DT>(g.out2, m * g.ldo2 + n, gt);
-          store_from_f32<DT>(g.out2, m * g.ldo2 + g.inter + n, up);
-          const float sg = round_to<DT>(silu_f(gt));
-          store_from_f32<DT>(g.out, m * g.ldo + n, sg * up);
-        } else {  // EPI_SWIGLU_BWD
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
-            const float da = round_to<DT>(acc[i][j][r]);
-            const float gt = load_as_f32<DT>(g.aux, m * g.ld_aux + n);
-            const float up = load_as_f32<DT>(g.aux, m * g.ld_aux + g.inter + n);
+          for (int h = 0; h < 2; ++h) {
+            const float da = bits_to_f32<DT>((uint16_t)(dw[q] >> (16 * h)));
+            const float gt = bits_to_f32<DT>((uint16_t)(gw[q] >> (16 * h)));
+            const float up = bits_to_f32<DT>((uint16_t)(uw[q] >> (16 * h)));
             const float sig = 1.0f / (1.0f + expf(-gt));
             const float sg = round_to<DT>(gt * sig);
-            const float du = da * sg;
             const float dsil = round_to<DT>(da * up);
-            const float dg = dsil * (sig * (1.0f + gt * (1.0f - sig)));
-            store_from_f32<DT>(g.out, m * g.ldo + n, dg);
-            store_from_f32<DT>(g.out, m * g.ldo + g.inter + n, du);
+            const float dg = (dsil * sig) * (1.0f + gt * (1.0f - sig));
+            a |= (uint32_t)round_bits<DT>(dg) << (16 * h);
+            b |= (uint32_t)round_bits<DT>(da * sg) << (16 * h);
           }
+          dg_w[q] = a;
+          du_w[q] = b;
         }
+        *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n) = u32x4{dg_w[0], dg_w[1], dg_w[2], dg_w[3]};
+        *reinterpret_cast<u32x4*>(g.out + m * g.ldo + g.inter + n) = u32x4{du_w[0], du_w[1], du_w[2], du_w[3]};
       }
     }
+    __syncthreads();  // sC aliases the stage buffers the next tile fills
   }
 }
 
+template <int BMODE, int EPI, int BQ, int DT>
+int launch_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  static bool attr_set = false;  // per instantiation; the attribute is a property of the function
+  if (!attr_set) {
+    // Raise the dynamic-LDS limit for this kernel.  A runtime that does not need
+    // (or know) the attribute may refuse it; the launch below reports any real problem.
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_kernel<BMODE, EPI, BQ, DT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSmemBytes);
+    (void)hipGetLastError();
+    attr_set = true;
+  }
+  moe_gemm_kernel<BMODE, EPI, BQ, DT><<<blocks, kThreads, kSmemBytes, st>>>(g);
+  return USAF_OK;
+}
+
 template <int BMODE, int EPI>
-int launch_gemm(const GemmArgs& g, int dt, int64_t max_tiles, hipStream_t st, const char* what) {
-  int64_t blocks = (int64_t)device_cu_count() * 2;
+int launch_gemm(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_total, hipStream_t st,
+                const char* what) {
+  // activation offsets are 32-bit inside the kernel
+  if (a_rows_total * g.lda >= ((int64_t)1 << 31))
+    return set_error(USAF_ERR_UNSUPPORTED, "%s: activation operand of %lld x %lld elements exceeds 2^31", what,
+                     (long long)a_rows_total, (long long)g.lda);
+  int64_t blocks = (int64_t)device_cu_count();
   if (blocks > max_tiles) blocks = max_tiles;
   if (blocks < 1) blocks = 1;
   const bool dense = g.w16 != nullptr;
-  if (dt == USAF_BF16) {
-    if (dense) moe_gemm_kernel<BMODE, EPI, BQ_DENSE16, USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>(g);
-    else moe_gemm_kernel<BMODE, EPI, BQ_Q4, USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>(g);
-  } else if (dt == USAF_F16) {
-    if (dense) moe_gemm_kernel<BMODE, EPI, BQ_DENSE16, USAF_F16><<<(unsigned)blocks, 256, 0, st>>>(g);
-    else moe_gemm_kernel<BMODE, EPI, BQ_Q4, USAF_F16><<<(unsigned)blocks, 256, 0, st>>>(g);
-  } else {
+  int rc;
+  if (dt == USAF_BF16)
+    rc = dense ? launch_one<BMODE, EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
+               : launch_one<BMODE, EPI, BQ_Q4, USAF_BF16>(g, (unsigned)blocks, st);
+  else if (dt == USAF_F16)
+    rc = dense ? launch_one<BMODE, EPI, BQ_DENSE16, USAF_F16>(g, (unsigned)blocks, st)
+               : launch_one<BMODE, EPI, BQ_Q4, USAF_F16>(g, (unsigned)blocks, st);
+  else
     return set_error(USAF_ERR_INVALID, "%s: dtype must be fp16 or bf16", what);
-  }
+  if (rc) return rc;
   return check_launch(what);
 }
 
@@ -406,7 +623,7 @@ int check_common(const char* what, int64_t S, int64_t E, const void* offsets, co
 using namespace usaf;
 
 // Forward gate_up + SwiGLU (qwen3moe_dml.py:58-60, per routed slot).
-extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t H, const int32_t* token_idx, const int32_t* offsets,
+extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T_rows, int64_t H, const int32_t* token_idx, const int32_t* offsets,
                                         int64_t S, int64_t E, int64_t I, const int8_t* wq, const uint16_t* ws,
                                         const uint16_t* wz, const void* w16, int32_t dtype, void* gu, void* act, void* stream) {
   if (int rc = check_common("moe_gate_up_fwd", S, E, offsets, wq, ws, wz, w16)) return rc;
@@ -421,7 +638,7 @@ extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t H, const int32_t*
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)act; g.ldo = I; g.out2 = (uint16_t*)gu; g.ldo2 = 2 * I;
   const int64_t max_tiles = (S / BM + E) * (I / 64);
-  return launch_gemm<BMODE_NK, EPI_SWIGLU_FWD>(g, dtype, max_tiles, as_stream(stream), "moe_gate_up_fwd");
+  return launch_gemm<BMODE_NK, EPI_SWIGLU_FWD>(g, dtype, max_tiles, T_rows, as_stream(stream), "moe_gate_up_fwd");
 }
 
 // Forward down projection (qwen3moe_dml.py:61): y[m] = act[m] @ W_down[e]^T.
@@ -440,7 +657,7 @@ extern "C" int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* 
   g.N = H; g.K = I; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)y; g.ldo = H;
   const int64_t max_tiles = (S / BM + E) * (H / BN);
-  return launch_gemm<BMODE_NK, EPI_STORE>(g, dtype, max_tiles, as_stream(stream), "moe_down_fwd");
+  return launch_gemm<BMODE_NK, EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_fwd");
 }
 
 // Backward through the down projection and SwiGLU: dgu[m] from dcur[m] @ W_down[e].
@@ -459,7 +676,7 @@ extern "C" int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)dgu; g.ldo = 2 * I; g.aux = (const uint16_t*)gu; g.ld_aux = 2 * I;
   const int64_t max_tiles = (S / BM + E) * (I / BN);
-  return launch_gemm<BMODE_KN, EPI_SWIGLU_BWD>(g, dtype, max_tiles, as_stream(stream), "moe_down_bwd");
+  return launch_gemm<BMODE_KN, EPI_SWIGLU_BWD>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_bwd");
 }
 
 // Backward grad-input through gate_up: dx_slots[m] = dgu[m] @ W_gate_up[e].
@@ -478,5 +695,5 @@ extern "C" int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_
   g.N = H; g.K = 2 * I; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)dx_slots; g.ldo = H;
   const int64_t max_tiles = (S / BM + E) * (H / BN);
-  return launch_gemm<BMODE_KN, EPI_STORE>(g, dtype, max_tiles, as_stream(stream), "moe_gate_up_bwd");
+  return launch_gemm<BMODE_KN, EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_gate_up_bwd");
 }

@@ -245,7 +245,7 @@ class RoutedExpertsFn(torch.autograd.Function):
         y = torch.empty(S, H, dtype=dt, device=dev)
         if S > 0:
             q, s, z, w16 = ew._ptrs("gate_up", dt)
-            _gemm_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
+            _gemm_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
                        S, E, I, q, s, z, w16, code, gu.data_ptr(), act.data_ptr(), st)
             q, s, z, w16 = ew._ptrs("down", dt)
             _gemm_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, s, z, w16,
