@@ -176,7 +176,10 @@ int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_t* offsets,
 
 /* ---- sparse gradient path and optimizer ----------------------------------- */
 
-/* out[c, s] = in[rows ? rows[s] : s, c] for 16-bit [.., C] -> [C, S] (slot-major operands). */
+/* out[c, s] = in[rows ? rows[s] : s, c] for 16-bit [.., C] -> [C, S] (slot-major operands).
+ * When C, ld_in and ld_out are multiples of 8 and both bases 16-byte aligned, the
+ * transposed rows are written as 16-byte vectors and out[c, S .. round_up(S, 8)) is
+ * zero-filled. */
 int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const int32_t* rows, int64_t S, int64_t C, void* out,
                               int64_t ld_out, void* stream);
 
@@ -185,14 +188,15 @@ int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const int32_t* rows
  * per-expert F.linear weight grad + SparseGradStore.add gather
  * (usaf/qwen3moe_dml.py:44-56, usaf/moe_loader.py:564-578):
  *   compact[pos(p)] += fp32(dtype( sum_{s in expert e} rowT[o, s] * colT[i, s] ))
- * for each active position p = (e, o, i) of a [E, R, C] weight, given as CSR over
- * the E*R rows (row_ptr [E*R+1] int64, col_idx [nnz] int32) and pos_map [nnz]
- * (compact index of CSR entry p; NULL = identity).  rowT, colT are slot-major
- * [*, ldT] 16-bit operands (dtype).
+ * for each active position p < n_pos of a [E, R, C] weight, given as
+ * row_idx[p] = e * R + o and col_idx[p] = i (int32; out-of-range entries are
+ * skipped) and pos_map[p] (int64 compact index of entry p; NULL = identity; each
+ * compact index at most once).  rowT [R, ldT] and colT [C, ldT] are slot-major
+ * 16-bit operands (dtype), 16-byte aligned, ldT a multiple of 8 and >= offsets[E].
  */
 int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t ldT, const int32_t* offsets, int64_t E,
-                          int64_t R, const int64_t* row_ptr, const int32_t* col_idx, const int64_t* pos_map,
-                          int32_t dtype, float* compact, void* stream);
+                          int64_t R, int64_t C, int64_t n_pos, const int32_t* row_idx, const int32_t* col_idx,
+                          const int64_t* pos_map, int32_t dtype, float* compact, void* stream);
 
 /*
  * One SparseAdam step on compact fp32 vectors (usaf/sparse_optim.py:94-130,

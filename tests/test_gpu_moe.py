@@ -353,3 +353,56 @@ def test_scale_check(gpu_device):
     N.call("usaf_hip_scale_check", x.data_ptr(), out.data_ptr(), x.numel(), 4096.0, flag.data_ptr(),
            N.stream_ptr(gpu_device))
     assert int(flag.item()) == 0
+
+
+# ---- slot-major operands and the sampled gradient ------------------------------------
+
+@pytest.mark.parametrize("C,S,gathered", [(64, 333, True), (2048, 4096, False), (36, 77, True), (8, 1, False)])
+def test_gather_transpose_bit_exact(gpu_device, C, S, gathered):
+    _say(f"gather_transpose C={C} S={S} gathered={gathered}")
+    g = torch.Generator().manual_seed(C + S)
+    T = S + 5 if gathered else S
+    x = torch.randn(T, C, generator=g).bfloat16()
+    rows = torch.randint(0, T, (S,), generator=g, dtype=torch.int32) if gathered else None
+    out = G.slot_major(x.to(gpu_device), None if rows is None else rows.to(gpu_device))
+    torch.cuda.synchronize()
+    ref = (x[rows.long()] if gathered else x[:S]).t()
+    assert out.shape == (C, S) and out.stride(0) % 8 == 0
+    assert torch.equal(out.cpu().view(torch.int16), ref.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sddmm_ragged_experts(gpu_device, dtype):
+    _say(f"sddmm ragged experts {dtype}")
+    g = torch.Generator().manual_seed(11)
+    counts = [0, 3, 700, 129, 8, 1, 256]
+    E, R, C = len(counts), 40, 48
+    offs = [0]
+    for c in counts:
+        offs.append(offs[-1] + c)
+    S = offs[-1]
+    dy = torch.randn(S, R, generator=g).to(dtype)
+    x = torch.randn(S, C, generator=g).to(dtype)
+    numel = E * R * C
+    act = torch.randperm(numel, generator=g)[: numel // 5]                 # unsorted: pos_map path
+    store = SparseGradStore({"L.w": act}, {"L.w": (E, R, C)}, device=gpu_device)
+    init = torch.randn(act.numel(), generator=g)
+    store.compact["L.w"].copy_(init)
+    rowT = G.slot_major(dy.to(gpu_device))
+    colT = G.slot_major(x.to(gpu_device))
+    # poison the row padding: the kernel must select it out, never multiply it in
+    rowT.as_strided((R, rowT.stride(0) - S), (rowT.stride(0), 1), S).fill_(float("nan"))
+    offsets = torch.tensor(offs, dtype=torch.int32, device=gpu_device)
+    store.add_sampled("L.w", rowT, colT, offsets, dtype)
+    torch.cuda.synchronize()
+    dw = torch.zeros(E, R, C, dtype=torch.float64)
+    for e in range(E):
+        s0, s1 = offs[e], offs[e + 1]
+        dw[e] = dy[s0:s1].double().t() @ x[s0:s1].double()
+    ref = init.double() + dw.reshape(-1)[act].to(dtype).double()
+    got = store.compact["L.w"].cpu().double()
+    assert torch.isfinite(got).all()
+    assert rel_err(got - init.double(), ref - init.double()) <= TOL[dtype]
+    # experts without slots contribute exact zeros
+    e0 = (act // (R * C)) == 0
+    assert torch.equal(got[e0], init.double()[e0])

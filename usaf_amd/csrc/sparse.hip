@@ -11,64 +11,123 @@ namespace usaf {
 namespace {
 
 // out[c, s] = in[rows ? rows[s] : s, c] for c < C, s < S; 16-bit elements.
-// 64 x 64 tiles through LDS so that both the row reads and the column writes
-// are contiguous 128-byte segments.
+// A 64 (s) x 64 (c) tile goes through LDS stored column-major, so that the row
+// reads and the column writes are both 16-byte vectors over contiguous runs.
+// VEC: C, ld_in and ld_out are multiples of 8 and both bases 16-byte aligned;
+// the writes then also cover out[c, S .. round_up(S, 8)) with zeros.
+template <bool VEC>
 __global__ __launch_bounds__(256) void gather_transpose_kernel(const uint16_t* __restrict__ in, int64_t ld_in,
                                                                const int32_t* __restrict__ rows, int64_t S, int64_t C,
                                                                uint16_t* __restrict__ out, int64_t ld_out) {
-  __shared__ uint16_t tile[64][65];
+  constexpr int LDT = 72;  // 64 slots + 8: rows stay 16-byte aligned
+  __shared__ __align__(16) uint16_t tile[64 * LDT];
   const int64_t s0 = (int64_t)blockIdx.x * 64;
   const int64_t c0 = (int64_t)blockIdx.y * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t s = s0 + r, c = c0 + tx;
-    uint16_t v = 0;
-    if (s < S && c < C) {
-      const int64_t row = rows ? (int64_t)rows[s] : s;
-      v = in[row * ld_in + c];
+  if constexpr (VEC) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int v = threadIdx.x + 256 * it;
+      const int sl = v >> 3, cg = v & 7;
+      const int64_t s = s0 + sl, c = c0 + 8 * cg;
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (s < S && c < C) {
+        const int64_t row = rows ? (int64_t)rows[s] : s;
+        w = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
+      }
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tile[(8 * cg + 2 * j) * LDT + sl] = (uint16_t)(ww[j] & 0xffffu);
+        tile[(8 * cg + 2 * j + 1) * LDT + sl] = (uint16_t)(ww[j] >> 16);
+      }
     }
-    tile[r][tx] = v;
-  }
-  __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t c = c0 + r, s = s0 + tx;
-    if (c < C && s < S) out[c * ld_out + s] = tile[tx][r];
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int v = threadIdx.x + 256 * it;
+      const int cl = v >> 3, sg = v & 7;
+      const int64_t c = c0 + cl, s = s0 + 8 * sg;
+      if (c < C && s < S)
+        *reinterpret_cast<uint4*>(out + c * ld_out + s) = *reinterpret_cast<const uint4*>(&tile[cl * LDT + 8 * sg]);
+    }
+  } else {
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+    for (int r = ty; r < 64; r += 4) {
+      const int64_t s = s0 + r, c = c0 + tx;
+      uint16_t v = 0;
+      if (s < S && c < C) {
+        const int64_t row = rows ? (int64_t)rows[s] : s;
+        v = in[row * ld_in + c];
+      }
+      tile[tx * LDT + r] = v;
+    }
+    __syncthreads();
+    for (int r = ty; r < 64; r += 4) {
+      const int64_t c = c0 + r, s = s0 + tx;
+      if (c < C && s < S) out[c * ld_out + s] = tile[r * LDT + tx];
+    }
   }
 }
 
-// One wavefront per weight row r = e * R + o of the [E, R, Cw] weight.  For
-// each active position (o, i) of the row (CSR: row_ptr, col_idx; compact
-// index pos_map[p] or p), dot over the expert's slots s of
-//   rowT[o, s] * colT[i, s]
-// rounded to the gradient's dtype (the reference's dense grad is a 16-bit
-// tensor), added to compact[pos] in fp32 (index_add_).
+template <int DT>
+__device__ __forceinline__ float lo_f32(uint32_t w) {
+  if constexpr (DT == USAF_BF16) return __uint_as_float(w << 16);
+  else return f16_bits_to_f32((uint16_t)(w & 0xffffu));
+}
+template <int DT>
+__device__ __forceinline__ float hi_f32(uint32_t w) {
+  if constexpr (DT == USAF_BF16) return __uint_as_float(w & 0xffff0000u);
+  else return f16_bits_to_f32((uint16_t)(w >> 16));
+}
+
+// Sixteen lanes per active position p = (row r = e * R + o, column i):
+//   compact[pos(p)] += fp32(DT( sum_{s0 <= s < s1} rowT[o, s] * colT[i, s] ))
+// over expert e's slots [s0, s1) = [offsets[e], offsets[e + 1]).  Lane l of a
+// group reads slots [b + 8l, b + 8l + 8) of each 128-slot window starting at
+// b = s0 rounded down to 8, as one 16-byte load per operand; slots outside
+// [s0, s1) belong to neighbouring experts (or the row padding) and are
+// selected out.  Positions of one weight row are adjacent, so the groups of a
+// wave mostly read the same rowT row.  Out-of-range rows or columns are
+// skipped.
 template <int DT>
 __global__ __launch_bounds__(256) void sddmm_kernel(const uint16_t* __restrict__ rowT, const uint16_t* __restrict__ colT,
-                                                    int64_t ldT, const int32_t* __restrict__ offsets, int64_t R,
-                                                    int64_t n_rows, const int64_t* __restrict__ row_ptr,
+                                                    int64_t ldT, const int32_t* __restrict__ offsets, int32_t E,
+                                                    int32_t R, int32_t C, int64_t n_pos,
+                                                    const int32_t* __restrict__ row_idx,
                                                     const int32_t* __restrict__ col_idx,
                                                     const int64_t* __restrict__ pos_map, float* __restrict__ compact) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t r = wave; r < n_rows; r += n_waves) {
-    const int64_t p0 = row_ptr[r], p1 = row_ptr[r + 1];
-    if (p0 == p1) continue;
-    const int64_t e = r / R, o = r - e * R;
-    const int64_t s0 = offsets[e], s1 = offsets[e + 1];
-    const uint16_t* rv = rowT + o * ldT;
-    for (int64_t p = p0; p < p1; ++p) {
-      const int64_t i = col_idx[p];
-      const uint16_t* cv = colT + i * ldT;
-      float acc = 0.f;
-      for (int64_t s = s0 + lane; s < s1; s += 64)
-        acc += load_as_f32<DT>(rv, s) * load_as_f32<DT>(cv, s);
+  const int gl = threadIdx.x & 15;
+  const int64_t n_grp = ((int64_t)gridDim.x * blockDim.x) >> 4;
+  const uint32_t n_rows = (uint32_t)E * (uint32_t)R;
+  for (int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; p < n_pos; p += n_grp) {
+    const uint32_t r = (uint32_t)row_idx[p];
+    const uint32_t i = (uint32_t)col_idx[p];
+    if (r >= n_rows || i >= (uint32_t)C) continue;
+    const uint32_t e = r / (uint32_t)R;
+    const uint32_t o = r - e * (uint32_t)R;
+    int s0 = offsets[e], s1 = offsets[e + 1];
+    s0 = s0 < 0 ? 0 : s0;
+    s1 = s1 > (int)ldT ? (int)ldT : s1;
+    const uint16_t* rv = rowT + (int64_t)o * ldT;
+    const uint16_t* cv = colT + (int64_t)i * ldT;
+    float acc = 0.f;
+    for (int s = (s0 & ~7) + 8 * gl; s < s1; s += 128) {
+      const uint4 a = *reinterpret_cast<const uint4*>(rv + s);
+      const uint4 b = *reinterpret_cast<const uint4*>(cv + s);
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
-      if (lane == 0) {
-        const int64_t pos = pos_map ? pos_map[p] : p;
-        compact[pos] += round_to<DT>(acc);
+      for (int j = 0; j < 4; ++j) {
+        const float pl = lo_f32<DT>(aw[j]) * lo_f32<DT>(bw[j]);
+        const float ph = hi_f32<DT>(aw[j]) * hi_f32<DT>(bw[j]);
+        acc += ((unsigned)(s + 2 * j - s0) < (unsigned)(s1 - s0)) ? pl : 0.f;
+        acc += ((unsigned)(s + 2 * j + 1 - s0) < (unsigned)(s1 - s0)) ? ph : 0.f;
       }
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+    if (gl == 0) {
+      const int64_t pos = pos_map ? pos_map[p] : p;
+      compact[pos] += round_to<DT>(acc);
     }
   }
 }
@@ -145,29 +204,44 @@ extern "C" int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const in
   if (!in || !out) return set_error(USAF_ERR_INVALID, "gather_transpose: null pointer");
   const int64_t gx = (S + 63) / 64, gy = (C + 63) / 64;
   if (gx > 0x7fffffff || gy > 65535) return set_error(USAF_ERR_INVALID, "gather_transpose: too large");
-  gather_transpose_kernel<<<dim3((unsigned)gx, (unsigned)gy), 256, 0, as_stream(stream)>>>(
-      (const uint16_t*)in, ld_in, rows, S, C, (uint16_t*)out, ld_out);
+  const bool vec = C % 8 == 0 && ld_in % 8 == 0 && ld_out % 8 == 0 && ((uintptr_t)in & 15) == 0 &&
+                   ((uintptr_t)out & 15) == 0;
+  const dim3 grid((unsigned)gx, (unsigned)gy);
+  if (vec)
+    gather_transpose_kernel<true><<<grid, 256, 0, as_stream(stream)>>>((const uint16_t*)in, ld_in, rows, S, C,
+                                                                       (uint16_t*)out, ld_out);
+  else
+    gather_transpose_kernel<false><<<grid, 256, 0, as_stream(stream)>>>((const uint16_t*)in, ld_in, rows, S, C,
+                                                                        (uint16_t*)out, ld_out);
   return check_launch("gather_transpose");
 }
 
 extern "C" int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t ldT, const int32_t* offsets,
-                                     int64_t E, int64_t R, const int64_t* row_ptr, const int32_t* col_idx,
-                                     const int64_t* pos_map, int32_t dtype, float* compact, void* stream) {
-  if (E <= 0 || R <= 0 || ldT < 0) return set_error(USAF_ERR_INVALID, "sddmm_masked: bad sizes");
-  if (!rowT || !colT || !offsets || !row_ptr || !col_idx || !compact)
+                                     int64_t E, int64_t R, int64_t C, int64_t n_pos, const int32_t* row_idx,
+                                     const int32_t* col_idx, const int64_t* pos_map, int32_t dtype, float* compact,
+                                     void* stream) {
+  if (E <= 0 || R <= 0 || C <= 0 || n_pos < 0 || ldT < 0) return set_error(USAF_ERR_INVALID, "sddmm_masked: bad sizes");
+  if (E * R > 0x7fffffff || C > 0x7fffffff || ldT > 0x7fffffff)
+    return set_error(USAF_ERR_INVALID, "sddmm_masked: E*R, C and ldT must fit in int32");
+  if (ldT % 8 != 0) return set_error(USAF_ERR_INVALID, "sddmm_masked: ldT must be a multiple of 8");
+  if (n_pos == 0) return clear_error();
+  if (!rowT || !colT || !offsets || !row_idx || !col_idx || !compact)
     return set_error(USAF_ERR_INVALID, "sddmm_masked: null pointer");
+  if (((uintptr_t)rowT & 15) || ((uintptr_t)colT & 15))
+    return set_error(USAF_ERR_INVALID, "sddmm_masked: rowT and colT must be 16-byte aligned");
   if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "sddmm_masked: dtype must be 16-bit");
-  const int64_t n_rows = E * R;
-  int64_t blocks = (n_rows + 3) / 4;
+  int64_t blocks = (n_pos + 15) / 16;
   const int64_t cap = (int64_t)device_cu_count() * 16;
   if (blocks > cap) blocks = cap;
   hipStream_t st = as_stream(stream);
   if (dtype == USAF_BF16)
     sddmm_kernel<USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)rowT, (const uint16_t*)colT, ldT,
-                                                              offsets, R, n_rows, row_ptr, col_idx, pos_map, compact);
+                                                              offsets, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
+                                                              row_idx, col_idx, pos_map, compact);
   else
     sddmm_kernel<USAF_F16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)rowT, (const uint16_t*)colT, ldT,
-                                                             offsets, R, n_rows, row_ptr, col_idx, pos_map, compact);
+                                                             offsets, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
+                                                             row_idx, col_idx, pos_map, compact);
   return check_launch("sddmm_masked");
 }
 

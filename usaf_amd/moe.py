@@ -292,13 +292,16 @@ class RoutedExpertsFn(torch.autograd.Function):
 
 
 def slot_major(x: torch.Tensor, rows: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """[S or T, C] -> [C, S] (rows gathered by `rows` when given)."""
+    """[S or T, C] -> [C, S] (rows gathered by `rows` when given), as a view of a
+    [C, round_up(S, 8)] buffer: the sampled-gradient kernel reads 16-byte
+    vectors along the slots."""
     C = x.shape[1]
     S = rows.numel() if rows is not None else x.shape[0]
-    out = torch.empty(C, S, dtype=x.dtype, device=x.device)
-    N.call("usaf_hip_gather_transpose", x.data_ptr(), x.stride(0), N.ptr(rows), S, C, out.data_ptr(), S,
+    ld = (S + 7) // 8 * 8
+    out = torch.empty(C, ld, dtype=x.dtype, device=x.device)
+    N.call("usaf_hip_gather_transpose", x.data_ptr(), x.stride(0), N.ptr(rows), S, C, out.data_ptr(), ld,
            N.stream_ptr(x.device))
-    return out
+    return out[:, :S]
 
 
 def routed_experts(hs: torch.Tensor, weights: torch.Tensor, experts: ExpertWeights, capture=None) -> torch.Tensor:

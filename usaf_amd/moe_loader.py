@@ -348,12 +348,15 @@ class SparseGradStore:
             identity = bool(torch.equal(order, torch.arange(idx.numel(), device=dev)))
             rows = torch.div(sidx, C, rounding_mode="floor")
             cols = (sidx - rows * C).to(torch.int32)
+            if E * R >= 2 ** 31 or C >= 2 ** 31:
+                raise ValueError(f"{name}: rows E*R and columns C must fit in int32, shape {shape}")
             row_ptr = torch.zeros(E * R + 1, dtype=torch.int64, device=dev)
             if idx.numel():
                 if int(sidx[0]) < 0 or int(sidx[-1]) >= E * R * C:
                     raise IndexError(f"{name}: active index out of range for shape {shape}")
                 row_ptr[1:] = torch.cumsum(torch.bincount(rows, minlength=E * R), 0)
-            self._csr[name] = (row_ptr, cols.contiguous(), None if identity else order.contiguous(), E, R, C)
+            self._csr[name] = (row_ptr, rows.to(torch.int32).contiguous(), cols.contiguous(),
+                               None if identity else order.contiguous(), E, R, C)
 
     def zero_(self) -> None:
         for v in self.compact.values():
@@ -365,14 +368,16 @@ class SparseGradStore:
         csr = self._csr.get(full_name)
         if csr is None:
             return
-        row_ptr, cols, pos_map, E, R, C = csr
+        _, rows, cols, pos_map, E, R, C = csr
         if rowT.shape[0] != R or colT.shape[0] != C or rowT.shape[1] != colT.shape[1]:
             raise ValueError(f"{full_name}: operands {tuple(rowT.shape)} / {tuple(colT.shape)} do not match "
                              f"the weight rows {R} x cols {C}")
-        if not (rowT.is_contiguous() and colT.is_contiguous()):
-            raise ValueError("slot-major operands must be contiguous")
-        N.call("usaf_hip_sddmm_masked", rowT.data_ptr(), colT.data_ptr(), rowT.shape[1], offsets.data_ptr(), E, R,
-               row_ptr.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
+        ldT = rowT.stride(0)
+        if rowT.stride(1) != 1 or colT.stride(1) != 1 or colT.stride(0) != ldT or ldT % 8:
+            raise ValueError("slot-major operands need unit column stride and one row stride, a multiple of 8 "
+                             "(use usaf_amd.moe.slot_major)")
+        N.call("usaf_hip_sddmm_masked", rowT.data_ptr(), colT.data_ptr(), ldT, offsets.data_ptr(), E, R, C,
+               cols.numel(), rows.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
                self.compact[full_name].data_ptr(), N.stream_ptr(self.device))
 
     def add(self, full_name: str, ei: int, g: torch.Tensor) -> None:
@@ -380,7 +385,7 @@ class SparseGradStore:
         csr = self._csr.get(full_name)
         if csr is None:
             return
-        row_ptr, cols, pos_map, E, R, C = csr
+        row_ptr, _, cols, pos_map, E, R, C = csr
         ei = int(ei)
         p0, p1 = int(row_ptr[ei * R]), int(row_ptr[(ei + 1) * R])
         if p0 == p1:
