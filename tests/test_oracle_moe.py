@@ -148,3 +148,48 @@ def test_sparse_adam_reference_qualitative():
     M.sparse_adam_step(p, torch.ones(3), m, v, 1, 1.0)
     assert bool((p < 1.0).all())
     assert math.isclose(float(p[0]), 0.0, abs_tol=1e-6)  # 1 - 1.0 * 1/(1+1e-8)
+
+
+def test_backward_dhs_dwgate_closed_form():
+    # float64 closed form of the SwiGLU expert backward: dact = (dout * w) Wd,
+    # dgate = dact * up * silu'(gate), dup = dact * silu(gate), dgu = [dgate, dup],
+    # dhs = sum_e dgu_e Wgu_e, dWgu_e = dgu_e^T x_e
+    hs, w, wg, wd = _layer(dtype=torch.float32)
+    g = torch.Generator().manual_seed(10)
+    dout = torch.randn(hs.shape, generator=g)
+    dhs, _, dwg, _ = M.experts_routed_autograd(hs, w, wg, wd, dout)
+    x, W, G, D, dO = hs.double(), w.double(), wg.double(), wd.double(), dout.double()
+    I = D.shape[2]
+    dhs_ref = torch.zeros_like(x)
+    for e in range(G.shape[0]):
+        idx = torch.nonzero(W[:, e]).reshape(-1)
+        if idx.numel() == 0:
+            assert torch.all(dwg[e] == 0)
+            continue
+        xe = x[idx]
+        gu = xe @ G[e].t()
+        gate, up = gu[:, :I], gu[:, I:]
+        sig = torch.sigmoid(gate)
+        dact = (dO[idx] * W[idx, e:e + 1]) @ D[e]
+        dgate = dact * up * (sig * (1 + gate * (1 - sig)))
+        dup = dact * gate * sig
+        dgu = torch.cat([dgate, dup], 1)
+        dhs_ref.index_add_(0, idx, dgu @ G[e])
+        assert torch.allclose(dwg[e].double(), dgu.t() @ xe, rtol=1e-4, atol=1e-6)
+    assert torch.allclose(dhs.double(), dhs_ref, rtol=1e-4, atol=1e-6)
+
+
+def test_combine_slots_brute_force():
+    g = torch.Generator().manual_seed(12)
+    T, E, H = 30, 5, 16
+    w = (torch.rand(T, E, generator=g) < 0.4).float() * torch.rand(T, E, generator=g)
+    counts, offsets, tok, _ = M.bucket(w)
+    y = torch.randn(int(offsets[-1]), H, generator=g)
+    out = M.combine_slots(y, offsets, tok, w)
+    ref = torch.zeros(T, H, dtype=torch.float64)
+    for e in range(E):
+        for s in range(int(offsets[e]), int(offsets[e + 1])):
+            t = int(tok[s])
+            ref[t] += y[s].double() * float(w[t, e])
+    assert torch.allclose(out.double(), ref, rtol=1e-6, atol=1e-6)
+    assert torch.all(out[(w != 0).sum(1) == 0] == 0)

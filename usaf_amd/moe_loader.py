@@ -176,6 +176,7 @@ class QuantizedExpertCache:
             return {p: torch.nn.Parameter(t, requires_grad=t.requires_grad) for p, t in cached.items()}
         self.misses += 1
         if expert_module_name in self._resident:
+            # resident modules join the cache without evicting others (moe_loader.py:153-164)
             params = self._get_resident(expert_module_name)
             for k, v in self._dequant(expert_module_name).items():
                 params.setdefault(k, v)
@@ -188,7 +189,7 @@ class QuantizedExpertCache:
                     t.record_stream(torch.cuda.current_stream(self._device))
             else:
                 params = self._dequant(expert_module_name)
-        self._evict_for(self._nbytes(params))
+            self._evict_for(self._nbytes(params))
         self._cache[expert_module_name] = params
         return {p: torch.nn.Parameter(t, requires_grad=True) for p, t in params.items()}
 
