@@ -74,6 +74,15 @@ int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f16, const u
 int usaf_hip_quantize_q4(const void* x, int32_t x_dtype, int64_t numel, int64_t group_size,
                          int8_t* packed, uint16_t* scale_f16, uint16_t* zero_f16, void* stream);
 
+/*
+ * Scale/zero pairs for the fused GEMMs: scale_zero[g] = scale bits | zero bits << 16
+ * (both fp16), one 32-bit word per group, so a GEMM reads a group's parameters with
+ * one load.  Derived once per 4-bit tensor from the codec's scale/zero arrays
+ * (the fp16 scale/zero of usaf/quantization.py:82-83); no counterpart in the reference.
+ */
+int usaf_hip_pack_scale_zero(const uint16_t* scale_f16, const uint16_t* zero_f16, int64_t n_groups,
+                             uint32_t* scale_zero, void* stream);
+
 /* ---- routing and bucketing ------------------------------------------------ */
 
 /*
@@ -139,12 +148,13 @@ int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_
 /* ---- fused 4-bit dequant grouped GEMMs (MFMA) ----------------------------- */
 /*
  * Weights are whole [E, rows, cols] tensors in the codec format above
- * (packed int8 [E*rows*cols/128, 64], fp16 scale/zero [E*rows*cols/128]);
+ * (packed int8 [E*rows*cols/128, 64]) with their scale/zero pairs `wsz`
+ * (usaf_hip_pack_scale_zero, [E*rows*cols/128]);
  * expert e owns slots offsets[e] .. offsets[e+1]-1.  Activations are fp16 or
  * bf16 (`dtype`); with bf16 the weight operand is the bf16 rounding of the
  * fp16 dequantized value.  Accumulation is fp32 on MFMA.  When `w16` is not
  * NULL the weight is instead that dense [E, rows, cols] tensor of `dtype` (the
- * reference's dense expert weights) and wq/ws/wz may be NULL.  Weight pointers
+ * reference's dense expert weights) and wq/wsz may be NULL.  Weight pointers
  * must be 16-byte aligned.
  */
 
@@ -152,26 +162,26 @@ int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_
  * ([S, 2I], dtype-rounded), act[s] = dtype(dtype(silu(gate)) * up) ([S, I]).
  * x [T, H] (token_idx values < T); W_gate_up [E, 2I, H]; needs H % 128 == 0, I % 64 == 0. */
 int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T, int64_t H, const int32_t* token_idx, const int32_t* offsets, int64_t S,
-                             int64_t E, int64_t I, const int8_t* wq, const uint16_t* ws, const uint16_t* wz,
+                             int64_t E, int64_t I, const int8_t* wq, const uint32_t* wsz,
                              const void* w16, int32_t dtype, void* gu, void* act, void* stream);
 
 /* Replaces qwen3moe_dml.py:61: y[s] = act[s] @ W_down[e]^T ([S, H]).  W_down [E, H, I];
  * needs I % 128 == 0, H % 128 == 0. */
 int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
-                          const int8_t* wq, const uint16_t* ws, const uint16_t* wz, const void* w16, int32_t dtype, void* y,
+                          const int8_t* wq, const uint32_t* wsz, const void* w16, int32_t dtype, void* y,
                           void* stream);
 
 /* Autograd of qwen3moe_dml.py:60-61: dact = dcur @ W_down[e] through the SwiGLU
  * (saved gu) -> dgu [S, 2I] (gate half, up half).  Needs I % 128 == 0, H % 64 == 0. */
 int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S, int64_t E,
-                          int64_t I, const int8_t* wq, const uint16_t* ws, const uint16_t* wz, const void* w16, int32_t dtype,
+                          int64_t I, const int8_t* wq, const uint32_t* wsz, const void* w16, int32_t dtype,
                           void* dgu, void* stream);
 
 /* Autograd of qwen3moe_dml.py:58 (grad-input): dx_slots[s] = dgu[s] @ W_gate_up[e]
  * ([S, H]); sum per token with usaf_hip_moe_combine(weights=NULL).
  * Needs H % 128 == 0, 2I % 64 == 0. */
 int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
-                             const int8_t* wq, const uint16_t* ws, const uint16_t* wz, const void* w16, int32_t dtype, void* dx_slots,
+                             const int8_t* wq, const uint32_t* wsz, const void* w16, int32_t dtype, void* dx_slots,
                              void* stream);
 
 /* ---- sparse gradient path and optimizer ----------------------------------- */

@@ -178,11 +178,11 @@ def test_experts_forward_intermediates(gpu_device):
     y = torch.empty(S, H, dtype=dt, device=gpu_device)
     from usaf_amd import _native as N
     st = N.stream_ptr(gpu_device)
-    q, s, z, w16 = ew._ptrs("gate_up", dt)
+    q, sz, w16 = ew._ptrs("gate_up", dt)
     N.call("usaf_hip_moe_gate_up_fwd", L["hs"].to(gpu_device).data_ptr(), L["hs"].shape[0], H, b.token_idx.data_ptr(),
-           b.offsets.data_ptr(), S, ew.E, I, q, s, z, w16, N.BF16, gu.data_ptr(), act.data_ptr(), st)
-    q, s, z, w16 = ew._ptrs("down", dt)
-    N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, ew.E, H, q, s, z, w16, N.BF16,
+           b.offsets.data_ptr(), S, ew.E, I, q, sz, w16, N.BF16, gu.data_ptr(), act.data_ptr(), st)
+    q, sz, w16 = ew._ptrs("down", dt)
+    N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, ew.E, H, q, sz, w16, N.BF16,
            y.data_ptr(), st)
     torch.cuda.synchronize()
     offs = b.offsets.cpu().tolist()

@@ -229,6 +229,17 @@ int launch_blocks(int64_t work_items, int per_block, int max_blocks_per_cu) {
 
 using namespace usaf;
 
+namespace usaf {
+namespace {
+__global__ __launch_bounds__(256) void pack_scale_zero_kernel(const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
+                                                              int64_t n, uint32_t* __restrict__ sz) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    sz[i] = (uint32_t)s[i] | ((uint32_t)z[i] << 16);
+}
+}  // namespace
+}  // namespace usaf
+
 extern "C" int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
                                    int64_t n_groups, int64_t packed_cols, int64_t group_size, int64_t numel,
                                    void* out, int32_t out_dtype, void* stream) {
@@ -295,4 +306,16 @@ extern "C" int usaf_hip_quantize_q4(const void* x, int32_t x_dtype, int64_t nume
                    quantize_kernel<DT><<<(unsigned)blocks, 256, 0, st>>>(x, numel, eff_gs, n_groups,
                                                                         (uint8_t*)packed, scale_f16, zero_f16));
   return check_launch("quantize_q4");
+}
+
+extern "C" int usaf_hip_pack_scale_zero(const uint16_t* scale_f16, const uint16_t* zero_f16, int64_t n_groups,
+                                        uint32_t* scale_zero, void* stream) {
+  if (n_groups < 0) return set_error(USAF_ERR_INVALID, "pack_scale_zero: negative group count");
+  if (n_groups == 0) return clear_error();
+  if (!scale_f16 || !zero_f16 || !scale_zero) return set_error(USAF_ERR_INVALID, "pack_scale_zero: null pointer");
+  int64_t blocks = (n_groups + 255) / 256;
+  const int64_t cap = (int64_t)device_cu_count() * 8;
+  if (blocks > cap) blocks = cap;
+  pack_scale_zero_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(scale_f16, zero_f16, n_groups, scale_zero);
+  return check_launch("pack_scale_zero");
 }

@@ -69,8 +69,7 @@ struct GemmArgs {
   int64_t lda;
   const int32_t* a_rows;   // A row of slot m (nullptr: row m)
   const uint8_t* wq;       // packed codes of the whole [E, w_rows, w_cols] weight
-  const uint16_t* ws;      // fp16 scales, one per 128 elements
-  const uint16_t* wz;      // fp16 zeros
+  const uint32_t* wsz;     // per 128-element group: fp16 scale bits | fp16 zero bits << 16
   const uint16_t* w16;     // dense 16-bit weight [E, w_rows, w_cols] (BQ == BQ_DENSE16)
   int64_t w_rows, w_cols;  // per-expert weight matrix
   int64_t N, K;            // output columns, contraction length
@@ -81,6 +80,16 @@ struct GemmArgs {
   uint16_t* out2; int64_t ldo2;  // SWIGLU_FWD: gu
   const uint16_t* aux; int64_t ld_aux;  // SWIGLU_BWD: saved gu
 };
+
+// Workgroup barrier ordering LDS accesses only.  __syncthreads() also orders
+// global memory, which makes every wave drain its outstanding global loads
+// (s_waitcnt vmcnt(0)) at each barrier and exposes the full memory latency of
+// the prefetched k-steps; no thread here communicates through global memory.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // ---- 4-bit -> 16-bit conversion (bit-identical to dequantize_4bit) ----------
 
@@ -224,13 +233,13 @@ __device__ __forceinline__ void produce_tile(const GemmArgs& g, uint16_t* sA0, u
       if constexpr (BMODE == BMODE_NK) {
         const int64_t el = b_off[0] + ks;
         rb4[S][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g.wq + (el >> 1)));
-        rsz[S][0] = (uint32_t)g.ws[el >> 7] | ((uint32_t)g.wz[el >> 7] << 16);
+        rsz[S][0] = g.wsz[el >> 7];
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int64_t el = b_off[0] + r * g.w_cols + ks;
           rw[S][r] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(g.wq + (el >> 1)));
-          rsz[S][r] = (uint32_t)g.ws[el >> 7] | ((uint32_t)g.wz[el >> 7] << 16);
+          rsz[S][r] = g.wsz[el >> 7];
         }
       }
     } else {
@@ -311,17 +320,17 @@ __device__ __forceinline__ void produce_tile(const GemmArgs& g, uint16_t* sA0, u
     if (nk > 1) load_tile(S1{}, 1);
     if (nk > 2) load_tile(S2{}, 2);
     store_tile(S0{}, 0);
-    __syncthreads();
+    lds_barrier();
     int k = 0;
     for (; k + 5 < nk; k += 3) {
-      store_tile(S1{}, (k + 1) & 1); load_tile(S0{}, k + 3); __syncthreads();
-      store_tile(S2{}, (k + 2) & 1); load_tile(S1{}, k + 4); __syncthreads();
-      store_tile(S0{}, (k + 3) & 1); load_tile(S2{}, k + 5); __syncthreads();
+      store_tile(S1{}, (k + 1) & 1); load_tile(S0{}, k + 3); lds_barrier();
+      store_tile(S2{}, (k + 2) & 1); load_tile(S1{}, k + 4); lds_barrier();
+      store_tile(S0{}, (k + 3) & 1); load_tile(S2{}, k + 5); lds_barrier();
     }
     auto step = [&](auto store_c, auto load_c, int kk) {
       if (kk + 1 < nk) store_tile(store_c, (kk + 1) & 1);
       if (kk + 3 < nk) load_tile(load_c, kk + 3);
-      __syncthreads();
+      lds_barrier();
     };
     for (; k < nk; k += 3) {
       step(S1{}, S0{}, k);
@@ -332,23 +341,23 @@ __device__ __forceinline__ void produce_tile(const GemmArgs& g, uint16_t* sA0, u
     load_tile(S0{}, 0);
     if (nk > 1) load_tile(S1{}, 1);
     store_tile(S0{}, 0);
-    __syncthreads();
+    lds_barrier();
     int k = 0;
     for (; k + 3 < nk; k += 2) {
-      store_tile(S1{}, (k + 1) & 1); load_tile(S0{}, k + 2); __syncthreads();
-      store_tile(S0{}, (k + 2) & 1); load_tile(S1{}, k + 3); __syncthreads();
+      store_tile(S1{}, (k + 1) & 1); load_tile(S0{}, k + 2); lds_barrier();
+      store_tile(S0{}, (k + 2) & 1); load_tile(S1{}, k + 3); lds_barrier();
     }
     auto step = [&](auto store_c, auto load_c, int kk) {
       if (kk + 1 < nk) store_tile(store_c, (kk + 1) & 1);
       if (kk + 2 < nk) load_tile(load_c, kk + 2);
-      __syncthreads();
+      lds_barrier();
     };
     for (; k < nk; k += 2) {
       step(S1{}, S0{}, k);
       if (k + 1 < nk) step(S0{}, S1{}, k + 1);
     }
   }
-  __syncthreads();  // the multiply waves park their accumulators
+  lds_barrier();  // the multiply waves park their accumulators
 }
 
 // ---- multiply waves: LDS fragments -> MFMA, accumulators parked in LDS ----
@@ -372,7 +381,7 @@ __device__ __forceinline__ void consume_tile(const uint16_t* sA0, const uint16_t
     return *reinterpret_cast<const u32x4*>(
         &sB0[st * (BN * LDSW) + (wn * 64 + j * 32 + (lane & 31)) * LDSW + kk * 16 + (lane >> 5) * 8]);
   };
-  __syncthreads();  // stage 0 filled
+  lds_barrier();  // stage 0 filled
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     u32x4 fa[WM_SUB], fb[2];
@@ -398,7 +407,7 @@ __device__ __forceinline__ void consume_tile(const uint16_t* sA0, const uint16_t
         for (int j = 0; j < 2; ++j) fb[j] = fbn[j];
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   // park dtype(acc) as the [BM][BN] tile; acc[i][j][r] is tile row
   // 32*(wm*WM_SUB+i) + 8*(r/4) + 4*(lane/32) + r%4, column wn*64 + j*32 + lane%32
@@ -414,7 +423,7 @@ __device__ __forceinline__ void consume_tile(const uint16_t* sA0, const uint16_t
           sC[row * LDSC + col] = round_bits<DT>(acc[i][j][r]);
         }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 template <int BMODE, int EPI, int BQ, int DT>
@@ -444,12 +453,12 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(const GemmArgs g) {
       if (e < E) local += (g.offsets[e + 1] - g.offsets[e] + BM - 1) / BM;
     }
     s_part[tid] = local;
-    __syncthreads();
+    lds_barrier();
     for (int off = 1; off < kThreads; off <<= 1) {
       const int v = (tid >= off) ? s_part[tid - off] : 0;
-      __syncthreads();
+      lds_barrier();
       s_part[tid] += v;
-      __syncthreads();
+      lds_barrier();
     }
     int run = s_part[tid] - local;
     for (int i = 0; i < per; ++i) {
@@ -460,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(const GemmArgs g) {
       }
     }
     if (tid == kThreads - 1) s_mt[E] = s_part[kThreads - 1];
-    __syncthreads();
+    lds_barrier();
   }
   const int64_t n_mt = s_mt[E];
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? g.N / 64 : g.N / BN;
@@ -563,8 +572,454 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(const GemmArgs g) {
         *reinterpret_cast<u32x4*>(g.out + m * g.ldo + g.inter + n) = u32x4{du_w[0], du_w[1], du_w[2], du_w[3]};
       }
     }
-    __syncthreads();  // sC aliases the stage buffers the next tile fills
+    lds_barrier();  // sC aliases the stage buffers the next tile fills
   }
+}
+
+// =====================================================================================
+// Forward (NK) kernel: weight fragments dequantized straight into MFMA registers.
+//
+// 256 threads = 4 waves, one per SIMD, one block per CU.  Tile: up to 320 slots
+// of one expert (10 row blocks of 32) x 256 output columns; wave w owns tile
+// columns [64w, 64w + 64) (two 32-column blocks) for every row.  Per k-step of 64:
+//   * the block stages the 320 x 64 activation tile in LDS (two stages), loaded
+//     one k-step ahead into registers;
+//   * each lane loads the 16 code bytes (32 k-values of one group) of its weight
+//     row per column block and dequantizes them in registers into the k-step's
+//     four MFMA B fragments: lane half h takes k = 32h + 8j + [0, 8) at sub-step
+//     j, and the activation fragments read the same k from LDS.
+// The weight tile never touches LDS and every weight element is dequantized
+// once; the activation tile is read from global memory once per 256 columns.
+// SwiGLU: column block 0 of wave w holds gate rows n, block 1 the up rows I + n
+// of the same 32 n, so silu(gate) * up is formed in registers.
+// =====================================================================================
+constexpr int NK_BM = 256, NK_BN = 256, NK_THREADS = 256;
+constexpr int NK_A_CHUNKS = NK_BM * BK / 8 / NK_THREADS;  // 16-byte A chunks per thread per k-step
+constexpr int NK_EPW = 40;      // epilogue staging row stride (16-bit elements; rows stay 16-byte aligned)
+constexpr int NK_EPI_ARR = 3;   // 32 x 32 blocks a wave stages per row block (gate, up, act)
+constexpr int NK_EPI_ELEMS = NK_EPI_ARR * 32 * NK_EPW;
+constexpr size_t kNkSmemBytes =
+    (size_t)2 * NK_BM * LDSW * 2 + (size_t)4 * NK_EPI_ELEMS * 2 + (size_t)(MAX_E + 1 + NK_THREADS) * 4;
+
+// 8 codes of one 32-bit word (code 2i in the low nibble of byte i) -> 8 16-bit
+// weights in natural order, bit-identical to dequantize_4bit:
+// fp16(fp16(q * s) + z), then RNE bf16 for bf16 operands.
+template <int DT>
+__device__ __forceinline__ u32x4 dq8(uint32_t w, f16x2 s2, f16x2 z2) {
+#pragma clang fp contract(off)
+  const f16x2 mul = {(f16)1.0f, (f16)0.0625f};
+  const f16x2 sub = {(f16)-1024.0f, (f16)-64.0f};
+  uint32_t o[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    // byte p in both halves: the low half keeps code 2p (bits 0-3), the high half
+    // code 2p+1 (bits 20-23), as fp16 1024 + q and 1024 + 16 q
+    const uint32_t t = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)p << 16) | (uint32_t)p);
+    const uint32_t bits = (t & 0x00F0000Fu) | 0x64006400u;
+    const f16x2 q = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, bits), mul, sub);  // exact codes
+    const f16x2 m = q * s2;
+    const f16x2 v = m + z2;
+    o[p] = __builtin_bit_cast(uint32_t, v);
+    if constexpr (DT == USAF_BF16) o[p] = h2_to_bf2(o[p]);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// Codes 2p, 2p+1 of a 32-bit code word (byte p) -> their two 16-bit weights
+// (dq8 for one pair).  v_perm places byte p under the fp16 exponent byte 0x64 in
+// both halves; the mask keeps code 2p in the low half (1024 + q) and code 2p+1
+// in the high half (1024 + 16 q).
+template <int DT>
+__device__ __forceinline__ uint32_t dq_pair(uint32_t w, int p, f16x2 s2, f16x2 z2) {
+#pragma clang fp contract(off)
+  const f16x2 mul = {(f16)1.0f, (f16)0.0625f};
+  const f16x2 sub = {(f16)-1024.0f, (f16)-64.0f};
+  const uint32_t t = __builtin_amdgcn_perm(0x64646464u, w, 0x04000400u | ((uint32_t)p << 16) | (uint32_t)p) & 0xFFF0FF0Fu;
+  const f16x2 q = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, t), mul, sub);  // exact codes
+  const f16x2 m = q * s2;
+  const f16x2 v = m + z2;
+  uint32_t o = __builtin_bit_cast(uint32_t, v);
+  if constexpr (DT == USAF_BF16) o = h2_to_bf2(o);
+  return o;
+}
+
+// m-tile prefix over experts (m-tiles of BMV slots): s_mt[e] = first m-tile of
+// expert e, s_mt[E] = total.  All THREADS threads call it.
+template <int THREADS, int BMV>
+__device__ __forceinline__ void mtile_prefix(const GemmArgs& g, int32_t* s_mt, int32_t* s_part, int tid) {
+  const int E = g.E;
+  const int per = (E + THREADS - 1) / THREADS;
+  const int e0 = tid * per;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) local += (g.offsets[e + 1] - g.offsets[e] + BMV - 1) / BMV;
+  }
+  s_part[tid] = local;
+  lds_barrier();
+  for (int off = 1; off < THREADS; off <<= 1) {
+    const int v = (tid >= off) ? s_part[tid - off] : 0;
+    lds_barrier();
+    s_part[tid] += v;
+    lds_barrier();
+  }
+  int run = s_part[tid] - local;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      s_mt[e] = run;
+      run += (g.offsets[e + 1] - g.offsets[e] + BMV - 1) / BMV;
+    }
+  }
+  if (tid == THREADS - 1) s_mt[E] = s_part[THREADS - 1];
+  lds_barrier();
+}
+
+// One tile of the NK kernel with NRB (>= the tile's occupied row blocks) row
+// blocks computed.  Row blocks past the expert's slots multiply rows of the
+// staged tile that are never stored.
+template <int NRB, int EPI, int BQ, int DT>
+__device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16_t* sE, const int tid, const int e,
+                                        const int64_t m_beg, const int valid, const int64_t nt, const int nk) {
+  const int lane = tid & 63, wave = tid >> 6, l32 = lane & 31, half = lane >> 5;
+  const int64_t K = g.K;
+  // this wave's weight rows (one per column block) and whether it has columns at all;
+  // a wave without columns (last n-tile of a ragged N) multiplies row 0's weights
+  // and stores nothing, so the k-loop has no wave-dependent branches
+  int64_t nbase;  // first output column of the wave (gate column for SwiGLU)
+  bool wave_on;
+  int64_t wrow[2];
+  if constexpr (EPI == EPI_SWIGLU_FWD) {
+    nbase = nt * 128 + wave * 32;
+    wave_on = nbase < g.inter;
+    wrow[0] = nbase + l32;
+    wrow[1] = g.inter + nbase + l32;
+  } else {
+    nbase = nt * NK_BN + wave * 64;
+    wave_on = nbase < g.N;
+    wrow[0] = nbase + l32;
+    wrow[1] = nbase + 32 + l32;
+  }
+  // element offset of (weight row, k = 32 * half) in the [E, w_rows, K] weight
+  int64_t woff[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) woff[cb] = ((int64_t)e * g.w_rows + (wave_on ? wrow[cb] : 0)) * K + 32 * half;
+
+  // A: chunk c = tid + 256 i is row (tid >> 3) + 32 i (row block i), k block tid & 7
+  int32_t a_off[NRB];
+#pragma unroll
+  for (int i = 0; i < NRB; ++i) {
+    const int row = (tid >> 3) + 32 * i;
+    const int64_t m = m_beg + (row < valid ? row : valid - 1);
+    const int64_t arow = g.a_rows ? (int64_t)g.a_rows[m] : m;
+    a_off[i] = (int32_t)(arow * g.lda + (tid & 7) * 8);
+  }
+  const int a_lds = (tid >> 3) * LDSW + (tid & 7) * 8;
+
+  using std::integral_constant;
+  constexpr int R = 4 * NRB;     // regions per k-step: (sub-step j = r / NRB, row block i = r % NRB)
+  constexpr int PF = 4;          // A-fragment prefetch distance (regions)
+  constexpr int NPAIR = (BQ == BQ_Q4) ? 32 : 0;  // weight pairs per k-step per lane
+  constexpr int PPR = (NPAIR + R - 1) / R;       // pairs dequantized per region
+  const int frag = l32 * LDSW + 32 * half;  // lane's A fragment: row l32 of a row block, k = 32 half + 8 j
+
+  u32x4 ra[NRB];            // A chunks of the next stage, in flight between global and LDS
+  u32x4 bfs[2][2][4];       // B fragments [slot][column block][sub-step j]
+  u32x4 cq[3][2];           // 4-bit codes of three k-steps (ring) [slot][column block]
+  uint32_t csz[3][2];       // their scale/zero pairs
+  f32x16 acc[NRB][2];
+#pragma unroll
+  for (int i = 0; i < NRB; ++i) acc[i][0] = acc[i][1] = f32x16{};
+
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < NRB; ++i) ra[i] = *reinterpret_cast<const u32x4*>(g.A + a_off[i] + kt * BK);
+  };
+  auto store_a = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < NRB; ++i) *reinterpret_cast<u32x4*>(&sA0[st * (NK_BM * LDSW) + a_lds + 32 * i * LDSW]) = ra[i];
+  };
+  // codes + scale/zero pairs of k-step kk (clamped to the last one) into ring slot CS
+  auto load_codes = [&](auto CSc, int kk) {
+    constexpr int CS = decltype(CSc)::value;
+    kk = kk < nk ? kk : nk - 1;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int64_t el = woff[cb] + (int64_t)kk * BK;
+      cq[CS][cb] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g.wq + (el >> 1)));
+      csz[CS][cb] = g.wsz[el >> 7];
+    }
+  };
+  // dense 16-bit weight fragments of k-step kk into B slot BS
+  auto load_dense = [&](auto BSc, int kk) {
+    constexpr int BS = decltype(BSc)::value;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int64_t el = woff[cb] + (int64_t)kk * BK;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfs[BS][cb][j] = *reinterpret_cast<const u32x4*>(g.w16 + el + 8 * j);
+    }
+  };
+  // whole-k-step dequant of ring slot CS into B slot BS (prologue and tail)
+  auto dequant_all = [&](auto BSc, auto CSc) {
+    constexpr int BS = decltype(BSc)::value, CS = decltype(CSc)::value;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const f16x2 s2 = __builtin_bit_cast(f16x2, (csz[CS][cb] & 0xFFFFu) * 0x10001u);
+      const f16x2 z2 = __builtin_bit_cast(f16x2, (csz[CS][cb] >> 16) * 0x10001u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfs[BS][cb][j] = dq8<DT>(cq[CS][cb][j], s2, z2);
+    }
+  };
+  // the MFMAs of k-step kt alone (last two k-steps), in the same regions
+  auto mma = [&](auto BSc, int kt) {
+    constexpr int BS = decltype(BSc)::value;
+    const uint16_t* sA = sA0 + (kt & 1) * (NK_BM * LDSW);
+    u32x4 af[R];
+#pragma unroll
+    for (int r = 0; r < PF && r < R; ++r)
+      af[r] = *reinterpret_cast<const u32x4*>(&sA[(r % NRB) * 32 * LDSW + frag + 8 * (r / NRB)]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int j = r / NRB, i = r % NRB;
+      if (r + PF < R)
+        af[r + PF] = *reinterpret_cast<const u32x4*>(&sA[((r + PF) % NRB) * 32 * LDSW + frag + 8 * ((r + PF) / NRB)]);
+      acc[i][0] = mfma32<DT>(af[r], bfs[BS][0][j], acc[i][0]);
+      acc[i][1] = mfma32<DT>(af[r], bfs[BS][1][j], acc[i][1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // One steady k-step kt (kt + 2 < nk), software-pipelined in source order: the
+  // 8 * NRB MFMAs form R regions of two; every region also reads the A
+  // fragment of region r + PF from LDS and dequantizes its share of the next
+  // k-step's weights (ring slot CS -> B slot BS ^ 1), and every other region
+  // stages one A chunk of kt + 1 into LDS or refills it with kt + 2.  The codes
+  // of kt + 3 are fetched at the top, two k-steps before they are needed.
+  // sched_barrier keeps the regions in this order, so the matrix pipe has
+  // independent VALU, LDS and memory work issued between its MFMAs.
+  auto step = [&](auto BSc, auto CSc, int kt) {
+    constexpr int BS = decltype(BSc)::value, CS = decltype(CSc)::value;
+    const uint16_t* sA = sA0 + (kt & 1) * (NK_BM * LDSW);
+    uint16_t* sAn = sA0 + ((kt + 1) & 1) * (NK_BM * LDSW);
+    u32x4 af[R];
+    f16x2 s2[2], z2[2];
+#pragma unroll
+    for (int r = 0; r < PF && r < R; ++r)
+      af[r] = *reinterpret_cast<const u32x4*>(&sA[(r % NRB) * 32 * LDSW + frag + 8 * (r / NRB)]);
+    if constexpr (BQ == BQ_Q4) load_codes(integral_constant<int, (CS + 2) % 3>{}, kt + 3);
+    else load_dense(integral_constant<int, BS ^ 1>{}, kt + 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int j = r / NRB, i = r % NRB;
+      if (r + PF < R)
+        af[r + PF] = *reinterpret_cast<const u32x4*>(&sA[((r + PF) % NRB) * 32 * LDSW + frag + 8 * ((r + PF) / NRB)]);
+      acc[i][0] = mfma32<DT>(af[r], bfs[BS][0][j], acc[i][0]);
+      acc[i][1] = mfma32<DT>(af[r], bfs[BS][1][j], acc[i][1]);
+      if constexpr (BQ == BQ_Q4) {
+#pragma unroll
+        for (int pp = 0; pp < PPR; ++pp) {
+          const int p = r * PPR + pp;
+          if (p < NPAIR) {
+            const int cb = p >> 4, wd = (p >> 2) & 3, q = p & 3;
+            if ((p & 15) == 0) {
+              s2[cb] = __builtin_bit_cast(f16x2, (csz[CS][cb] & 0xFFFFu) * 0x10001u);
+              z2[cb] = __builtin_bit_cast(f16x2, (csz[CS][cb] >> 16) * 0x10001u);
+            }
+            bfs[BS ^ 1][cb][wd][q] = dq_pair<DT>(cq[CS][cb][wd], q, s2[cb], z2[cb]);
+          }
+        }
+      }
+      if ((r & 1) == 0 && (r >> 1) < NRB)  // stage chunk r/2 of k-step kt + 1
+        *reinterpret_cast<u32x4*>(&sAn[a_lds + 32 * (r >> 1) * LDSW]) = ra[r >> 1];
+      if ((r & 1) == 1 && (r >> 1) < NRB)  // then refill it with k-step kt + 2
+        ra[r >> 1] = *reinterpret_cast<const u32x4*>(g.A + a_off[r >> 1] + (kt + 2) * BK);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier();
+  };
+
+  // prologue: A of k-step 0 staged in LDS and k-step 1 in flight; B of k-step 0
+  // in slot 0; codes of k-steps 1 and 2 in ring slots 0 and 1
+  using I0 = integral_constant<int, 0>;
+  using I1 = integral_constant<int, 1>;
+  using I2 = integral_constant<int, 2>;
+  load_a(0);
+  if constexpr (BQ == BQ_Q4) {
+    load_codes(I2{}, 0);
+    load_codes(I0{}, 1);
+    load_codes(I1{}, 2);
+  } else {
+    load_dense(I0{}, 0);
+  }
+  store_a(0);
+  if constexpr (BQ == BQ_Q4) dequant_all(I0{}, I2{});
+  load_a(1);
+  lds_barrier();
+
+  // steady state, unrolled by six so that the B slots (period 2) and the code
+  // ring (period 3) are addressed statically: no register moves of data whose
+  // loads may still be in flight
+  int kt = 0;
+  for (; kt + 7 < nk; kt += 6) {
+    step(I0{}, I0{}, kt);
+    step(I1{}, I1{}, kt + 1);
+    step(I0{}, I2{}, kt + 2);
+    step(I1{}, I0{}, kt + 3);
+    step(I0{}, I1{}, kt + 4);
+    step(I1{}, I2{}, kt + 5);
+  }
+  // remaining steady steps (fewer than six) rotate the slots back to the same
+  // positions after each step
+  for (; kt + 2 < nk; ++kt) {
+    step(I0{}, I0{}, kt);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfs[0][cb][j] = bfs[1][cb][j];
+      cq[0][cb] = cq[1][cb];
+      csz[0][cb] = csz[1][cb];
+      cq[1][cb] = cq[2][cb];
+      csz[1][cb] = csz[2][cb];
+    }
+  }
+  // the last two k-steps (nk >= 2: the entry points require K % 128 == 0)
+  mma(I0{}, kt);
+  store_a((kt + 1) & 1);
+  if constexpr (BQ == BQ_Q4) dequant_all(I1{}, I0{});
+  else load_dense(I1{}, kt + 1);
+  lds_barrier();
+  mma(I1{}, kt + 1);
+  lds_barrier();  // every wave is done with the staged tiles
+
+  // ---- epilogue: per row block, the wave's dtype results go through its own LDS
+  //      area (C-fragment layout -> rows) and out as 16-byte row stores ----
+  if (!wave_on) return;
+  const int nrb = (valid + 31) >> 5;
+#pragma unroll
+  for (int i = 0; i < NRB; ++i) {
+    if (i >= nrb) continue;
+    const int rows = valid - 32 * i;  // valid rows in this row block (may exceed 32)
+    if constexpr (EPI == EPI_SWIGLU_FWD) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+        const uint16_t gb = round_bits<DT>(acc[i][0][r]);
+        const uint16_t ub = round_bits<DT>(acc[i][1][r]);
+        const float sg = round_to<DT>(silu_f(bits_to_f32<DT>(gb)));
+        const uint16_t ab = round_bits<DT>(sg * bits_to_f32<DT>(ub));
+        sE[row * NK_EPW + l32] = gb;
+        sE[32 * NK_EPW + row * NK_EPW + l32] = ub;
+        sE[64 * NK_EPW + row * NK_EPW + l32] = ab;
+      }
+#pragma unroll
+      for (int q = 0; q < 6; ++q) {
+        const int c = lane + 64 * q;
+        const int arr = c >> 7, rr = (c & 127) >> 2, part = c & 3;
+        if (rr < rows) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&sE[arr * 32 * NK_EPW + rr * NK_EPW + part * 8]);
+          const int64_t m = m_beg + 32 * i + rr;
+          const int64_t n = nbase + part * 8;
+          uint16_t* dst = (arr == 2) ? g.out + m * g.ldo + n : g.out2 + m * g.ldo2 + (arr == 1 ? g.inter : 0) + n;
+          *reinterpret_cast<u32x4*>(dst) = v;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 8 * (r >> 2) + 4 * half + (r & 3);
+          sE[cb * 32 * NK_EPW + row * NK_EPW + l32] = round_bits<DT>(acc[i][cb][r]);
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = lane + 64 * q;
+        const int cb = c >> 7, rr = (c & 127) >> 2, part = c & 3;
+        if (rr < rows) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(&sE[cb * 32 * NK_EPW + rr * NK_EPW + part * 8]);
+          const int64_t m = m_beg + 32 * i + rr;
+          *reinterpret_cast<u32x4*>(g.out + m * g.ldo + nbase + cb * 32 + part * 8) = v;
+        }
+      }
+    }
+  }
+}
+
+template <int EPI, int BQ, int DT>
+__global__ __launch_bounds__(NK_THREADS) void moe_gemm_nk_kernel(const GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* const sA0 = smem;                           // [2][NK_BM * LDSW]
+  uint16_t* const sE0 = smem + 2 * NK_BM * LDSW;        // [4 waves][NK_EPI_ELEMS]
+  int32_t* const s_mt = reinterpret_cast<int32_t*>(sE0 + 4 * NK_EPI_ELEMS);  // [MAX_E + 1]
+  int32_t* const s_part = s_mt + MAX_E + 1;                                 // [NK_THREADS]
+  const int tid = threadIdx.x;
+  uint16_t* const sE = sE0 + (tid >> 6) * NK_EPI_ELEMS;
+  const int E = g.E;
+  mtile_prefix<NK_THREADS, NK_BM>(g, s_mt, s_part, tid);
+  const int64_t n_mt = s_mt[E];
+  const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + NK_BN - 1) / NK_BN;
+  const int64_t n_tiles = n_mt * n_nt;
+  const int nk = (int)(g.K / BK);
+  // XCD-aware walk, as in moe_gemm_kernel: one contiguous slice of the tile list per die
+  const int64_t nblk = gridDim.x;
+  const int dies = nblk < kXcds ? (int)nblk : kXcds;
+  const int xcd = (int)(blockIdx.x % dies);
+  const int64_t per_xcd = (nblk + dies - 1 - xcd) / dies;
+  const int64_t local_b = blockIdx.x / dies;
+  const int64_t t_beg = n_tiles * xcd / dies, t_end = n_tiles * (xcd + 1) / dies;
+  for (int64_t tile = t_beg + local_b; tile < t_end; tile += per_xcd) {
+    const int64_t mt = tile / n_nt, nt = tile % n_nt;
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_mt[mid] <= mt) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    const int64_t m_beg = g.offsets[e] + (mt - s_mt[e]) * NK_BM;
+    const int64_t m_end = g.offsets[e + 1];
+    const int valid = (int)((m_end - m_beg < NK_BM) ? (m_end - m_beg) : NK_BM);
+    const int nrb = (valid + 31) >> 5;
+    if (nrb > 4) nk_tile<8, EPI, BQ, DT>(g, sA0, sE, tid, e, m_beg, valid, nt, nk);
+    else if (nrb > 2) nk_tile<4, EPI, BQ, DT>(g, sA0, sE, tid, e, m_beg, valid, nt, nk);
+    else nk_tile<2, EPI, BQ, DT>(g, sA0, sE, tid, e, m_beg, valid, nt, nk);
+  }
+}
+
+template <int EPI, int BQ, int DT>
+int launch_nk_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_nk_kernel<EPI, BQ, DT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kNkSmemBytes);
+    (void)hipGetLastError();
+    attr_set = true;
+  }
+  moe_gemm_nk_kernel<EPI, BQ, DT><<<blocks, NK_THREADS, kNkSmemBytes, st>>>(g);
+  return USAF_OK;
+}
+
+template <int EPI>
+int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_total, hipStream_t st,
+                   const char* what) {
+  if (a_rows_total * g.lda >= ((int64_t)1 << 31))
+    return set_error(USAF_ERR_UNSUPPORTED, "%s: activation operand of %lld x %lld elements exceeds 2^31", what,
+                     (long long)a_rows_total, (long long)g.lda);
+  int64_t blocks = (int64_t)device_cu_count();
+  if (blocks > max_tiles) blocks = max_tiles;
+  if (blocks < 1) blocks = 1;
+  const bool dense = g.w16 != nullptr;
+  int rc;
+  if (dt == USAF_BF16)
+    rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
+               : launch_nk_one<EPI, BQ_Q4, USAF_BF16>(g, (unsigned)blocks, st);
+  else if (dt == USAF_F16)
+    rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_F16>(g, (unsigned)blocks, st)
+               : launch_nk_one<EPI, BQ_Q4, USAF_F16>(g, (unsigned)blocks, st);
+  else
+    return set_error(USAF_ERR_INVALID, "%s: dtype must be fp16 or bf16", what);
+  if (rc) return rc;
+  return check_launch(what);
 }
 
 template <int BMODE, int EPI, int BQ, int DT>
@@ -606,12 +1061,12 @@ int launch_gemm(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_tot
   return check_launch(what);
 }
 
-int check_common(const char* what, int64_t S, int64_t E, const void* offsets, const void* wq, const void* ws,
-                 const void* wz, const void* w16) {
+int check_common(const char* what, int64_t S, int64_t E, const void* offsets, const void* wq, const void* wsz,
+                 const void* w16) {
   if (E <= 0 || E > MAX_E) return set_error(USAF_ERR_INVALID, "%s: need 0 < E <= %d", what, MAX_E);
   if (S < 0) return set_error(USAF_ERR_INVALID, "%s: negative slot count", what);
-  if (!offsets || (!w16 && (!wq || !ws || !wz)))
-    return set_error(USAF_ERR_INVALID, "%s: null pointer (offsets, and either q/s/z or the dense weight)", what);
+  if (!offsets || (!w16 && (!wq || !wsz)))
+    return set_error(USAF_ERR_INVALID, "%s: null pointer (offsets, and either codes + scale/zero pairs or the dense weight)", what);
   if (w16 && ((uintptr_t)w16 & 15)) return set_error(USAF_ERR_INVALID, "%s: dense weight must be 16-byte aligned", what);
   if (!w16 && ((uintptr_t)wq & 15)) return set_error(USAF_ERR_INVALID, "%s: codes must be 16-byte aligned", what);
   return USAF_OK;
@@ -624,47 +1079,47 @@ using namespace usaf;
 
 // Forward gate_up + SwiGLU (qwen3moe_dml.py:58-60, per routed slot).
 extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T_rows, int64_t H, const int32_t* token_idx, const int32_t* offsets,
-                                        int64_t S, int64_t E, int64_t I, const int8_t* wq, const uint16_t* ws,
-                                        const uint16_t* wz, const void* w16, int32_t dtype, void* gu, void* act, void* stream) {
-  if (int rc = check_common("moe_gate_up_fwd", S, E, offsets, wq, ws, wz, w16)) return rc;
-  if (H % 128 != 0 || H <= 0 || I % 64 != 0 || I <= 0)
-    return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_fwd: needs H %% 128 == 0 and I %% 64 == 0 (H=%lld, I=%lld)",
+                                        int64_t S, int64_t E, int64_t I, const int8_t* wq, const uint32_t* wsz,
+                                        const void* w16, int32_t dtype, void* gu, void* act, void* stream) {
+  if (int rc = check_common("moe_gate_up_fwd", S, E, offsets, wq, wsz, w16)) return rc;
+  if (H % 128 != 0 || H <= 0 || I % 32 != 0 || I <= 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_fwd: needs H %% 128 == 0 and I %% 32 == 0 (H=%lld, I=%lld)",
                      (long long)H, (long long)I);
   if (S == 0) return clear_error();
   if (!x || !token_idx || !gu || !act) return set_error(USAF_ERR_INVALID, "moe_gate_up_fwd: null pointer");
   GemmArgs g{};
   g.A = (const uint16_t*)x; g.lda = H; g.a_rows = token_idx;
-  g.wq = (const uint8_t*)wq; g.ws = ws; g.wz = wz; g.w16 = (const uint16_t*)w16; g.w_rows = 2 * I; g.w_cols = H;
+  g.wq = (const uint8_t*)wq; g.wsz = wsz; g.w16 = (const uint16_t*)w16; g.w_rows = 2 * I; g.w_cols = H;
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)act; g.ldo = I; g.out2 = (uint16_t*)gu; g.ldo2 = 2 * I;
-  const int64_t max_tiles = (S / BM + E) * (I / 64);
-  return launch_gemm<BMODE_NK, EPI_SWIGLU_FWD>(g, dtype, max_tiles, T_rows, as_stream(stream), "moe_gate_up_fwd");
+  const int64_t max_tiles = (S / NK_BM + E) * ((I + 127) / 128);
+  return launch_gemm_nk<EPI_SWIGLU_FWD>(g, dtype, max_tiles, T_rows, as_stream(stream), "moe_gate_up_fwd");
 }
 
 // Forward down projection (qwen3moe_dml.py:61): y[m] = act[m] @ W_down[e]^T.
 extern "C" int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* offsets, int64_t S, int64_t E,
-                                     int64_t H, const int8_t* wq, const uint16_t* ws, const uint16_t* wz,
+                                     int64_t H, const int8_t* wq, const uint32_t* wsz,
                                      const void* w16, int32_t dtype, void* y, void* stream) {
-  if (int rc = check_common("moe_down_fwd", S, E, offsets, wq, ws, wz, w16)) return rc;
-  if (I % 128 != 0 || I <= 0 || H % BN != 0 || H <= 0)
-    return set_error(USAF_ERR_UNSUPPORTED, "moe_down_fwd: needs I %% 128 == 0 and H %% 128 == 0 (I=%lld, H=%lld)",
+  if (int rc = check_common("moe_down_fwd", S, E, offsets, wq, wsz, w16)) return rc;
+  if (I % 128 != 0 || I <= 0 || H % 64 != 0 || H <= 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_down_fwd: needs I %% 128 == 0 and H %% 64 == 0 (I=%lld, H=%lld)",
                      (long long)I, (long long)H);
   if (S == 0) return clear_error();
   if (!act || !y) return set_error(USAF_ERR_INVALID, "moe_down_fwd: null pointer");
   GemmArgs g{};
   g.A = (const uint16_t*)act; g.lda = I; g.a_rows = nullptr;
-  g.wq = (const uint8_t*)wq; g.ws = ws; g.wz = wz; g.w16 = (const uint16_t*)w16; g.w_rows = H; g.w_cols = I;
+  g.wq = (const uint8_t*)wq; g.wsz = wsz; g.w16 = (const uint16_t*)w16; g.w_rows = H; g.w_cols = I;
   g.N = H; g.K = I; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)y; g.ldo = H;
-  const int64_t max_tiles = (S / BM + E) * (H / BN);
-  return launch_gemm<BMODE_NK, EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_fwd");
+  const int64_t max_tiles = (S / NK_BM + E) * ((H + NK_BN - 1) / NK_BN);
+  return launch_gemm_nk<EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_fwd");
 }
 
 // Backward through the down projection and SwiGLU: dgu[m] from dcur[m] @ W_down[e].
 extern "C" int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S,
-                                     int64_t E, int64_t I, const int8_t* wq, const uint16_t* ws, const uint16_t* wz,
+                                     int64_t E, int64_t I, const int8_t* wq, const uint32_t* wsz,
                                      const void* w16, int32_t dtype, void* dgu, void* stream) {
-  if (int rc = check_common("moe_down_bwd", S, E, offsets, wq, ws, wz, w16)) return rc;
+  if (int rc = check_common("moe_down_bwd", S, E, offsets, wq, wsz, w16)) return rc;
   if (I % 128 != 0 || I <= 0 || H % BK != 0 || H <= 0)
     return set_error(USAF_ERR_UNSUPPORTED, "moe_down_bwd: needs I %% 128 == 0 and H %% 64 == 0 (I=%lld, H=%lld)",
                      (long long)I, (long long)H);
@@ -672,7 +1127,7 @@ extern "C" int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu
   if (!dcur || !gu || !dgu) return set_error(USAF_ERR_INVALID, "moe_down_bwd: null pointer");
   GemmArgs g{};
   g.A = (const uint16_t*)dcur; g.lda = H; g.a_rows = nullptr;
-  g.wq = (const uint8_t*)wq; g.ws = ws; g.wz = wz; g.w16 = (const uint16_t*)w16; g.w_rows = H; g.w_cols = I;
+  g.wq = (const uint8_t*)wq; g.wsz = wsz; g.w16 = (const uint16_t*)w16; g.w_rows = H; g.w_cols = I;
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)dgu; g.ldo = 2 * I; g.aux = (const uint16_t*)gu; g.ld_aux = 2 * I;
   const int64_t max_tiles = (S / BM + E) * (I / BN);
@@ -681,9 +1136,9 @@ extern "C" int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu
 
 // Backward grad-input through gate_up: dx_slots[m] = dgu[m] @ W_gate_up[e].
 extern "C" int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E,
-                                        int64_t H, const int8_t* wq, const uint16_t* ws, const uint16_t* wz,
+                                        int64_t H, const int8_t* wq, const uint32_t* wsz,
                                         const void* w16, int32_t dtype, void* dx_slots, void* stream) {
-  if (int rc = check_common("moe_gate_up_bwd", S, E, offsets, wq, ws, wz, w16)) return rc;
+  if (int rc = check_common("moe_gate_up_bwd", S, E, offsets, wq, wsz, w16)) return rc;
   if (H % 128 != 0 || H <= 0 || (2 * I) % BK != 0 || I <= 0)
     return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_bwd: needs H %% 128 == 0 and 2I %% 64 == 0 (H=%lld, I=%lld)",
                      (long long)H, (long long)I);
@@ -691,7 +1146,7 @@ extern "C" int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_
   if (!dgu || !dx_slots) return set_error(USAF_ERR_INVALID, "moe_gate_up_bwd: null pointer");
   GemmArgs g{};
   g.A = (const uint16_t*)dgu; g.lda = 2 * I; g.a_rows = nullptr;
-  g.wq = (const uint8_t*)wq; g.ws = ws; g.wz = wz; g.w16 = (const uint16_t*)w16; g.w_rows = 2 * I; g.w_cols = H;
+  g.wq = (const uint8_t*)wq; g.wsz = wsz; g.w16 = (const uint16_t*)w16; g.w_rows = 2 * I; g.w_cols = H;
   g.N = H; g.K = 2 * I; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)dx_slots; g.ldo = H;
   const int64_t max_tiles = (S / BM + E) * (H / BN);

@@ -10,7 +10,7 @@ and an fp32 combine over experts in ascending expert order.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Any, Optional
 
 import torch
@@ -30,6 +30,7 @@ class Q4Tensor:
     z: torch.Tensor        # fp16 [groups]
     shape: torch.Size
     group_size: int = 128
+    _sz: Optional[torch.Tensor] = field(default=None, repr=False, compare=False)
 
     @classmethod
     def from_entry(cls, entry: Any, device=None, group_size: int = 128) -> "Q4Tensor":
@@ -73,6 +74,16 @@ class Q4Tensor:
         from .quantization import dequantize_4bit
         return dequantize_4bit(self.q, self.s, self.z, self.shape, self.group_size, out_dtype=out_dtype, out=out)
 
+    def scale_zero(self) -> torch.Tensor:
+        """int32 [groups]: scale bits | zero bits << 16, the form the fused GEMMs
+        read (built once, on the tensor's device)."""
+        if self._sz is None or self._sz.device != self.q.device:
+            sz = torch.empty(self.s.numel(), dtype=torch.int32, device=self.q.device)
+            N.call("usaf_hip_pack_scale_zero", self.s.data_ptr(), self.z.data_ptr(), self.s.numel(), sz.data_ptr(),
+                   N.stream_ptr(self.q.device))
+            self._sz = sz
+        return self._sz
+
     def fused_ok(self) -> bool:
         """True when the layout is the one the fused GEMMs read directly:
         group size 128 along whole rows (last dim % 128 == 0)."""
@@ -105,12 +116,12 @@ class ExpertWeights:
                 raise NotImplementedError(
                     f"fused 4-bit GEMM needs group_size 128 along whole rows (shape {tuple(w.shape)}, "
                     f"group_size {w.group_size})")
-            return w.q.data_ptr(), w.s.data_ptr(), w.z.data_ptr(), None
+            return w.q.data_ptr(), w.scale_zero().data_ptr(), None
         if w.dtype != dtype:
             raise TypeError(f"dense expert weight dtype {w.dtype} must match the activations ({dtype})")
         if not w.is_contiguous():
             raise ValueError("dense expert weights must be contiguous")
-        return None, None, None, w.data_ptr()
+        return None, None, w.data_ptr()
 
 
 # ---------------------------------------------------------------------------
@@ -244,11 +255,11 @@ class RoutedExpertsFn(torch.autograd.Function):
         act = torch.empty(S, I, dtype=dt, device=dev)
         y = torch.empty(S, H, dtype=dt, device=dev)
         if S > 0:
-            q, s, z, w16 = ew._ptrs("gate_up", dt)
+            q, sz, w16 = ew._ptrs("gate_up", dt)
             _gemm_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
-                       S, E, I, q, s, z, w16, code, gu.data_ptr(), act.data_ptr(), st)
-            q, s, z, w16 = ew._ptrs("down", dt)
-            _gemm_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, s, z, w16,
+                       S, E, I, q, sz, w16, code, gu.data_ptr(), act.data_ptr(), st)
+            q, sz, w16 = ew._ptrs("down", dt)
+            _gemm_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
                        code, y.data_ptr(), st)
         out = combine(y, weights, b.pair_slot, dt)
         ctx.ew = ew
@@ -276,14 +287,14 @@ class RoutedExpertsFn(torch.autograd.Function):
         N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
                b.slot_w.data_ptr(), b.offsets.data_ptr(), S, E, H, code, dcur.data_ptr(), dweights.data_ptr(), st)
         dgu = torch.empty(S, 2 * I, dtype=dt, device=dev)
-        q, s, z, w16 = ew._ptrs("down", dt)
+        q, sz, w16 = ew._ptrs("down", dt)
         _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
-                   q, s, z, w16, code, dgu.data_ptr(), st)
+                   q, sz, w16, code, dgu.data_ptr(), st)
         if capture is not None:
             _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt)
         dx_slots = torch.empty(S, H, dtype=dt, device=dev)
-        q, s, z, w16 = ew._ptrs("gate_up", dt)
-        _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, s, z, w16,
+        q, sz, w16 = ew._ptrs("gate_up", dt)
+        _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
                    code, dx_slots.data_ptr(), st)
         if capture is not None:
             _capture(capture, "gate_up_proj", dgu, hs, b.token_idx, b, (E, 2 * I, H), dt)
