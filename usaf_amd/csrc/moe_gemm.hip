@@ -149,6 +149,32 @@ __device__ __forceinline__ float bits_to_f32(uint16_t b) {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// Epilogue conversions on pairs: fp32 -> two 16-bit values of DT (round to
+// nearest even, one v_cvt_pk_bf16_f32 for bf16) packed low/high, and back.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (DT == USAF_BF16) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  } else {
+    const f16x2 h = {(f16)a, (f16)b};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+template <int DT>
+__device__ __forceinline__ f32x2 unpack2(uint32_t w) {
+  if constexpr (DT == USAF_BF16) return f32x2{__uint_as_float(w << 16), __uint_as_float(w & 0xFFFF0000u)};
+  else {
+    const f16x2 h = __builtin_bit_cast(f16x2, w);
+    return f32x2{(float)h.x, (float)h.y};
+  }
+}
+// silu(x) = x / (1 + e^-x) with the hardware exp2 and reciprocal (about 1 ulp
+// of fp32 each, far below the 16-bit rounding that follows)
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
 template <int DT>
 __device__ __forceinline__ f32x16 mfma32(const u32x4 a, const u32x4 b, f32x16 c) {
   if constexpr (DT == USAF_BF16)
@@ -717,8 +743,14 @@ __device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16
   const int a_lds = (tid >> 3) * LDSW + (tid & 7) * 8;
 
   using std::integral_constant;
-  constexpr int R = 4 * NRB;     // regions per k-step: (sub-step j = r / NRB, row block i = r % NRB)
-  constexpr int PF = 4;          // A-fragment prefetch distance (regions)
+  // Regions per k-step: each covers sub-step j and G consecutive row blocks
+  // (2G MFMAs); with G = 2 a region also holds two weight pairs whose
+  // dependent dequant chains interleave instead of stalling on each other.
+  constexpr int G = NRB >= 2 ? 2 : 1;
+  constexpr int RPJ = NRB / G;   // regions per sub-step
+  constexpr int R = 4 * RPJ;     // regions per k-step
+  constexpr int NF = 4 * NRB;    // A fragments per k-step, f = j * NRB + i
+  constexpr int PF = 4 * G;      // A-fragment prefetch distance (fragments)
   constexpr int NPAIR = (BQ == BQ_Q4) ? 32 : 0;  // weight pairs per k-step per lane
   constexpr int PPR = (NPAIR + R - 1) / R;       // pairs dequantized per region
   const int frag = l32 * LDSW + 32 * half;  // lane's A fragment: row l32 of a row block, k = 32 half + 8 j
@@ -775,17 +807,21 @@ __device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16
   auto mma = [&](auto BSc, int kt) {
     constexpr int BS = decltype(BSc)::value;
     const uint16_t* sA = sA0 + (kt & 1) * (NK_BM * LDSW);
-    u32x4 af[R];
+    u32x4 af[NF];
 #pragma unroll
-    for (int r = 0; r < PF && r < R; ++r)
-      af[r] = *reinterpret_cast<const u32x4*>(&sA[(r % NRB) * 32 * LDSW + frag + 8 * (r / NRB)]);
+    for (int f = 0; f < PF && f < NF; ++f)
+      af[f] = *reinterpret_cast<const u32x4*>(&sA[(f % NRB) * 32 * LDSW + frag + 8 * (f / NRB)]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int j = r / NRB, i = r % NRB;
-      if (r + PF < R)
-        af[r + PF] = *reinterpret_cast<const u32x4*>(&sA[((r + PF) % NRB) * 32 * LDSW + frag + 8 * ((r + PF) / NRB)]);
-      acc[i][0] = mfma32<DT>(af[r], bfs[BS][0][j], acc[i][0]);
-      acc[i][1] = mfma32<DT>(af[r], bfs[BS][1][j], acc[i][1]);
+      const int j = r / RPJ;
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        const int f = j * NRB + (r % RPJ) * G + gg, i = f % NRB;
+        if (f + PF < NF)
+          af[f + PF] = *reinterpret_cast<const u32x4*>(&sA[((f + PF) % NRB) * 32 * LDSW + frag + 8 * ((f + PF) / NRB)]);
+        acc[i][0] = mfma32<DT>(af[f], bfs[BS][0][j], acc[i][0]);
+        acc[i][1] = mfma32<DT>(af[f], bfs[BS][1][j], acc[i][1]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -802,20 +838,24 @@ __device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16
     constexpr int BS = decltype(BSc)::value, CS = decltype(CSc)::value;
     const uint16_t* sA = sA0 + (kt & 1) * (NK_BM * LDSW);
     uint16_t* sAn = sA0 + ((kt + 1) & 1) * (NK_BM * LDSW);
-    u32x4 af[R];
+    u32x4 af[NF];
     f16x2 s2[2], z2[2];
 #pragma unroll
-    for (int r = 0; r < PF && r < R; ++r)
-      af[r] = *reinterpret_cast<const u32x4*>(&sA[(r % NRB) * 32 * LDSW + frag + 8 * (r / NRB)]);
+    for (int f = 0; f < PF && f < NF; ++f)
+      af[f] = *reinterpret_cast<const u32x4*>(&sA[(f % NRB) * 32 * LDSW + frag + 8 * (f / NRB)]);
     if constexpr (BQ == BQ_Q4) load_codes(integral_constant<int, (CS + 2) % 3>{}, kt + 3);
     else load_dense(integral_constant<int, BS ^ 1>{}, kt + 1);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int j = r / NRB, i = r % NRB;
-      if (r + PF < R)
-        af[r + PF] = *reinterpret_cast<const u32x4*>(&sA[((r + PF) % NRB) * 32 * LDSW + frag + 8 * ((r + PF) / NRB)]);
-      acc[i][0] = mfma32<DT>(af[r], bfs[BS][0][j], acc[i][0]);
-      acc[i][1] = mfma32<DT>(af[r], bfs[BS][1][j], acc[i][1]);
+      const int j = r / RPJ;
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        const int f = j * NRB + (r % RPJ) * G + gg, i = f % NRB;
+        if (f + PF < NF)
+          af[f + PF] = *reinterpret_cast<const u32x4*>(&sA[((f + PF) % NRB) * 32 * LDSW + frag + 8 * ((f + PF) / NRB)]);
+        acc[i][0] = mfma32<DT>(af[f], bfs[BS][0][j], acc[i][0]);
+        acc[i][1] = mfma32<DT>(af[f], bfs[BS][1][j], acc[i][1]);
+      }
       if constexpr (BQ == BQ_Q4) {
 #pragma unroll
         for (int pp = 0; pp < PPR; ++pp) {
@@ -830,10 +870,16 @@ __device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16
           }
         }
       }
-      if ((r & 1) == 0 && (r >> 1) < NRB)  // stage chunk r/2 of k-step kt + 1
-        *reinterpret_cast<u32x4*>(&sAn[a_lds + 32 * (r >> 1) * LDSW]) = ra[r >> 1];
-      if ((r & 1) == 1 && (r >> 1) < NRB)  // then refill it with k-step kt + 2
-        ra[r >> 1] = *reinterpret_cast<const u32x4*>(g.A + a_off[r >> 1] + (kt + 2) * BK);
+      // stage the A chunks of k-step kt + 1 and refill them with kt + 2, CPR chunks per region
+      constexpr int CPR = (NRB + R - 1) / R;
+#pragma unroll
+      for (int cc = 0; cc < CPR; ++cc) {
+        const int c = r * CPR + cc;
+        if (c < NRB) {
+          *reinterpret_cast<u32x4*>(&sAn[a_lds + 32 * c * LDSW]) = ra[c];
+          ra[c] = *reinterpret_cast<const u32x4*>(g.A + a_off[c] + (kt + 2) * BK);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     lds_barrier();
@@ -901,16 +947,21 @@ __device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16
     if (i >= nrb) continue;
     const int rows = valid - 32 * i;  // valid rows in this row block (may exceed 32)
     if constexpr (EPI == EPI_SWIGLU_FWD) {
+      // gate, up rounded to DT; act = DT(DT(silu(gate)) * up), two rows at a time
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < 16; r += 2) {
         const int row = 8 * (r >> 2) + 4 * half + (r & 3);
-        const uint16_t gb = round_bits<DT>(acc[i][0][r]);
-        const uint16_t ub = round_bits<DT>(acc[i][1][r]);
-        const float sg = round_to<DT>(silu_f(bits_to_f32<DT>(gb)));
-        const uint16_t ab = round_bits<DT>(sg * bits_to_f32<DT>(ub));
-        sE[row * NK_EPW + l32] = gb;
-        sE[32 * NK_EPW + row * NK_EPW + l32] = ub;
-        sE[64 * NK_EPW + row * NK_EPW + l32] = ab;
+        const uint32_t gb = pack2<DT>(acc[i][0][r], acc[i][0][r + 1]);
+        const uint32_t ub = pack2<DT>(acc[i][1][r], acc[i][1][r + 1]);
+        const f32x2 gf = unpack2<DT>(gb), uf = unpack2<DT>(ub);
+        const f32x2 sf = unpack2<DT>(pack2<DT>(silu_fast(gf.x), silu_fast(gf.y)));
+        const uint32_t ab = pack2<DT>(sf.x * uf.x, sf.y * uf.y);
+        sE[row * NK_EPW + l32] = (uint16_t)gb;
+        sE[(row + 1) * NK_EPW + l32] = (uint16_t)(gb >> 16);
+        sE[32 * NK_EPW + row * NK_EPW + l32] = (uint16_t)ub;
+        sE[32 * NK_EPW + (row + 1) * NK_EPW + l32] = (uint16_t)(ub >> 16);
+        sE[64 * NK_EPW + row * NK_EPW + l32] = (uint16_t)ab;
+        sE[64 * NK_EPW + (row + 1) * NK_EPW + l32] = (uint16_t)(ab >> 16);
       }
 #pragma unroll
       for (int q = 0; q < 6; ++q) {
@@ -928,9 +979,11 @@ __device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < 16; r += 2) {
           const int row = 8 * (r >> 2) + 4 * half + (r & 3);
-          sE[cb * 32 * NK_EPW + row * NK_EPW + l32] = round_bits<DT>(acc[i][cb][r]);
+          const uint32_t v = pack2<DT>(acc[i][cb][r], acc[i][cb][r + 1]);
+          sE[cb * 32 * NK_EPW + row * NK_EPW + l32] = (uint16_t)v;
+          sE[cb * 32 * NK_EPW + (row + 1) * NK_EPW + l32] = (uint16_t)(v >> 16);
         }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
