@@ -199,13 +199,14 @@ int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const int32_t* rows
  * (usaf/qwen3moe_dml.py:44-56, usaf/moe_loader.py:564-578):
  *   compact[pos(p)] += fp32(dtype( sum_{s in expert e} rowT[o, s] * colT[i, s] ))
  * for each active position p < n_pos of a [E, R, C] weight, given as
- * row_idx[p] = e * R + o and col_idx[p] = i (int32; out-of-range entries are
+ * row_code[p] = e << 21 | o and col_idx[p] = i (int32; out-of-range entries are
  * skipped) and pos_map[p] (int64 compact index of entry p; NULL = identity; each
  * compact index at most once).  rowT [R, ldT] and colT [C, ldT] are slot-major
  * 16-bit operands (dtype), 16-byte aligned, ldT a multiple of 8 and >= offsets[E].
+ * E <= 1024, R < 2^21.
  */
 int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t ldT, const int32_t* offsets, int64_t E,
-                          int64_t R, int64_t C, int64_t n_pos, const int32_t* row_idx, const int32_t* col_idx,
+                          int64_t R, int64_t C, int64_t n_pos, const int32_t* row_code, const int32_t* col_idx,
                           const int64_t* pos_map, int32_t dtype, float* compact, void* stream);
 
 /*

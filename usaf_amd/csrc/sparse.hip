@@ -69,58 +69,62 @@ __global__ __launch_bounds__(256) void gather_transpose_kernel(const uint16_t* _
   }
 }
 
+// Products of two 16-bit pairs accumulated in fp32 (v_dot2_f32_bf16 / _f16).
 template <int DT>
-__device__ __forceinline__ float lo_f32(uint32_t w) {
-  if constexpr (DT == USAF_BF16) return __uint_as_float(w << 16);
-  else return f16_bits_to_f32((uint16_t)(w & 0xffffu));
-}
-template <int DT>
-__device__ __forceinline__ float hi_f32(uint32_t w) {
-  if constexpr (DT == USAF_BF16) return __uint_as_float(w & 0xffff0000u);
-  else return f16_bits_to_f32((uint16_t)(w >> 16));
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == USAF_BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
 }
 
-// Sixteen lanes per active position p = (row r = e * R + o, column i):
+// Sixteen lanes per active position p: row code rcode[p] = e << 21 | o (expert
+// e, weight row o < 2^21), column col_idx[p] = i:
 //   compact[pos(p)] += fp32(DT( sum_{s0 <= s < s1} rowT[o, s] * colT[i, s] ))
 // over expert e's slots [s0, s1) = [offsets[e], offsets[e + 1]).  Lane l of a
 // group reads slots [b + 8l, b + 8l + 8) of each 128-slot window starting at
-// b = s0 rounded down to 8, as one 16-byte load per operand; slots outside
-// [s0, s1) belong to neighbouring experts (or the row padding) and are
-// selected out.  Positions of one weight row are adjacent, so the groups of a
-// wave mostly read the same rowT row.  Out-of-range rows or columns are
-// skipped.
+// b = s0 rounded down to 8, as one 16-byte load per operand, and accumulates
+// them with v_dot2 in fp32; elements outside [s0, s1) (neighbouring experts,
+// row padding) are masked to zero in both operands.  Positions of one weight
+// row are adjacent, so the groups of a wave mostly read the same rowT line.
+// Rows >= R, experts >= E and columns >= C are skipped.
 template <int DT>
 __global__ __launch_bounds__(256) void sddmm_kernel(const uint16_t* __restrict__ rowT, const uint16_t* __restrict__ colT,
                                                     int64_t ldT, const int32_t* __restrict__ offsets, int32_t E,
                                                     int32_t R, int32_t C, int64_t n_pos,
-                                                    const int32_t* __restrict__ row_idx,
+                                                    const int32_t* __restrict__ rcode,
                                                     const int32_t* __restrict__ col_idx,
                                                     const int64_t* __restrict__ pos_map, float* __restrict__ compact) {
   const int gl = threadIdx.x & 15;
   const int64_t n_grp = ((int64_t)gridDim.x * blockDim.x) >> 4;
-  const uint32_t n_rows = (uint32_t)E * (uint32_t)R;
   for (int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; p < n_pos; p += n_grp) {
-    const uint32_t r = (uint32_t)row_idx[p];
+    const uint32_t code = (uint32_t)rcode[p];
     const uint32_t i = (uint32_t)col_idx[p];
-    if (r >= n_rows || i >= (uint32_t)C) continue;
-    const uint32_t e = r / (uint32_t)R;
-    const uint32_t o = r - e * (uint32_t)R;
+    const uint32_t e = code >> 21, o = code & 0x1FFFFFu;
+    if (e >= (uint32_t)E || o >= (uint32_t)R || i >= (uint32_t)C) continue;
     int s0 = offsets[e], s1 = offsets[e + 1];
     s0 = s0 < 0 ? 0 : s0;
     s1 = s1 > (int)ldT ? (int)ldT : s1;
     const uint16_t* rv = rowT + (int64_t)o * ldT;
     const uint16_t* cv = colT + (int64_t)i * ldT;
+    const unsigned span = (unsigned)(s1 - s0);
     float acc = 0.f;
-    for (int s = (s0 & ~7) + 8 * gl; s < s1; s += 128) {
-      const uint4 a = *reinterpret_cast<const uint4*>(rv + s);
-      const uint4 b = *reinterpret_cast<const uint4*>(cv + s);
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+    for (int w = (s0 & ~7) + 8 * gl; w < s1; w += 128) {
+      const uint4 a = *reinterpret_cast<const uint4*>(rv + w);
+      const uint4 c = *reinterpret_cast<const uint4*>(cv + w);
+      if ((unsigned)(w - s0) < span && (unsigned)(w + 7 - s0) < span) {  // interior: no masking
+        acc = dot2<DT>(a.x, c.x, acc);
+        acc = dot2<DT>(a.y, c.y, acc);
+        acc = dot2<DT>(a.z, c.z, acc);
+        acc = dot2<DT>(a.w, c.w, acc);
+      } else {
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, cw[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float pl = lo_f32<DT>(aw[j]) * lo_f32<DT>(bw[j]);
-        const float ph = hi_f32<DT>(aw[j]) * hi_f32<DT>(bw[j]);
-        acc += ((unsigned)(s + 2 * j - s0) < (unsigned)(s1 - s0)) ? pl : 0.f;
-        acc += ((unsigned)(s + 2 * j + 1 - s0) < (unsigned)(s1 - s0)) ? ph : 0.f;
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t m = (((unsigned)(w + 2 * q - s0) < span) ? 0x0000FFFFu : 0u) |
+                             (((unsigned)(w + 2 * q + 1 - s0) < span) ? 0xFFFF0000u : 0u);
+          acc = dot2<DT>(aw[q] & m, cw[q] & m, acc);
+        }
       }
     }
 #pragma unroll
@@ -217,15 +221,15 @@ extern "C" int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const in
 }
 
 extern "C" int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t ldT, const int32_t* offsets,
-                                     int64_t E, int64_t R, int64_t C, int64_t n_pos, const int32_t* row_idx,
+                                     int64_t E, int64_t R, int64_t C, int64_t n_pos, const int32_t* row_code,
                                      const int32_t* col_idx, const int64_t* pos_map, int32_t dtype, float* compact,
                                      void* stream) {
   if (E <= 0 || R <= 0 || C <= 0 || n_pos < 0 || ldT < 0) return set_error(USAF_ERR_INVALID, "sddmm_masked: bad sizes");
-  if (E * R > 0x7fffffff || C > 0x7fffffff || ldT > 0x7fffffff)
-    return set_error(USAF_ERR_INVALID, "sddmm_masked: E*R, C and ldT must fit in int32");
+  if (E > 1024 || R >= (1 << 21) || C > 0x7fffffff || ldT > 0x7fffffff)
+    return set_error(USAF_ERR_INVALID, "sddmm_masked: needs E <= 1024, R < 2^21, C and ldT < 2^31");
   if (ldT % 8 != 0) return set_error(USAF_ERR_INVALID, "sddmm_masked: ldT must be a multiple of 8");
   if (n_pos == 0) return clear_error();
-  if (!rowT || !colT || !offsets || !row_idx || !col_idx || !compact)
+  if (!rowT || !colT || !offsets || !row_code || !col_idx || !compact)
     return set_error(USAF_ERR_INVALID, "sddmm_masked: null pointer");
   if (((uintptr_t)rowT & 15) || ((uintptr_t)colT & 15))
     return set_error(USAF_ERR_INVALID, "sddmm_masked: rowT and colT must be 16-byte aligned");
@@ -237,11 +241,11 @@ extern "C" int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t
   if (dtype == USAF_BF16)
     sddmm_kernel<USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)rowT, (const uint16_t*)colT, ldT,
                                                               offsets, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
-                                                              row_idx, col_idx, pos_map, compact);
+                                                              row_code, col_idx, pos_map, compact);
   else
     sddmm_kernel<USAF_F16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)rowT, (const uint16_t*)colT, ldT,
                                                              offsets, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
-                                                             row_idx, col_idx, pos_map, compact);
+                                                             row_code, col_idx, pos_map, compact);
   return check_launch("sddmm_masked");
 }
 

@@ -356,8 +356,11 @@ class SparseGradStore:
                 if int(sidx[0]) < 0 or int(sidx[-1]) >= E * R * C:
                     raise IndexError(f"{name}: active index out of range for shape {shape}")
                 row_ptr[1:] = torch.cumsum(torch.bincount(rows, minlength=E * R), 0)
-            self._csr[name] = (row_ptr, rows.to(torch.int32).contiguous(), cols.contiguous(),
-                               None if identity else order.contiguous(), E, R, C)
+            if E > 1024 or R >= 2 ** 21:
+                raise ValueError(f"{name}: the sampled-gradient kernel needs E <= 1024 and rows < 2^21, shape {shape}")
+            e_of = torch.div(rows, R, rounding_mode="floor")
+            row_code = ((e_of << 21) | (rows - e_of * R)).to(torch.int32).contiguous()  # e << 21 | o
+            self._csr[name] = (row_ptr, row_code, cols.contiguous(), None if identity else order.contiguous(), E, R, C)
 
     def zero_(self) -> None:
         for v in self.compact.values():
@@ -369,7 +372,7 @@ class SparseGradStore:
         csr = self._csr.get(full_name)
         if csr is None:
             return
-        _, rows, cols, pos_map, E, R, C = csr
+        _, row_code, cols, pos_map, E, R, C = csr
         if rowT.shape[0] != R or colT.shape[0] != C or rowT.shape[1] != colT.shape[1]:
             raise ValueError(f"{full_name}: operands {tuple(rowT.shape)} / {tuple(colT.shape)} do not match "
                              f"the weight rows {R} x cols {C}")
@@ -378,7 +381,7 @@ class SparseGradStore:
             raise ValueError("slot-major operands need unit column stride and one row stride, a multiple of 8 "
                              "(use usaf_amd.moe.slot_major)")
         N.call("usaf_hip_sddmm_masked", rowT.data_ptr(), colT.data_ptr(), ldT, offsets.data_ptr(), E, R, C,
-               cols.numel(), rows.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
+               cols.numel(), row_code.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
                self.compact[full_name].data_ptr(), N.stream_ptr(self.device))
 
     def add(self, full_name: str, ei: int, g: torch.Tensor) -> None:
