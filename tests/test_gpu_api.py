@@ -181,3 +181,74 @@ def test_quantized_streaming_fused_block(gpu_device):
     torch.cuda.synchronize()
     assert rel_err(out, ref) <= 1e-2
     assert getattr(block.experts, "_usaf_q4", None) is None   # detached again by the post-hook
+
+
+def _tiny_olmoe(E=8, H=256, I=128, k=2, seed=0, norm=False):
+    from transformers import OlmoeConfig
+    from transformers.models.olmoe.modeling_olmoe import OlmoeSparseMoeBlock
+    cfg = OlmoeConfig(hidden_size=H, intermediate_size=I, num_experts=E, num_experts_per_tok=k,
+                      norm_topk_prob=norm, hidden_act="silu", num_hidden_layers=1, num_attention_heads=4,
+                      num_key_value_heads=4, vocab_size=64)
+    block = OlmoeSparseMoeBlock(cfg)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        block.experts.gate_up_proj.copy_(torch.randn(E, 2 * I, H, generator=g) * 0.02)
+        block.experts.down_proj.copy_(torch.randn(E, H, I, generator=g) * 0.02)
+        block.gate.weight.copy_(torch.randn(E, H, generator=g) / H ** 0.5)
+    return block
+
+
+def test_patched_olmoe_block_fp16_with_dense_weight_grads(gpu_device):
+    # the reference runs this variant's expert math in fp32 (olmoe_dml.py:10-33): the oracle
+    # is its fp32 dense-masked loop with autograd; the GPU computes it in bf16 on MFMA
+    _say("patch_olmoe_for_dml: fp16 block, fp32 oracle, dense expert-weight grads")
+    from usaf_amd.olmoe_dml import patch_olmoe_for_dml
+    patch_olmoe_for_dml()
+    block = _tiny_olmoe(seed=7)
+    block.gate.half()  # the router in the activations' dtype, fp32 expert Parameters
+    hs = torch.randn(2, 64, 256, generator=torch.Generator().manual_seed(8)).half()
+    dout = torch.randn(2, 64, 256, generator=torch.Generator().manual_seed(9)).half()
+    wg = block.experts.gate_up_proj.detach().clone().requires_grad_(True)
+    wd = block.experts.down_proj.detach().clone().requires_grad_(True)
+    x = hs.float().reshape(-1, 256)
+    logits = torch.nn.functional.linear(hs.reshape(-1, 256), block.gate.weight.detach()).float()
+    w, _, _ = M.route(logits, 2, False, torch.float16)
+    w = w.float()
+    ref = M.experts_dense_masked(x, w, wg, wd)
+    ref.backward(dout.float().reshape(-1, 256))
+    block = block.to(gpu_device)
+    out = block(hs.to(gpu_device))
+    out.backward(dout.to(gpu_device))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16 and out.shape == hs.shape
+    assert rel_err(out.reshape(-1, 256), ref) <= 1e-2
+    assert block.experts.gate_up_proj.grad.dtype == torch.float32
+    assert rel_err(block.experts.gate_up_proj.grad, wg.grad) <= 1e-2
+    assert rel_err(block.experts.down_proj.grad, wd.grad) <= 1e-2
+
+
+def test_olmoe_streaming_capture(gpu_device):
+    _say("olmoe setup_streaming + apply_captured_expert_grads")
+    from usaf_amd.olmoe_dml import patch_olmoe_for_dml
+    from usaf_amd.olmoe_streaming import apply_captured_expert_grads, setup_streaming
+    patch_olmoe_for_dml()
+    block = _tiny_olmoe(seed=11)
+    layer = nn.Module()
+    layer.mlp = block
+    model = nn.Module()
+    model.model = nn.Module()
+    model.model.layers = nn.ModuleList([layer])
+    setup_streaming(model, gpu_device, verbose=False)
+    assert all(p.device.type == "cuda" for p in model.parameters())
+    hs = torch.randn(1, 32, 256, generator=torch.Generator().manual_seed(12)).to(gpu_device)
+    out = model.model.layers[0].mlp(hs)
+    out.sum().backward()
+    torch.cuda.synchronize()
+    names = set(model._expert_grads)
+    assert names == {"model.layers.0.mlp.experts.gate_up_proj", "model.layers.0.mlp.experts.down_proj"}
+    g_before = model._expert_grads["model.layers.0.mlp.experts.down_proj"].clone()
+    assert apply_captured_expert_grads(model, scale=0.5) == 2
+    assert model._expert_grads == {}
+    p = dict(model.named_parameters())["model.layers.0.mlp.experts.down_proj"]
+    assert torch.allclose(p.grad, g_before * 0.5)
+    assert model._stream_state["max"] == 1 and model._stream_state["resident"] == 0

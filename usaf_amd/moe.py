@@ -11,7 +11,7 @@ and an fp32 combine over experts in ascending expert order.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Any, Optional
+from typing import Any, Optional, Tuple
 
 import torch
 
@@ -235,7 +235,10 @@ class RoutedExpertsFn(torch.autograd.Function):
     """out = sum_e w[:, e] * down_e(silu(gate_e(x)) * up_e(x)) over routed pairs."""
 
     @staticmethod
-    def forward(ctx, hs: torch.Tensor, weights: torch.Tensor, ew: ExpertWeights, capture):
+    def forward(ctx, hs: torch.Tensor, weights: torch.Tensor, ew: ExpertWeights, capture,
+                w_gate_up: Optional[torch.Tensor] = None, w_down: Optional[torch.Tensor] = None):
+        # w_gate_up / w_down: the dense expert Parameters the kernels' weights were
+        # taken from, passed only so that autograd delivers their gradients
         dt = hs.dtype
         if dt not in (torch.float16, torch.bfloat16):
             raise TypeError(f"activations must be fp16 or bf16, got {dt}")
@@ -265,6 +268,7 @@ class RoutedExpertsFn(torch.autograd.Function):
         ctx.ew = ew
         ctx.capture = capture
         ctx.b = b
+        ctx.wdt = (None if w_gate_up is None else w_gate_up.dtype, None if w_down is None else w_down.dtype)
         ctx.save_for_backward(hs, gu, act, y)
         return out
 
@@ -281,8 +285,11 @@ class RoutedExpertsFn(torch.autograd.Function):
         st = N.stream_ptr(dev)
         code = N.dtype_code(dt)
         dweights = torch.zeros(T, E, dtype=dt, device=dev)
+        want_gu, want_dn = ctx.needs_input_grad[4], ctx.needs_input_grad[5]
+        d_wgu = torch.zeros(E, 2 * I, H, dtype=ctx.wdt[0], device=dev) if want_gu else None
+        d_wdn = torch.zeros(E, H, I, dtype=ctx.wdt[1], device=dev) if want_dn else None
         if S == 0:
-            return torch.zeros_like(hs), dweights, None, None
+            return torch.zeros_like(hs), dweights, None, None, d_wgu, d_wdn
         dcur = torch.empty(S, H, dtype=dt, device=dev)
         N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
                b.slot_w.data_ptr(), b.offsets.data_ptr(), S, E, H, code, dcur.data_ptr(), dweights.data_ptr(), st)
@@ -292,14 +299,32 @@ class RoutedExpertsFn(torch.autograd.Function):
                    q, sz, w16, code, dgu.data_ptr(), st)
         if capture is not None:
             _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt)
+        if want_dn:
+            _dense_weight_grad(d_wdn, dcur, act, None, b)
         dx_slots = torch.empty(S, H, dtype=dt, device=dev)
         q, sz, w16 = ew._ptrs("gate_up", dt)
         _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
                    code, dx_slots.data_ptr(), st)
         if capture is not None:
             _capture(capture, "gate_up_proj", dgu, hs, b.token_idx, b, (E, 2 * I, H), dt)
+        if want_gu:
+            _dense_weight_grad(d_wgu, dgu, hs, b.token_idx, b)
         dhs = combine(dx_slots, None, b.pair_slot, dt)
-        return dhs, dweights, None, None
+        return dhs, dweights, None, None, d_wgu, d_wdn
+
+
+def _dense_weight_grad(out: torch.Tensor, dy: torch.Tensor, x: torch.Tensor, x_rows: Optional[torch.Tensor],
+                       b: "Buckets") -> None:
+    """out[e] = dy_e^T @ x_e for every expert with slots (fp32 products, stored in
+    out's dtype): the dense expert-weight gradient autograd gives the reference's
+    trainable experts (olmoe_dml.py:22-31, olmoe_streaming.py:91-97)."""
+    offs = b.offsets.tolist()
+    for ei in range(len(offs) - 1):
+        s0, s1 = offs[ei], offs[ei + 1]
+        if s0 == s1:
+            continue
+        xe = x.index_select(0, x_rows[s0:s1].long()) if x_rows is not None else x[s0:s1]
+        out[ei] = torch.mm(dy[s0:s1].t().float(), xe.float()).to(out.dtype)
 
 
 def slot_major(x: torch.Tensor, rows: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -315,9 +340,15 @@ def slot_major(x: torch.Tensor, rows: Optional[torch.Tensor] = None) -> torch.Te
     return out[:, :S]
 
 
-def routed_experts(hs: torch.Tensor, weights: torch.Tensor, experts: ExpertWeights, capture=None) -> torch.Tensor:
-    """Experts forward with the reference signature's data: hs [T, H], weights [T, E]."""
-    return RoutedExpertsFn.apply(hs, weights, experts, capture)
+def routed_experts(hs: torch.Tensor, weights: torch.Tensor, experts: ExpertWeights, capture=None,
+                   weight_params: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+    """Experts forward with the reference signature's data: hs [T, H], weights [T, E].
+
+    weight_params: optional (gate_up, down) dense Parameters that ``experts``
+    holds (possibly as converted copies); when they require grad they receive
+    dense gradients, as the reference's autograd through the expert loop."""
+    wg, wd = weight_params if weight_params is not None else (None, None)
+    return RoutedExpertsFn.apply(hs, weights, experts, capture, wg, wd)
 
 
 class RouteTopKFn(torch.autograd.Function):
