@@ -279,12 +279,45 @@ def cpu_baseline_moe(max_seconds: float = 20.0) -> dict:
                        f"x{reps} reps in {dt:.1f} s; the dense-masked reference path does 16x this work")
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_qwen3_cfg2.json")
+
+
+def probe_kernels(dev) -> None:
+    """One launch of each hot-path kernel on the bench workloads, preceded by an
+    elementwise copy of known size (512 MiB read + 512 MiB written) that
+    calibrates the rocprofv3 FETCH_SIZE / WRITE_SIZE counters; the target of
+    the counter passes that fill ``roofline.traffic``."""
+    n = 256 * 2 ** 20  # fp16 elements: 512 MiB
+    src = torch.ones(n, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.add(src, 0, out=dst)  # calibration: 536,870,912 B read, 536,870,912 B written
+    torch.cuda.synchronize()
+    del src, dst
+    bench_dequant(dev, 1, 0)
+    L = build_moe(dev)
+    bench_moe_kernels(L, 1)
+    torch.cuda.synchronize()
+
+
+def _load_traffic() -> dict:
+    """Per-launch HBM bytes of the hot kernels measured with rocprofv3 counters
+    (profiles/hbm_traffic_qwen3_cfg2.md gives the commands); {} if absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get("bytes_per_launch", {})
+    except (OSError, ValueError):
+        return {}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--probe-kernels", action="store_true",
+                    help="launch each hot kernel once (counter-collection target) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -296,6 +329,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     from usaf_amd import _native
     _native.load()
+    if args.probe_kernels:
+        probe_kernels(dev)
+        return 0
 
     _log("moe step: Qwen3-30B-A3B expert layer, 4096 tokens, top-8, 4-bit, fwd+bwd+SparseAdam")
     mo = bench_moe_step(dev, args.steps, args.warmup)
@@ -318,6 +354,7 @@ def main() -> int:
     kern = {n: v for n, v in mo["kernels"].items() if isinstance(v, dict)}
     dom = max(kern, key=lambda n: kern[n]["ms"])
     dk = kern[dom]
+    traffic = _load_traffic()
     line = {
         "metric": METRIC,
         "value": round(mo["tokens_per_s"], 1),
@@ -340,13 +377,15 @@ def main() -> int:
                    "step_tflops": round(mo["tflops"], 1),
                    "step_mfma_frac": round(mo["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": dk["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(dk["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(dk["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": traffic.get(dom),
                      "ms_per_launch": dk["ms"], "flop_per_launch": dk["flop_per_launch"]},
         "kernels": mo["kernels"],
         "dequant": {"workload": "one Qwen3-30B-A3B MoE layer (gate_up+down) as one 4-bit arena -> bf16",
                     "elements": LAYER_ELEMS, "ms_per_launch": round(dq["ms_per_launch"], 4),
                     "roofline": {"bound": "hbm", "achieved": round(dq["gbs"], 1), "peak": HBM_PEAK_GBS,
-                                 "unit": "GB/s", "frac": round(dq["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                                 "unit": "GB/s", "frac": round(dq["gbs"] / HBM_PEAK_GBS, 4),
+                                 "traffic": traffic.get("dequant")},
                     "cpu_baseline": cpu_dq},
         "cpu_baseline": cpu,
     }

@@ -55,7 +55,7 @@ constexpr int LDSW = BK + 8;  // LDS row stride in 16-bit elements (16 B pad: co
 constexpr int LDSC = BN + 8; // epilogue tile row stride (16-bit elements)
 constexpr int MAX_E = 1024;
 constexpr int kXcds = 8;      // MI355X: 8 accelerator dies, blocks dispatched round-robin over them
-constexpr size_t kSmemBytes = (size_t)2 * (BM + BN) * LDSW * 2 + (MAX_E + 1 + kThreads) * 4;
+constexpr size_t kSmemBytes = (size_t)2 * (BM + BN) * LDSW * 2 + (2 * (MAX_E + 1) + kThreads) * 4;
 
 enum { BMODE_NK = 0, BMODE_KN = 1 };
 enum { BQ_Q4 = 0, BQ_DENSE16 = 1 };
@@ -452,13 +452,138 @@ __device__ __forceinline__ void consume_tile(const uint16_t* sA0, const uint16_t
   lds_barrier();
 }
 
+// ---- tile list ------------------------------------------------------------------
+// Expert e's slots form ceil(S_e / BMV) m-tiles of BMV rows; the last one is
+// "light" when it holds fewer than BMV / 2 rows.  The list puts every heavy
+// m-tile (expert-major) before every light one, so tiles of equal cost run in
+// the same rounds and the blocks sharing an m-tile stay in step.
+// s_h[e] / s_l[e]: prefix counts of heavy / light m-tiles before expert e
+// (s_h[E], s_l[E] the totals).  All THREADS threads call it.
+template <int THREADS>
+__device__ __forceinline__ void block_scan(int32_t* s_part, int tid, int local) {
+  s_part[tid] = local;
+  lds_barrier();
+  for (int off = 1; off < THREADS; off <<= 1) {
+    const int v = (tid >= off) ? s_part[tid - off] : 0;
+    lds_barrier();
+    s_part[tid] += v;
+    lds_barrier();
+  }
+}
+
+template <int THREADS, int BMV>
+__device__ __forceinline__ void mtile_prefix(const GemmArgs& g, int32_t* s_h, int32_t* s_l, int32_t* s_part,
+                                             int tid) {
+  const int E = g.E;
+  const int per = (E + THREADS - 1) / THREADS;
+  const int e0 = tid * per;
+  auto counts = [&](int e, int& h, int& l) {
+    const int S = g.offsets[e + 1] - g.offsets[e];
+    const int c = (S + BMV - 1) / BMV;
+    l = (c > 0 && S - (c - 1) * BMV < BMV / 2) ? 1 : 0;
+    h = c - l;
+  };
+  int hl = 0, ll = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      int h, l;
+      counts(e, h, l);
+      hl += h;
+      ll += l;
+    }
+  }
+  block_scan<THREADS>(s_part, tid, hl);
+  int run = s_part[tid] - hl;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      int h, l;
+      counts(e, h, l);
+      s_h[e] = run;
+      run += h;
+    }
+  }
+  if (tid == THREADS - 1) s_h[E] = s_part[THREADS - 1];
+  lds_barrier();
+  block_scan<THREADS>(s_part, tid, ll);
+  run = s_part[tid] - ll;
+  for (int i = 0; i < per; ++i) {
+    const int e = e0 + i;
+    if (e < E) {
+      int h, l;
+      counts(e, h, l);
+      s_l[e] = run;
+      run += l;
+    }
+  }
+  if (tid == THREADS - 1) s_l[E] = s_part[THREADS - 1];
+  lds_barrier();
+}
+
+// largest e with pre[e] <= x (pre non-decreasing, pre[0] = 0 <= x)
+__device__ __forceinline__ int prefix_owner(const int32_t* pre, int E, int64_t x) {
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pre[mid] <= x) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// m-tile mt of the list -> expert, first slot, rows
+template <int BMV>
+__device__ __forceinline__ void mtile_decode(const GemmArgs& g, const int32_t* s_h, const int32_t* s_l, int64_t mt,
+                                             int& e, int64_t& m_beg, int& valid) {
+  const int E = g.E;
+  int64_t j;
+  if (mt < s_h[E]) {
+    e = prefix_owner(s_h, E, mt);
+    j = mt - s_h[e];
+  } else {
+    e = prefix_owner(s_l, E, mt - s_h[E]);
+    const int S = g.offsets[e + 1] - g.offsets[e];
+    j = (S + BMV - 1) / BMV - 1;
+  }
+  m_beg = g.offsets[e] + j * BMV;
+  const int64_t rem = g.offsets[e + 1] - m_beg;
+  valid = (int)(rem < BMV ? rem : BMV);
+}
+
+// XCD-aware tile walk: blocks are dispatched round-robin over kXcds dies
+// (block b on die b % dies), and die d takes the m-tiles mt = d, d + dies, ...
+// with all their n-tiles, spread over the die's blocks; the n-tiles of one
+// m-tile -- which read the same activation rows -- run together on one die
+// and share its L2, and every die gets the same mix of heavy and light tiles.
+struct TileWalk {
+  int64_t n_mt, n_nt;
+  int dies, xcd;
+  int64_t per_xcd, local_b, count;  // blocks on this die, this block's rank, m-tiles of this die
+  __device__ TileWalk(int64_t n_mt_, int64_t n_nt_) : n_mt(n_mt_), n_nt(n_nt_) {
+    const int64_t nblk = gridDim.x;
+    dies = nblk < kXcds ? (int)nblk : kXcds;
+    xcd = (int)(blockIdx.x % dies);
+    per_xcd = (nblk + dies - 1 - xcd) / dies;
+    local_b = blockIdx.x / dies;
+    count = n_mt > xcd ? (n_mt - xcd + dies - 1) / dies : 0;
+  }
+  __device__ int64_t first() const { return local_b; }
+  __device__ int64_t end() const { return count * n_nt; }
+  __device__ int64_t step() const { return per_xcd; }
+  __device__ void decode(int64_t u, int64_t& mt, int64_t& nt) const {
+    mt = xcd + (int64_t)dies * (u / n_nt);
+    nt = u % n_nt;
+  }
+};
+
 template <int BMODE, int EPI, int BQ, int DT>
 __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* const sA0 = smem;                      // [2][BM * LDSW]
   uint16_t* const sB0 = smem + 2 * BM * LDSW;      // [2][BN * LDSW]
-  int32_t* const s_mt = reinterpret_cast<int32_t*>(smem + 2 * (BM + BN) * LDSW);  // [MAX_E + 1]
-  int32_t* const s_part = s_mt + MAX_E + 1;                                        // [kThreads]
+  int32_t* const s_h = reinterpret_cast<int32_t*>(smem + 2 * (BM + BN) * LDSW);  // [MAX_E + 1]
+  int32_t* const s_l = s_h + MAX_E + 1;                                           // [MAX_E + 1]
+  int32_t* const s_part = s_l + MAX_E + 1;                                        // [kThreads]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -469,62 +594,16 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(const GemmArgs g) {
   const int wm = (wave & 3) >> 1, wn = wave & 1;
   const int E = g.E;
 
-  // m-tile prefix over experts: each thread owns a run of experts, then a block scan
-  {
-    const int per = (E + kThreads - 1) / kThreads;
-    const int e0 = tid * per;
-    int local = 0;
-    for (int i = 0; i < per; ++i) {
-      const int e = e0 + i;
-      if (e < E) local += (g.offsets[e + 1] - g.offsets[e] + BM - 1) / BM;
-    }
-    s_part[tid] = local;
-    lds_barrier();
-    for (int off = 1; off < kThreads; off <<= 1) {
-      const int v = (tid >= off) ? s_part[tid - off] : 0;
-      lds_barrier();
-      s_part[tid] += v;
-      lds_barrier();
-    }
-    int run = s_part[tid] - local;
-    for (int i = 0; i < per; ++i) {
-      const int e = e0 + i;
-      if (e < E) {
-        s_mt[e] = run;
-        run += (g.offsets[e + 1] - g.offsets[e] + BM - 1) / BM;
-      }
-    }
-    if (tid == kThreads - 1) s_mt[E] = s_part[kThreads - 1];
-    lds_barrier();
-  }
-  const int64_t n_mt = s_mt[E];
+  mtile_prefix<kThreads, BM>(g, s_h, s_l, s_part, tid);
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? g.N / 64 : g.N / BN;
-  const int64_t n_tiles = n_mt * n_nt;
   const int nk = (int)(g.K / BK);
-
-  // XCD-aware walk: blocks are dispatched round-robin over kXcds dies, so
-  // block b runs on die b % kXcds.  Each die takes one contiguous slice of the
-  // (expert, m-tile, n-tile) list, so the n-tiles of an expert -- which share
-  // the expert's activation rows -- run on one die and share its L2.
-  // With fewer blocks than dies, every block is its own slice.
-  const int64_t nblk = gridDim.x;
-  const int dies = nblk < kXcds ? (int)nblk : kXcds;
-  const int xcd = (int)(blockIdx.x % dies);
-  const int64_t per_xcd = (nblk + dies - 1 - xcd) / dies;  // blocks on this die (>= 1)
-  const int64_t local_b = blockIdx.x / dies;
-  const int64_t t_beg = n_tiles * xcd / dies, t_end = n_tiles * (xcd + 1) / dies;
-
-  for (int64_t tile = t_beg + local_b; tile < t_end; tile += per_xcd) {
-    const int64_t mt = tile / n_nt, nt = tile % n_nt;
-    int lo = 0, hi = E - 1;  // expert of m-tile mt: largest e with s_mt[e] <= mt
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_mt[mid] <= mt) lo = mid; else hi = mid - 1;
-    }
-    const int e = lo;
-    const int64_t m_beg = g.offsets[e] + (mt - s_mt[e]) * BM;
-    const int64_t m_end = g.offsets[e + 1];
-    const int valid = (int)((m_end - m_beg < BM) ? (m_end - m_beg) : BM);
+  const TileWalk walk(s_h[E] + s_l[E], n_nt);
+  for (int64_t u = walk.first(); u < walk.end(); u += walk.step()) {
+    int64_t mt, nt;
+    walk.decode(u, mt, nt);
+    int e, valid;
+    int64_t m_beg;
+    mtile_decode<BM>(g, s_h, s_l, mt, e, m_beg, valid);
     const int nrb = (valid + 31) >> 5;  // 32-row blocks holding slots
     const int64_t n0 = (EPI == EPI_SWIGLU_FWD) ? nt * 64 : nt * BN;
 
@@ -625,7 +704,7 @@ constexpr int NK_EPW = 40;      // epilogue staging row stride (16-bit elements;
 constexpr int NK_EPI_ARR = 3;   // 32 x 32 blocks a wave stages per row block (gate, up, act)
 constexpr int NK_EPI_ELEMS = NK_EPI_ARR * 32 * NK_EPW;
 constexpr size_t kNkSmemBytes =
-    (size_t)2 * NK_BM * LDSW * 2 + (size_t)4 * NK_EPI_ELEMS * 2 + (size_t)(MAX_E + 1 + NK_THREADS) * 4;
+    (size_t)2 * NK_BM * LDSW * 2 + (size_t)4 * NK_EPI_ELEMS * 2 + (size_t)(2 * (MAX_E + 1) + NK_THREADS) * 4;
 
 // 8 codes of one 32-bit word (code 2i in the low nibble of byte i) -> 8 16-bit
 // weights in natural order, bit-identical to dequantize_4bit:
@@ -667,38 +746,6 @@ __device__ __forceinline__ uint32_t dq_pair(uint32_t w, int p, f16x2 s2, f16x2 z
   uint32_t o = __builtin_bit_cast(uint32_t, v);
   if constexpr (DT == USAF_BF16) o = h2_to_bf2(o);
   return o;
-}
-
-// m-tile prefix over experts (m-tiles of BMV slots): s_mt[e] = first m-tile of
-// expert e, s_mt[E] = total.  All THREADS threads call it.
-template <int THREADS, int BMV>
-__device__ __forceinline__ void mtile_prefix(const GemmArgs& g, int32_t* s_mt, int32_t* s_part, int tid) {
-  const int E = g.E;
-  const int per = (E + THREADS - 1) / THREADS;
-  const int e0 = tid * per;
-  int local = 0;
-  for (int i = 0; i < per; ++i) {
-    const int e = e0 + i;
-    if (e < E) local += (g.offsets[e + 1] - g.offsets[e] + BMV - 1) / BMV;
-  }
-  s_part[tid] = local;
-  lds_barrier();
-  for (int off = 1; off < THREADS; off <<= 1) {
-    const int v = (tid >= off) ? s_part[tid - off] : 0;
-    lds_barrier();
-    s_part[tid] += v;
-    lds_barrier();
-  }
-  int run = s_part[tid] - local;
-  for (int i = 0; i < per; ++i) {
-    const int e = e0 + i;
-    if (e < E) {
-      s_mt[e] = run;
-      run += (g.offsets[e + 1] - g.offsets[e] + BMV - 1) / BMV;
-    }
-  }
-  if (tid == THREADS - 1) s_mt[E] = s_part[THREADS - 1];
-  lds_barrier();
 }
 
 // One tile of the NK kernel with NRB (>= the tile's occupied row blocks) row
@@ -1004,34 +1051,22 @@ __global__ __launch_bounds__(NK_THREADS) void moe_gemm_nk_kernel(const GemmArgs 
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* const sA0 = smem;                           // [2][NK_BM * LDSW]
   uint16_t* const sE0 = smem + 2 * NK_BM * LDSW;        // [4 waves][NK_EPI_ELEMS]
-  int32_t* const s_mt = reinterpret_cast<int32_t*>(sE0 + 4 * NK_EPI_ELEMS);  // [MAX_E + 1]
-  int32_t* const s_part = s_mt + MAX_E + 1;                                 // [NK_THREADS]
+  int32_t* const s_h = reinterpret_cast<int32_t*>(sE0 + 4 * NK_EPI_ELEMS);  // [MAX_E + 1]
+  int32_t* const s_l = s_h + MAX_E + 1;                                     // [MAX_E + 1]
+  int32_t* const s_part = s_l + MAX_E + 1;                                  // [NK_THREADS]
   const int tid = threadIdx.x;
   uint16_t* const sE = sE0 + (tid >> 6) * NK_EPI_ELEMS;
   const int E = g.E;
-  mtile_prefix<NK_THREADS, NK_BM>(g, s_mt, s_part, tid);
-  const int64_t n_mt = s_mt[E];
+  mtile_prefix<NK_THREADS, NK_BM>(g, s_h, s_l, s_part, tid);
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + NK_BN - 1) / NK_BN;
-  const int64_t n_tiles = n_mt * n_nt;
   const int nk = (int)(g.K / BK);
-  // XCD-aware walk, as in moe_gemm_kernel: one contiguous slice of the tile list per die
-  const int64_t nblk = gridDim.x;
-  const int dies = nblk < kXcds ? (int)nblk : kXcds;
-  const int xcd = (int)(blockIdx.x % dies);
-  const int64_t per_xcd = (nblk + dies - 1 - xcd) / dies;
-  const int64_t local_b = blockIdx.x / dies;
-  const int64_t t_beg = n_tiles * xcd / dies, t_end = n_tiles * (xcd + 1) / dies;
-  for (int64_t tile = t_beg + local_b; tile < t_end; tile += per_xcd) {
-    const int64_t mt = tile / n_nt, nt = tile % n_nt;
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_mt[mid] <= mt) lo = mid; else hi = mid - 1;
-    }
-    const int e = lo;
-    const int64_t m_beg = g.offsets[e] + (mt - s_mt[e]) * NK_BM;
-    const int64_t m_end = g.offsets[e + 1];
-    const int valid = (int)((m_end - m_beg < NK_BM) ? (m_end - m_beg) : NK_BM);
+  const TileWalk walk(s_h[E] + s_l[E], n_nt);
+  for (int64_t u = walk.first(); u < walk.end(); u += walk.step()) {
+    int64_t mt, nt;
+    walk.decode(u, mt, nt);
+    int e, valid;
+    int64_t m_beg;
+    mtile_decode<NK_BM>(g, s_h, s_l, mt, e, m_beg, valid);
     const int nrb = (valid + 31) >> 5;
     if (nrb > 4) nk_tile<8, EPI, BQ, DT>(g, sA0, sE, tid, e, m_beg, valid, nt, nk);
     else if (nrb > 2) nk_tile<4, EPI, BQ, DT>(g, sA0, sE, tid, e, m_beg, valid, nt, nk);
