@@ -1074,6 +1074,399 @@ __global__ __launch_bounds__(NK_THREADS) void moe_gemm_nk_kernel(const GemmArgs 
   }
 }
 
+// =====================================================================================
+// Forward (NK) kernel for 4-bit weights with LDS-DMA staging.
+//
+//   C[m, n] = sum_k A[row(m), k] * W_e[n, k]
+//
+// 256 threads = 4 waves, one per SIMD, one block per CU, persistent over a
+// per-die tile list.  Tile: up to 320 slots of one expert (10 blocks of 32) x
+// 256 weight rows; wave w owns weight rows [64w, 64w + 64) (two 32-row blocks)
+// for every slot, so each weight element is dequantized once per tile.
+// The MFMA takes the weights as its A operand (32 n x 16 k) and the slots as
+// its B operand (32 m x 16 k): a lane's accumulator then holds 4 consecutive
+// output columns of one slot, which go to global memory as 8-byte stores with
+// no LDS round trip.
+// Every global read is a global_load_lds (DMA into LDS, no VGPR staging)
+// into a 3-stage ring, stage s = k-step % 3:
+//   activations  256 rows x 128 B (16-byte chunks XOR-swizzled by row)
+//   codes        256 weight rows x 32 B, scale|zero 256 x 4 B
+// At k-step gs a thread issues the codes of gs + 3 and the activations of
+// gs + 2 (11 DMA instructions), multiplies k-step gs, and dequantizes the
+// codes of gs + 1 into the other register set of weight fragments; the step
+// ends with s_waitcnt vmcnt(11) (everything but this step's DMAs landed) and
+// a workgroup barrier.  The load streams run straight across tile boundaries,
+// so the next tile's first k-steps are in flight during this tile's last
+// steps and epilogue.
+// =====================================================================================
+constexpr int Q_BM = 256, Q_BN = 256, Q_THREADS = 256;
+constexpr int Q_A_BYTES = Q_BM * BK * 2;                 // activation rows of one k-step
+constexpr int Q_C_BYTES = Q_BN * BK / 2;                 // codes of one k-step
+constexpr int Q_Z_BYTES = Q_BN * 4;                      // scale|zero pairs of one k-step
+constexpr int Q_STAGE = Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES;
+constexpr int Q_A_LOADS = Q_A_BYTES / (16 * Q_THREADS);  // 8 x 16 B per thread
+constexpr int Q_C_LOADS = Q_C_BYTES / (16 * Q_THREADS);  // 2 x 16 B per thread
+constexpr int Q_TAB_BYTES = (2 * (MAX_E + 1) + Q_THREADS) * 4;
+constexpr int Q_EPW = 104;                      // staging row stride, 16-bit elements (96 columns + pad)
+constexpr int Q_EP_BYTES = 32 * Q_EPW * 2;      // one wave's 32 x 96 staging tile
+constexpr int Q_EP_OFF = (3 * Q_STAGE + Q_TAB_BYTES + 15) / 16 * 16;
+constexpr size_t kQSmemBytes = (size_t)Q_EP_OFF + 4 * Q_EP_BYTES;
+static_assert(kQSmemBytes <= 160 * 1024, "LDS budget");
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// 16-byte chunk of an activation row: logical chunk c of row r sits at physical
+// chunk c ^ (r & 7), so the 8 rows a fragment read touches per LDS cycle hit
+// distinct banks.
+__device__ __forceinline__ int q_swz(int r) { return r & 7; }
+
+__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds_dst, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds_dst, 4, 0, 0);
+}
+
+struct QTile {
+  int e, valid;
+  int64_t m_beg, nt;
+};
+
+template <int EPI, int DT>
+__global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
+  int32_t* const s_h = reinterpret_cast<int32_t*>(qsm + 3 * Q_STAGE);  // [MAX_E + 1]
+  int32_t* const s_l = s_h + MAX_E + 1;                                 // [MAX_E + 1]
+  int32_t* const s_part = s_l + MAX_E + 1;                              // [Q_THREADS]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, half = lane >> 5;
+  const int E = g.E;
+  const int64_t K = g.K;
+  const int nk = (int)(K / BK);  // even and >= 2: K % 128 == 0
+  mtile_prefix<Q_THREADS, Q_BM>(g, s_h, s_l, s_part, tid);
+  const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
+  const TileWalk walk(s_h[E] + s_l[E], n_nt);
+  const int64_t first = walk.first(), stride = walk.step(), wend = walk.end();
+  const int n_my = first < wend ? (int)((wend - first + stride - 1) / stride) : 0;
+  if (n_my == 0) return;  // block-uniform
+
+  auto decode = [&](int ord) {
+    QTile t;
+    int64_t mt;
+    walk.decode(first + (int64_t)ord * stride, mt, t.nt);
+    mtile_decode<Q_BM>(g, s_h, s_l, mt, t.e, t.m_beg, t.valid);
+    return t;
+  };
+  // weight row of tile row b (0..255); columns past N (or I) read row 0 and are never stored
+  auto wrow = [&](const QTile& t, int b) -> int64_t {
+    if constexpr (EPI == EPI_SWIGLU_FWD) {
+      const int64_t n = t.nt * 128 + (b >> 6) * 32 + (b & 31);
+      return n < g.inter ? (((b >> 5) & 1) ? g.inter : 0) + n : 0;
+    } else {
+      const int64_t n = t.nt * Q_BN + b;
+      return n < g.N ? n : 0;
+    }
+  };
+
+  // ---- load streams: the codes run one k-step ahead of the activations ----
+  // code stream: byte offsets of this thread's two 16-byte code chunks and its
+  // scale|zero word at k-step 0 of the stream's tile
+  int c_ord = 0, c_kt = 0;
+  int64_t c_off0 = 0, c_off1 = 0, z_off = 0;
+  // activation stream: element offsets of this thread's 8 chunks at k-step 0
+  // (row * lda + chunk; the host checks that they fit in 31 bits)
+  int a_ord = 0, a_kt = 0;
+  int32_t a_off[Q_A_LOADS], a_next[Q_A_LOADS];
+  const int a_lc8 = ((tid & 7) ^ q_swz(tid >> 3)) * 8;  // logical chunk of this thread's DMA slot, in elements
+  auto c_setup = [&](const QTile& t) {
+    const int b0 = tid >> 1, b1 = 128 + (tid >> 1);
+    c_off0 = ((((int64_t)t.e * g.w_rows + wrow(t, b0)) * K) >> 1) + 16 * (tid & 1);
+    c_off1 = ((((int64_t)t.e * g.w_rows + wrow(t, b1)) * K) >> 1) + 16 * (tid & 1);
+    z_off = (((int64_t)t.e * g.w_rows + wrow(t, tid)) * K) >> 7;
+  };
+  // activation rows of this thread's chunks (the slot index itself without a row map);
+  // the offsets are formed only when the stream enters the tile, one k-step
+  // after these loads, so they never hold up the DMAs issued in between
+  auto a_rows_load = [&](const QTile& t, int32_t* dst) {
+#pragma unroll
+    for (int c = 0; c < Q_A_LOADS; ++c) {
+      const int r = 32 * c + (tid >> 3);
+      const int64_t m = t.m_beg + (r < t.valid ? r : t.valid - 1);
+      dst[c] = g.a_rows ? g.a_rows[m] : (int32_t)m;
+    }
+  };
+  const int32_t lda32 = (int32_t)g.lda;
+  // One DMA instruction of a k-step: d = 0, 1 the two code chunks, d = 2 the
+  // scale|zero word (code stream, into stage sc_stage), d >= 3 activation
+  // chunk d - 3 (activation stream, into stage sa_stage).  A k-step's 11 DMAs
+  // are spread over its MFMA regions so that the four waves do not queue them
+  // on the vector memory pipe all at once.
+  constexpr int Q_DMAS = 3 + Q_A_LOADS;
+  auto dma_one = [&](int d, int sc_stage, int sa_stage) {
+    if (d < 2) {
+      uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
+      dma16(g.wq + (d ? c_off1 : c_off0) + c_kt * 32, sc + (d * 256 + wave * 64) * 16);
+    } else if (d == 2) {
+      uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
+      dma4(g.wsz + z_off + (c_kt >> 1), sc + Q_C_BYTES + wave * 64 * 4);
+    } else {
+      const int c = d - 3;
+      uint8_t* sa = qsm + sa_stage * Q_STAGE;
+      dma16(g.A + a_off[c] + a_kt * BK, sa + (c * 256 + wave * 64) * 16);
+    }
+  };
+  // advance both streams by one k-step; the code stream's tile change also
+  // fetches the next tile's activation rows, which the activation stream turns
+  // into offsets when it enters that tile one k-step later
+  auto advance = [&]() {
+    if (++c_kt == nk) {
+      if (c_ord + 1 < n_my) {
+        ++c_ord;
+        c_kt = 0;
+        const QTile t = decode(c_ord);
+        c_setup(t);
+        a_rows_load(t, a_next);
+      } else {
+        c_kt = nk - 1;  // past the last tile: repeat the last k-step into a stage nobody reads
+      }
+    }
+    if (++a_kt == nk) {
+      if (a_ord + 1 < n_my) {
+        ++a_ord;
+        a_kt = 0;
+#pragma unroll
+        for (int c = 0; c < Q_A_LOADS; ++c) a_off[c] = a_next[c] * lda32 + a_lc8;
+      } else {
+        a_kt = nk - 1;
+      }
+    }
+  };
+
+  // ---- weight fragments: wf[slot][column block][sub-step j]; lane half h holds
+  //      k = 32h + 8j + [0, 8) of weight row 32cb + l32 of the wave ----
+  u32x4 wf[2][2][4];
+  auto codes_read = [&](int stage, u32x4 (&cq)[2], uint32_t (&csz)[2]) {
+    const uint8_t* sc = qsm + stage * Q_STAGE + Q_A_BYTES;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int b = 64 * wave + 32 * cb + l32;
+      cq[cb] = *reinterpret_cast<const u32x4*>(sc + (2 * b + half) * 16);
+      csz[cb] = *reinterpret_cast<const uint32_t*>(sc + Q_C_BYTES + b * 4);
+    }
+  };
+  auto dequant_all = [&](auto bs_c, int stage) {
+    constexpr int BS = decltype(bs_c)::value;
+    u32x4 cq[2];
+    uint32_t csz[2];
+    codes_read(stage, cq, csz);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const f16x2 s2 = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
+      const f16x2 z2 = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wf[BS][cb][j] = dq8<DT>(cq[cb][j], s2, z2);
+    }
+  };
+
+  // ---- one k-step: MFMAs of k-step gs (activations in stage s0, weights in
+  //      slot BS) with the dequant of k-step gs + 1 (codes in stage s1) into slot BS ^ 1 ----
+  auto step = [&](auto bs_c, auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value][2], int s0, int s1, int s2) {
+    constexpr int BS = decltype(bs_c)::value, NRB = decltype(nrb_c)::value;
+    constexpr int NF = 4 * NRB;     // activation fragments, f = j * NRB + i
+    constexpr int R = NF / 2;       // regions of two fragments (four MFMAs)
+    constexpr int PF = 4;           // fragment prefetch distance
+    constexpr int PPR = (32 + R - 2) / (R - 1);  // weight pairs dequantized per region (regions 1..R-1)
+    constexpr int DPR = (Q_DMAS + R - 1) / R;    // DMAs issued per region
+    u32x4 cq[2];
+    uint32_t csz[2];
+    codes_read(s1, cq, csz);
+    const uint8_t* sa = qsm + s0 * Q_STAGE;
+    auto frag = [&](int f) -> u32x4 {
+      const int i = f % NRB, j = f / NRB;
+      const int m = 32 * i + l32;
+      return *reinterpret_cast<const u32x4*>(sa + m * 128 + 16 * ((4 * half + j) ^ q_swz(m)));
+    };
+    u32x4 af[NF];
+#pragma unroll
+    for (int f = 0; f < PF; ++f) af[f] = frag(f);
+    f16x2 s2v[2], z2v[2];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const int f = 2 * r + gg, i = f % NRB, j = f / NRB;
+        if (f + PF < NF) af[f + PF] = frag(f + PF);
+        acc[i][0] = mfma32<DT>(wf[BS][0][j], af[f], acc[i][0]);
+        acc[i][1] = mfma32<DT>(wf[BS][1][j], af[f], acc[i][1]);
+      }
+      // codes of gs + 3 into the stage k-step gs's codes left, activations of gs + 2
+#pragma unroll
+      for (int dd = 0; dd < DPR; ++dd)
+        if (r * DPR + dd < Q_DMAS) dma_one(r * DPR + dd, s0, s2);
+      if (r >= 1) {
+#pragma unroll
+        for (int pp = 0; pp < PPR; ++pp) {
+          const int p = (r - 1) * PPR + pp;
+          if (p < 32) {
+            const int cb = p >> 4, wd = (p >> 2) & 3, q = p & 3;
+            if ((p & 15) == 0) {
+              s2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
+              z2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
+            }
+            uint32_t v = dq_pair<DT>(cq[cb][wd], q, s2v[cb], z2v[cb]);
+            asm volatile("" : "+v"(v));  // computed here, next to the MFMAs, not sunk to its first use
+            wf[BS ^ 1][cb][wd][q] = v;
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // this step's 11 DMAs may stay in flight; everything older (the stages the
+    // next step reads) has landed in this wave, and after the barrier in all waves.
+    // sched_barrier keeps the step's register work on its side of the barrier.
+    advance();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(11)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- epilogue: per 32-slot block, the wave's dtype results go through its
+  //      own LDS tile ([32 slots][96 columns]: gate, up, act or the 64 output
+  //      columns) and out as 16-byte row stores, 4-8 lanes per row segment ----
+  uint16_t* const sEp = reinterpret_cast<uint16_t*>(qsm + Q_EP_OFF + wave * Q_EP_BYTES);
+  // lane's accumulator values r = 4q..4q+3 of weight block cb -> columns 32cb + 8q + 4half + [0,4) of slot l32
+  auto stage4 = [&](int col, uint32_t lo, uint32_t hi) {
+    *reinterpret_cast<uint2*>(sEp + l32 * Q_EPW + col) = make_uint2(lo, hi);
+  };
+  auto epilogue = [&](auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value][2], const QTile& t) {
+    constexpr int NRB = decltype(nrb_c)::value;
+    if constexpr (EPI == EPI_SWIGLU_FWD) {
+      const int64_t n0 = t.nt * 128 + wave * 32;
+      if (n0 >= g.inter) return;
+#pragma unroll
+      for (int i = 0; i < NRB; ++i) {
+        if (32 * i >= t.valid) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t gb[2], ub[2], ab[2];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            gb[h2] = pack2<DT>(acc[i][0][4 * q + 2 * h2], acc[i][0][4 * q + 2 * h2 + 1]);
+            ub[h2] = pack2<DT>(acc[i][1][4 * q + 2 * h2], acc[i][1][4 * q + 2 * h2 + 1]);
+            const f32x2 gf = unpack2<DT>(gb[h2]), uf = unpack2<DT>(ub[h2]);
+            const f32x2 sf = unpack2<DT>(pack2<DT>(silu_fast(gf.x), silu_fast(gf.y)));
+            ab[h2] = pack2<DT>(sf.x * uf.x, sf.y * uf.y);
+          }
+          const int col = 8 * q + 4 * half;
+          stage4(col, gb[0], gb[1]);
+          stage4(32 + col, ub[0], ub[1]);
+          stage4(64 + col, ab[0], ab[1]);
+        }
+        // 32 rows x 3 x 64 B: lane l takes 16-byte chunk l & 3 of row (l >> 2) + 16p
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int rr = (lane >> 2) + 16 * p;
+          if (32 * i + rr < t.valid) {
+            const int64_t m = t.m_beg + 32 * i + rr;
+            const int ch = (lane & 3) * 8;
+            const u32x4 gv = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
+            const u32x4 uv = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + 32 + ch);
+            const u32x4 av = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + 64 + ch);
+            *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + n0 + ch) = gv;
+            *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + g.inter + n0 + ch) = uv;
+            *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n0 + ch) = av;
+          }
+        }
+      }
+    } else {
+      const int64_t n0 = t.nt * Q_BN + wave * 64;
+      if (n0 >= g.N) return;  // N % 64 == 0: a wave's 64 columns are all valid or none
+#pragma unroll
+      for (int i = 0; i < NRB; ++i) {
+        if (32 * i >= t.valid) break;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            stage4(32 * cb + 8 * q + 4 * half, pack2<DT>(acc[i][cb][4 * q], acc[i][cb][4 * q + 1]),
+                   pack2<DT>(acc[i][cb][4 * q + 2], acc[i][cb][4 * q + 3]));
+        // 32 rows x 128 B: lane l takes 16-byte chunk l & 7 of row (l >> 3) + 8p
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const int rr = (lane >> 3) + 8 * p;
+          if (32 * i + rr < t.valid) {
+            const int ch = (lane & 7) * 8;
+            *reinterpret_cast<u32x4*>(g.out + (t.m_beg + 32 * i + rr) * g.ldo + n0 + ch) =
+                *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
+          }
+        }
+      }
+    }
+  };
+
+  using std::integral_constant;
+  using I0 = integral_constant<int, 0>;
+  using I1 = integral_constant<int, 1>;
+
+  // ---- prologue: codes of k-steps 0..2 and activations of k-steps 0..1 ----
+  {
+    const QTile t0 = decode(0);
+    c_setup(t0);
+    a_rows_load(t0, a_off);
+#pragma unroll
+    for (int c = 0; c < Q_A_LOADS; ++c) a_off[c] = a_off[c] * lda32 + a_lc8;
+  }
+  // code stream at k-step 0, activation stream at k-step 0: issue codes 0,
+  // then (codes 1, activations 0), then (codes 2, activations 1); afterwards
+  // the code stream stands at k-step 3 and the activation stream at k-step 2
+  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0);
+  if (++c_kt == nk) {
+    if (c_ord + 1 < n_my) {
+      ++c_ord;
+      c_kt = 0;
+      const QTile t = decode(c_ord);
+      c_setup(t);
+      a_rows_load(t, a_next);
+    } else {
+      c_kt = nk - 1;
+    }
+  }
+  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 1, 0);
+  advance();
+  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 2, 1);
+  advance();
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  dequant_all(I0{}, 0);
+  asm volatile("s_barrier" ::: "memory");  // stage 0's codes are refilled by k-step 0
+
+  // ---- tiles ----
+  int s0 = 0;  // stage of the current k-step
+  for (int ord = 0; ord < n_my; ++ord) {
+    const QTile t = decode(ord);
+    const int nrb = (t.valid + 31) >> 5;
+    auto run = [&](auto nrb_c) {
+      constexpr int NRB = decltype(nrb_c)::value;
+      f32x16 acc[NRB][2];
+#pragma unroll
+      for (int i = 0; i < NRB; ++i) acc[i][0] = acc[i][1] = f32x16{};
+      for (int kt = 0; kt < nk; kt += 2) {
+        int s1 = s0 == 2 ? 0 : s0 + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+        step(I0{}, nrb_c, acc, s0, s1, s2);
+        s0 = s1;
+        s1 = s2;
+        s2 = s2 == 2 ? 0 : s2 + 1;
+        step(I1{}, nrb_c, acc, s0, s1, s2);
+        s0 = s1;
+      }
+      epilogue(nrb_c, acc, t);
+    };
+    if (nrb > 6) run(integral_constant<int, 8>{});
+    else if (nrb > 4) run(integral_constant<int, 6>{});
+    else if (nrb > 2) run(integral_constant<int, 4>{});
+    else run(integral_constant<int, 2>{});
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // drain the trailing DMAs before the wave ends
+}
+
 template <int EPI, int BQ, int DT>
 int launch_nk_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   static bool attr_set = false;
@@ -1087,6 +1480,19 @@ int launch_nk_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   return USAF_OK;
 }
 
+template <int EPI, int DT>
+int launch_q4_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQSmemBytes);
+    (void)hipGetLastError();
+    attr_set = true;
+  }
+  moe_gemm_q4_kernel<EPI, DT><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
+  return USAF_OK;
+}
+
 template <int EPI>
 int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_total, hipStream_t st,
                    const char* what) {
@@ -1097,12 +1503,16 @@ int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_
   if (blocks > max_tiles) blocks = max_tiles;
   if (blocks < 1) blocks = 1;
   const bool dense = g.w16 != nullptr;
+  // 4-bit weights: the LDS-DMA kernel (activation rows must be 16-byte aligned)
+  const bool dma = !dense && ((uintptr_t)g.A & 15) == 0 && g.lda % 8 == 0 && g.K % 128 == 0;
   int rc;
   if (dt == USAF_BF16)
     rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
+         : dma ? launch_q4_one<EPI, USAF_BF16>(g, (unsigned)blocks, st)
                : launch_nk_one<EPI, BQ_Q4, USAF_BF16>(g, (unsigned)blocks, st);
   else if (dt == USAF_F16)
     rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_F16>(g, (unsigned)blocks, st)
+         : dma ? launch_q4_one<EPI, USAF_F16>(g, (unsigned)blocks, st)
                : launch_nk_one<EPI, BQ_Q4, USAF_F16>(g, (unsigned)blocks, st);
   else
     return set_error(USAF_ERR_INVALID, "%s: dtype must be fp16 or bf16", what);

@@ -85,7 +85,8 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // group reads slots [b + 8l, b + 8l + 8) of each 128-slot window starting at
 // b = s0 rounded down to 8, as one 16-byte load per operand, and accumulates
 // them with v_dot2 in fp32; elements outside [s0, s1) (neighbouring experts,
-// row padding) are masked to zero in both operands.  Positions of one weight
+// row padding) are masked to zero in both operands.  Every load stays inside
+// the operand rows: w < s1 <= ldT and ldT % 8 == 0, so w + 7 < ldT.  Positions of one weight
 // row are adjacent, so the groups of a wave mostly read the same rowT line.
 // Rows >= R, experts >= E and columns >= C are skipped.
 template <int DT>
@@ -96,8 +97,16 @@ __global__ __launch_bounds__(256) void sddmm_kernel(const uint16_t* __restrict__
                                                     const int32_t* __restrict__ col_idx,
                                                     const int64_t* __restrict__ pos_map, float* __restrict__ compact) {
   const int gl = threadIdx.x & 15;
-  const int64_t n_grp = ((int64_t)gridDim.x * blockDim.x) >> 4;
-  for (int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; p < n_pos; p += n_grp) {
+  // The position list is cut into one contiguous slice per accelerator die
+  // (blocks are dispatched round-robin over the dies: block b runs on die
+  // b % dies).  Positions come sorted by expert, so the groups of a die work
+  // through one expert at a time and its operand rows stay in that die's L2.
+  const int dies = gridDim.x < 8 ? (int)gridDim.x : 8;
+  const int die = (int)(blockIdx.x % dies);
+  const int64_t die_blocks = ((int64_t)gridDim.x + dies - 1 - die) / dies;
+  const int64_t lo = n_pos * die / dies, hi = n_pos * (die + 1) / dies;
+  const int64_t n_grp = die_blocks * (blockDim.x >> 4);
+  for (int64_t p = lo + (int64_t)(blockIdx.x / dies) * (blockDim.x >> 4) + (threadIdx.x >> 4); p < hi; p += n_grp) {
     const uint32_t code = (uint32_t)rcode[p];
     const uint32_t i = (uint32_t)col_idx[p];
     const uint32_t e = code >> 21, o = code & 0x1FFFFFu;
