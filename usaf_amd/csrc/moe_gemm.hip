@@ -1100,18 +1100,24 @@ __global__ __launch_bounds__(NK_THREADS) void moe_gemm_nk_kernel(const GemmArgs 
 // steps and epilogue.
 // =====================================================================================
 constexpr int Q_BM = 256, Q_BN = 256, Q_THREADS = 256;
+constexpr int Q_MAX_E = 512;
 constexpr int Q_A_BYTES = Q_BM * BK * 2;                 // activation rows of one k-step
 constexpr int Q_C_BYTES = Q_BN * BK / 2;                 // codes of one k-step
 constexpr int Q_Z_BYTES = Q_BN * 4;                      // scale|zero pairs of one k-step
 constexpr int Q_STAGE = Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES;
 constexpr int Q_A_LOADS = Q_A_BYTES / (16 * Q_THREADS);  // 8 x 16 B per thread
-constexpr int Q_C_LOADS = Q_C_BYTES / (16 * Q_THREADS);  // 2 x 16 B per thread
-constexpr int Q_TAB_BYTES = (2 * (MAX_E + 1) + Q_THREADS) * 4;
+constexpr int Q_DMAS = 3 + Q_A_LOADS;                    // DMA instructions per thread per k-step
+// Dynamic LDS (the DMA targets): 3 stages | s_h, s_l, s_off tables | token rows [2][Q_BM].
+// The epilogue tiles are a separate static array: the compiler then knows that
+// their stores cannot collide with DMA writes still in flight and does not
+// drain the DMAs before them.
+constexpr int Q_TAB_OFF = 3 * Q_STAGE;
+constexpr int Q_TOK_OFF = Q_TAB_OFF + 3 * (Q_MAX_E + 1) * 4;
+constexpr size_t kQSmemBytes = (size_t)Q_TOK_OFF + 2 * Q_BM * 4;
 constexpr int Q_EPW = 104;                      // staging row stride, 16-bit elements (96 columns + pad)
-constexpr int Q_EP_BYTES = 32 * Q_EPW * 2;      // one wave's 32 x 96 staging tile
-constexpr int Q_EP_OFF = (3 * Q_STAGE + Q_TAB_BYTES + 15) / 16 * 16;
-constexpr size_t kQSmemBytes = (size_t)Q_EP_OFF + 4 * Q_EP_BYTES;
-static_assert(kQSmemBytes <= 160 * 1024, "LDS budget");
+constexpr int Q_EP_ELEMS = 32 * Q_EPW;          // one wave's 32 x 96 staging tile
+static_assert(kQSmemBytes + 4 * Q_EP_ELEMS * 2 <= 160 * 1024, "LDS budget");
+static_assert(4 * Q_EP_ELEMS * 2 >= Q_THREADS * 4, "the prefix scratch lives in the epilogue tiles");
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -1126,115 +1132,162 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
 __device__ __forceinline__ void dma4(const void* src, void* lds_dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds_dst, 4, 0, 0);
 }
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 struct QTile {
-  int e, valid;
-  int64_t m_beg, nt;
+  int e, valid, m_beg, nt;  // all wave-uniform
 };
 
 template <int EPI, int DT>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
-  int32_t* const s_h = reinterpret_cast<int32_t*>(qsm + 3 * Q_STAGE);  // [MAX_E + 1]
-  int32_t* const s_l = s_h + MAX_E + 1;                                 // [MAX_E + 1]
-  int32_t* const s_part = s_l + MAX_E + 1;                              // [Q_THREADS]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, half = lane >> 5;
+  __shared__ __attribute__((aligned(16))) uint16_t q_ep[4 * Q_EP_ELEMS];
+  int32_t* const s_h = reinterpret_cast<int32_t*>(qsm + Q_TAB_OFF);  // [Q_MAX_E + 1]
+  int32_t* const s_l = s_h + Q_MAX_E + 1;                             // [Q_MAX_E + 1]
+  int32_t* const s_off = s_l + Q_MAX_E + 1;                           // [Q_MAX_E + 1] expert offsets
+  int32_t* const s_tok = reinterpret_cast<int32_t*>(qsm + Q_TOK_OFF); // [2][Q_BM] activation rows
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, half = lane >> 5;
+  const int wave = uni(tid >> 6);
   const int E = g.E;
-  const int64_t K = g.K;
-  const int nk = (int)(K / BK);  // even and >= 2: K % 128 == 0
-  mtile_prefix<Q_THREADS, Q_BM>(g, s_h, s_l, s_part, tid);
+  const int nk = (int)(g.K / BK);  // even and >= 2: K % 128 == 0
+  {
+    int32_t* const s_part = reinterpret_cast<int32_t*>(q_ep);  // scratch, before any epilogue
+    mtile_prefix<Q_THREADS, Q_BM>(g, s_h, s_l, s_part, tid);
+    for (int e = tid; e <= E; e += Q_THREADS) s_off[e] = g.offsets[e];
+    lds_barrier();
+  }
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
   const TileWalk walk(s_h[E] + s_l[E], n_nt);
   const int64_t first = walk.first(), stride = walk.step(), wend = walk.end();
   const int n_my = first < wend ? (int)((wend - first + stride - 1) / stride) : 0;
   if (n_my == 0) return;  // block-uniform
 
+  // tile ordinal -> expert, first slot, rows, n-tile (m-tile list as in mtile_decode, offsets from LDS)
   auto decode = [&](int ord) {
+    int64_t mt, nt;
+    walk.decode(first + (int64_t)ord * stride, mt, nt);
+    int e;
+    int64_t j;
+    if (mt < s_h[E]) {
+      e = prefix_owner(s_h, E, mt);
+      j = mt - s_h[e];
+    } else {
+      e = prefix_owner(s_l, E, mt - s_h[E]);
+      j = (s_off[e + 1] - s_off[e] + Q_BM - 1) / Q_BM - 1;
+    }
     QTile t;
-    int64_t mt;
-    walk.decode(first + (int64_t)ord * stride, mt, t.nt);
-    mtile_decode<Q_BM>(g, s_h, s_l, mt, t.e, t.m_beg, t.valid);
+    t.e = uni(e);
+    t.m_beg = uni((int)(s_off[t.e] + j * Q_BM));
+    const int rem = s_off[t.e + 1] - t.m_beg;
+    t.valid = uni(rem < Q_BM ? rem : Q_BM);
+    t.nt = uni((int)nt);
     return t;
   };
   // weight row of tile row b (0..255); columns past N (or I) read row 0 and are never stored
   auto wrow = [&](const QTile& t, int b) -> int64_t {
     if constexpr (EPI == EPI_SWIGLU_FWD) {
-      const int64_t n = t.nt * 128 + (b >> 6) * 32 + (b & 31);
+      const int64_t n = (int64_t)t.nt * 128 + (b >> 6) * 32 + (b & 31);
       return n < g.inter ? (((b >> 5) & 1) ? g.inter : 0) + n : 0;
     } else {
-      const int64_t n = t.nt * Q_BN + b;
+      const int64_t n = (int64_t)t.nt * Q_BN + b;
       return n < g.N ? n : 0;
     }
   };
 
-  // ---- load streams: the codes run one k-step ahead of the activations ----
-  // code stream: byte offsets of this thread's two 16-byte code chunks and its
-  // scale|zero word at k-step 0 of the stream's tile
+  // ---- load streams.  Each DMA address is a wave-uniform base plus a 32-bit
+  //      per-lane byte offset (the host checks that the operands fit) ----
+  // code stream: the codes of a k-step run one k-step ahead of its activations
   int c_ord = 0, c_kt = 0;
-  int64_t c_off0 = 0, c_off1 = 0, z_off = 0;
-  // activation stream: element offsets of this thread's 8 chunks at k-step 0
-  // (row * lda + chunk; the host checks that they fit in 31 bits)
+  uint32_t c_off0 = 0, c_off1 = 0, z_off = 0;  // byte offsets of this thread's code chunks / scale|zero word at k-step 0
+  QTile c_next;                               // the tile the code stream enters next
+  // activation stream
   int a_ord = 0, a_kt = 0;
-  int32_t a_off[Q_A_LOADS], a_next[Q_A_LOADS];
-  const int a_lc8 = ((tid & 7) ^ q_swz(tid >> 3)) * 8;  // logical chunk of this thread's DMA slot, in elements
+  bool a_enter = false;                       // entered a new tile at the last advance: refresh a_off
+  uint32_t a_off[Q_A_LOADS];                  // byte offsets of this thread's chunks at k-step 0
+  const int a_lc = (tid & 7) ^ q_swz(tid >> 3);  // logical chunk of this thread's DMA slot
+  const uint32_t lda_b = (uint32_t)g.lda * 2;
   auto c_setup = [&](const QTile& t) {
     const int b0 = tid >> 1, b1 = 128 + (tid >> 1);
-    c_off0 = ((((int64_t)t.e * g.w_rows + wrow(t, b0)) * K) >> 1) + 16 * (tid & 1);
-    c_off1 = ((((int64_t)t.e * g.w_rows + wrow(t, b1)) * K) >> 1) + 16 * (tid & 1);
-    z_off = (((int64_t)t.e * g.w_rows + wrow(t, tid)) * K) >> 7;
+    const int64_t base = (int64_t)t.e * g.w_rows;
+    c_off0 = (uint32_t)((((base + wrow(t, b0)) * g.K) >> 1) + 16 * (tid & 1));
+    c_off1 = (uint32_t)((((base + wrow(t, b1)) * g.K) >> 1) + 16 * (tid & 1));
+    z_off = (uint32_t)((((base + wrow(t, tid)) * g.K) >> 7) * 4);
   };
-  // activation rows of this thread's chunks (the slot index itself without a row map);
-  // the offsets are formed only when the stream enters the tile, one k-step
-  // after these loads, so they never hold up the DMAs issued in between
-  auto a_rows_load = [&](const QTile& t, int32_t* dst) {
-#pragma unroll
-    for (int c = 0; c < Q_A_LOADS; ++c) {
-      const int r = 32 * c + (tid >> 3);
-      const int64_t m = t.m_beg + (r < t.valid ? r : t.valid - 1);
-      dst[c] = g.a_rows ? g.a_rows[m] : (int32_t)m;
+  // with a row map, the activation rows of tile t are fetched into token buffer
+  // buf by a DMA (visible to all threads after the next barrier); without one
+  // the row is the slot itself
+  auto tok_fill = [&](const QTile& t, int buf) {
+    if (g.a_rows) {
+      const int r = tid < t.valid ? tid : t.valid - 1;
+      dma4(g.a_rows + t.m_beg + r, s_tok + buf * Q_BM + wave * 64);
     }
   };
-  const int32_t lda32 = (int32_t)g.lda;
-  // One DMA instruction of a k-step: d = 0, 1 the two code chunks, d = 2 the
-  // scale|zero word (code stream, into stage sc_stage), d >= 3 activation
-  // chunk d - 3 (activation stream, into stage sa_stage).  A k-step's 11 DMAs
-  // are spread over its MFMA regions so that the four waves do not queue them
-  // on the vector memory pipe all at once.
-  constexpr int Q_DMAS = 3 + Q_A_LOADS;
+  auto a_refresh = [&](int ord) {
+    if (g.a_rows) {
+      const int32_t* src = s_tok + (ord & 1) * Q_BM;
+#pragma unroll
+      for (int c = 0; c < Q_A_LOADS; ++c) a_off[c] = (uint32_t)src[32 * c + (tid >> 3)] * lda_b + a_lc * 16;
+    } else {
+      const QTile t = decode(ord);
+#pragma unroll
+      for (int c = 0; c < Q_A_LOADS; ++c) {
+        const int r = 32 * c + (tid >> 3);
+        a_off[c] = (uint32_t)(t.m_beg + (r < t.valid ? r : t.valid - 1)) * lda_b + a_lc * 16;
+      }
+    }
+  };
+  // one DMA instruction of a k-step: d = 0, 1 the code chunks, 2 the scale|zero
+  // word (into stage sc_stage), d >= 3 activation chunk d - 3 (into stage sa_stage)
   auto dma_one = [&](int d, int sc_stage, int sa_stage) {
+    sc_stage = uni(sc_stage);
+    sa_stage = uni(sa_stage);
+    const int c_kt_u = uni(c_kt), a_kt_u = uni(a_kt);
     if (d < 2) {
       uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
-      dma16(g.wq + (d ? c_off1 : c_off0) + c_kt * 32, sc + (d * 256 + wave * 64) * 16);
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wq) + c_kt_u * 32;
+      dma16(base + (d ? c_off1 : c_off0), sc + (d * 256 + wave * 64) * 16);
     } else if (d == 2) {
       uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
-      dma4(g.wsz + z_off + (c_kt >> 1), sc + Q_C_BYTES + wave * 64 * 4);
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wsz) + (c_kt_u >> 1) * 4;
+      dma4(base + z_off, sc + Q_C_BYTES + wave * 64 * 4);
     } else {
       const int c = d - 3;
       uint8_t* sa = qsm + sa_stage * Q_STAGE;
-      dma16(g.A + a_off[c] + a_kt * BK, sa + (c * 256 + wave * 64) * 16);
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.A) + a_kt_u * (BK * 2);
+      dma16(base + a_off[c], sa + (c * 256 + wave * 64) * 16);
     }
   };
-  // advance both streams by one k-step; the code stream's tile change also
-  // fetches the next tile's activation rows, which the activation stream turns
-  // into offsets when it enters that tile one k-step later
+  // start of a k-step: the activation stream picks up the rows of the tile it
+  // entered (their DMA landed before the last barrier); when the code stream is
+  // about to enter a new tile, fetch that tile's activation rows now, ahead of
+  // this k-step's DMAs
+  auto pre_step = [&]() {
+    if (a_enter) {
+      a_refresh(a_ord);
+      a_enter = false;
+    }
+    if (c_kt == nk - 1 && c_ord + 1 < n_my) {
+      c_next = decode(c_ord + 1);
+      tok_fill(c_next, (c_ord + 1) & 1);
+    }
+  };
+  // end of a k-step: advance both streams (past the last tile they repeat the
+  // last k-step into a stage nobody reads)
   auto advance = [&]() {
     if (++c_kt == nk) {
       if (c_ord + 1 < n_my) {
         ++c_ord;
         c_kt = 0;
-        const QTile t = decode(c_ord);
-        c_setup(t);
-        a_rows_load(t, a_next);
+        c_setup(c_next);
       } else {
-        c_kt = nk - 1;  // past the last tile: repeat the last k-step into a stage nobody reads
+        c_kt = nk - 1;
       }
     }
     if (++a_kt == nk) {
       if (a_ord + 1 < n_my) {
         ++a_ord;
         a_kt = 0;
-#pragma unroll
-        for (int c = 0; c < Q_A_LOADS; ++c) a_off[c] = a_next[c] * lda32 + a_lc8;
+        a_enter = true;
       } else {
         a_kt = nk - 1;
       }
@@ -1268,7 +1321,10 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   };
 
   // ---- one k-step: MFMAs of k-step gs (activations in stage s0, weights in
-  //      slot BS) with the dequant of k-step gs + 1 (codes in stage s1) into slot BS ^ 1 ----
+  //      slot BS) with the dequant of k-step gs + 1 (codes in stage s1) into
+  //      slot BS ^ 1; the k-step's DMAs (codes of gs + 3 into stage s0,
+  //      activations of gs + 2 into stage s2) are spread over its regions so
+  //      that the four waves do not queue them on the memory pipe at once ----
   auto step = [&](auto bs_c, auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value][2], int s0, int s1, int s2) {
     constexpr int BS = decltype(bs_c)::value, NRB = decltype(nrb_c)::value;
     constexpr int NF = 4 * NRB;     // activation fragments, f = j * NRB + i
@@ -1276,6 +1332,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     constexpr int PF = 4;           // fragment prefetch distance
     constexpr int PPR = (32 + R - 2) / (R - 1);  // weight pairs dequantized per region (regions 1..R-1)
     constexpr int DPR = (Q_DMAS + R - 1) / R;    // DMAs issued per region
+    pre_step();
     u32x4 cq[2];
     uint32_t csz[2];
     codes_read(s1, cq, csz);
@@ -1298,7 +1355,6 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
         acc[i][0] = mfma32<DT>(wf[BS][0][j], af[f], acc[i][0]);
         acc[i][1] = mfma32<DT>(wf[BS][1][j], af[f], acc[i][1]);
       }
-      // codes of gs + 3 into the stage k-step gs's codes left, activations of gs + 2
 #pragma unroll
       for (int dd = 0; dd < DPR; ++dd)
         if (r * DPR + dd < Q_DMAS) dma_one(r * DPR + dd, s0, s2);
@@ -1320,10 +1376,11 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // this step's 11 DMAs may stay in flight; everything older (the stages the
-    // next step reads) has landed in this wave, and after the barrier in all waves.
-    // sched_barrier keeps the step's register work on its side of the barrier.
     advance();
+    // this step's 11 DMAs may stay in flight; everything older (the stages the
+    // next step reads, the token rows) has landed in this wave, and after the
+    // barrier in all waves.  sched_barrier keeps the step's register work on
+    // its side of the barrier.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(11)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
@@ -1332,15 +1389,21 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // ---- epilogue: per 32-slot block, the wave's dtype results go through its
   //      own LDS tile ([32 slots][96 columns]: gate, up, act or the 64 output
   //      columns) and out as 16-byte row stores, 4-8 lanes per row segment ----
-  uint16_t* const sEp = reinterpret_cast<uint16_t*>(qsm + Q_EP_OFF + wave * Q_EP_BYTES);
-  // lane's accumulator values r = 4q..4q+3 of weight block cb -> columns 32cb + 8q + 4half + [0,4) of slot l32
+  uint16_t* const sEp = q_ep + wave * Q_EP_ELEMS;
+  // lane's accumulator values r = 4q..4q+3 of weight block cb -> columns 32cb + 8q + 4half + [0,4) of slot l32.
+  // Written with an explicit ds_write_b64: the compiler would otherwise drain
+  // every DMA in flight (the next tile's first k-steps) before an LDS store.
+  // The wave's own LDS operations complete in order, so the reads below see it.
+  const uint32_t sEp_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sEp;
   auto stage4 = [&](int col, uint32_t lo, uint32_t hi) {
-    *reinterpret_cast<uint2*>(sEp + l32 * Q_EPW + col) = make_uint2(lo, hi);
+    const uint32_t addr = sEp_lds + (uint32_t)(l32 * Q_EPW + col) * 2;
+    const uint64_t v = (uint64_t)lo | ((uint64_t)hi << 32);
+    asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(v) : "memory");
   };
   auto epilogue = [&](auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value][2], const QTile& t) {
     constexpr int NRB = decltype(nrb_c)::value;
     if constexpr (EPI == EPI_SWIGLU_FWD) {
-      const int64_t n0 = t.nt * 128 + wave * 32;
+      const int64_t n0 = (int64_t)t.nt * 128 + wave * 32;
       if (n0 >= g.inter) return;
 #pragma unroll
       for (int i = 0; i < NRB; ++i) {
@@ -1378,7 +1441,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
         }
       }
     } else {
-      const int64_t n0 = t.nt * Q_BN + wave * 64;
+      const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 64;
       if (n0 >= g.N) return;  // N % 64 == 0: a wave's 64 columns are all valid or none
 #pragma unroll
       for (int i = 0; i < NRB; ++i) {
@@ -1395,7 +1458,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
           const int rr = (lane >> 3) + 8 * p;
           if (32 * i + rr < t.valid) {
             const int ch = (lane & 7) * 8;
-            *reinterpret_cast<u32x4*>(g.out + (t.m_beg + 32 * i + rr) * g.ldo + n0 + ch) =
+            *reinterpret_cast<u32x4*>(g.out + ((int64_t)t.m_beg + 32 * i + rr) * g.ldo + n0 + ch) =
                 *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
           }
         }
@@ -1407,32 +1470,33 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   using I0 = integral_constant<int, 0>;
   using I1 = integral_constant<int, 1>;
 
-  // ---- prologue: codes of k-steps 0..2 and activations of k-steps 0..1 ----
+  // ---- prologue: rows of tile 0, codes of k-steps 0..2, activations of k-steps 0..1;
+  //      afterwards the code stream stands at k-step 3 and the activation stream at 2 ----
   {
     const QTile t0 = decode(0);
     c_setup(t0);
-    a_rows_load(t0, a_off);
-#pragma unroll
-    for (int c = 0; c < Q_A_LOADS; ++c) a_off[c] = a_off[c] * lda32 + a_lc8;
+    tok_fill(t0, 0);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    a_refresh(0);
   }
-  // code stream at k-step 0, activation stream at k-step 0: issue codes 0,
-  // then (codes 1, activations 0), then (codes 2, activations 1); afterwards
-  // the code stream stands at k-step 3 and the activation stream at k-step 2
-  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0);
+  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0);  // codes 0
+  if (nk == 2 && n_my > 1) {                       // the code stream enters tile 1 after codes 1
+    c_next = decode(1);
+    tok_fill(c_next, 1);
+  }
   if (++c_kt == nk) {
     if (c_ord + 1 < n_my) {
       ++c_ord;
       c_kt = 0;
-      const QTile t = decode(c_ord);
-      c_setup(t);
-      a_rows_load(t, a_next);
+      c_setup(c_next);
     } else {
       c_kt = nk - 1;
     }
   }
-  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 1, 0);
+  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 1, 0);  // codes 1, activations 0
   advance();
-  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 2, 1);
+  pre_step();
+  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 2, 1);  // codes 2, activations 1
   advance();
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   dequant_all(I0{}, 0);
@@ -1504,7 +1568,10 @@ int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_
   if (blocks < 1) blocks = 1;
   const bool dense = g.w16 != nullptr;
   // 4-bit weights: the LDS-DMA kernel (activation rows must be 16-byte aligned)
-  const bool dma = !dense && ((uintptr_t)g.A & 15) == 0 && g.lda % 8 == 0 && g.K % 128 == 0;
+  // (row offsets and code offsets within one operand as 32-bit byte offsets)
+  const bool dma = !dense && ((uintptr_t)g.A & 15) == 0 && g.lda % 8 == 0 && g.K % 128 == 0 && g.E <= Q_MAX_E &&
+                   a_rows_total * g.lda * 2 < ((int64_t)1 << 32) &&
+                   (int64_t)g.E * g.w_rows * g.w_cols / 2 < ((int64_t)1 << 32);
   int rc;
   if (dt == USAF_BF16)
     rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
