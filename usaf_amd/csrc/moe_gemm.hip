@@ -1142,8 +1142,8 @@ template <int EPI, int DT>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
   __shared__ __attribute__((aligned(16))) uint16_t q_ep[4 * Q_EP_ELEMS];
-  int32_t* const s_h = reinterpret_cast<int32_t*>(qsm + Q_TAB_OFF);  // [Q_MAX_E + 1]
-  int32_t* const s_l = s_h + Q_MAX_E + 1;                             // [Q_MAX_E + 1]
+  int32_t* const s_h = reinterpret_cast<int32_t*>(qsm + Q_TAB_OFF);  // [Q_MAX_E + 1] heavy m-tile prefix
+  int32_t* const s_l = s_h + Q_MAX_E + 1;                             // [Q_MAX_E + 1] light m-tile prefix
   int32_t* const s_off = s_l + Q_MAX_E + 1;                           // [Q_MAX_E + 1] expert offsets
   int32_t* const s_tok = reinterpret_cast<int32_t*>(qsm + Q_TOK_OFF); // [2][Q_BM] activation rows
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, half = lane >> 5;
@@ -1162,22 +1162,22 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   const int n_my = first < wend ? (int)((wend - first + stride - 1) / stride) : 0;
   if (n_my == 0) return;  // block-uniform
 
-  // tile ordinal -> expert, first slot, rows, n-tile (m-tile list as in mtile_decode, offsets from LDS)
+  // tile ordinal -> expert, first slot, rows, n-tile (the m-tile list of
+  // mtile_decode: every full-size tile before every light remainder; tables in LDS)
   auto decode = [&](int ord) {
     int64_t mt, nt;
     walk.decode(first + (int64_t)ord * stride, mt, nt);
-    int e;
-    int64_t j;
+    int e, j;
     if (mt < s_h[E]) {
       e = prefix_owner(s_h, E, mt);
-      j = mt - s_h[e];
+      j = (int)mt - s_h[e];
     } else {
       e = prefix_owner(s_l, E, mt - s_h[E]);
       j = (s_off[e + 1] - s_off[e] + Q_BM - 1) / Q_BM - 1;
     }
     QTile t;
     t.e = uni(e);
-    t.m_beg = uni((int)(s_off[t.e] + j * Q_BM));
+    t.m_beg = uni(s_off[t.e] + j * Q_BM);
     const int rem = s_off[t.e + 1] - t.m_beg;
     t.valid = uni(rem < Q_BM ? rem : Q_BM);
     t.nt = uni((int)nt);
