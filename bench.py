@@ -228,15 +228,17 @@ def bench_moe_kernels(L, reps: int) -> dict:
     code = N.BF16
     qg = ew._ptrs("gate_up", dt)
     qd = ew._ptrs("down", dt)
+    qgt = ew._ptrs_t("gate_up")  # the grad-input GEMMs run on the transposed copies, as in the step
+    qdt = ew._ptrs_t("down")
     calls = {
         "gate_up_fwd": lambda: N.call("usaf_hip_moe_gate_up_fwd", x.data_ptr(), T, H, b.token_idx.data_ptr(),
                                       b.offsets.data_ptr(), S, E, I, *qg, code, gu.data_ptr(), act.data_ptr(), st),
         "down_fwd": lambda: N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *qd,
                                    code, y.data_ptr(), st),
-        "down_bwd": lambda: N.call("usaf_hip_moe_down_bwd", y.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(),
-                                   S, E, I, *qd, code, dgu.data_ptr(), st),
-        "gate_up_bwd": lambda: N.call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E,
-                                      H, *qg, code, dx.data_ptr(), st),
+        "down_bwd": lambda: N.call("usaf_hip_moe_down_bwd_t", y.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(),
+                                   S, E, I, *qdt, code, dgu.data_ptr(), st),
+        "gate_up_bwd": lambda: N.call("usaf_hip_moe_gate_up_bwd_t", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E,
+                                      H, *qgt, code, dx.data_ptr(), st),
     }
     flops = {"gate_up_fwd": 2 * S * H * 2 * I, "down_fwd": 2 * S * I * H, "down_bwd": 2 * S * H * I,
              "gate_up_bwd": 2 * S * 2 * I * H}

@@ -83,6 +83,20 @@ int usaf_hip_quantize_q4(const void* x, int32_t x_dtype, int64_t numel, int64_t 
 int usaf_hip_pack_scale_zero(const uint16_t* scale_f16, const uint16_t* zero_f16, int64_t n_groups,
                              uint32_t* scale_zero, void* stream);
 
+/*
+ * Transposed copy of a 4-bit [E, rows, cols] tensor (groups of 128 along cols) for
+ * the grad-input GEMMs, which contract over rows:
+ *   packed_t [E, cols, rows/2] int8: the code of element (r, c) at row c, nibble r
+ *            (even r in the low nibble, the codec's order applied to W^T)
+ *   sz_t     [E, cols/128, rows/2, 2] uint32: {s(r) | s(r+1) << 16, z(r) | z(r+1) << 16}
+ *            with s(r), z(r) the fp16 scale/zero of the group holding (r, c)
+ * Bits are copied unchanged, so W^T dequantizes to exactly the transposed
+ * values of W.  Needs cols % 128 == 0, rows % 64 == 0, 16-byte aligned code
+ * buffers.  A derived layout of this build; no counterpart in the reference.
+ */
+int usaf_hip_q4_transpose(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16, int64_t E,
+                          int64_t rows, int64_t cols, int8_t* packed_t, uint32_t* sz_t, void* stream);
+
 /* ---- routing and bucketing ------------------------------------------------ */
 
 /*
@@ -183,6 +197,17 @@ int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu, const int
 int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
                              const int8_t* wq, const uint32_t* wsz, const void* w16, int32_t dtype, void* dx_slots,
                              void* stream);
+
+/* The two grad-input GEMMs above on the transposed 4-bit copies (usaf_hip_q4_transpose
+ * of W_down [E, H, I] -> [E, I, H], of W_gate_up [E, 2I, H] -> [E, H, 2I]); same
+ * results up to fp32 summation order.  Replace the same autograd steps
+ * (qwen3moe_dml.py:58-61).  down_bwd_t needs I % 128 == 0 and H % 128 == 0;
+ * gate_up_bwd_t needs H % 128 == 0 and I % 64 == 0; both E <= 512. */
+int usaf_hip_moe_down_bwd_t(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S, int64_t E,
+                            int64_t I, const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype, void* dgu,
+                            void* stream);
+int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
+                               const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype, void* dx_slots, void* stream);
 
 /* ---- sparse gradient path and optimizer ----------------------------------- */
 

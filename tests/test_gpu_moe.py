@@ -406,3 +406,65 @@ def test_sddmm_ragged_experts(gpu_device, dtype):
     # experts without slots contribute exact zeros
     e0 = (act // (R * C)) == 0
     assert torch.equal(got[e0], init.double()[e0])
+
+
+# ---- transposed 4-bit copies for the grad-input GEMMs -----------------------------
+
+def test_q4_transpose_bit_exact(gpu_device):
+    _say("q4 transpose E=3 rows=128 cols=256")
+    E, R, C = 3, 128, 256
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn(E, R, C, generator=g) * 0.02).half()
+    qt = G.Q4Tensor.quantize(w.to(gpu_device))
+    codes_t, sz_t = qt.transposed()
+    torch.cuda.synchronize()
+    q = qt.q.cpu().numpy().view(np.uint8).reshape(E, R, C // 2)
+    codes = np.stack([q & 15, q >> 4], axis=-1).reshape(E, R, C)           # element (r, c)
+    got = codes_t.cpu().numpy().view(np.uint8).reshape(E, C, R // 2)
+    got_codes = np.stack([got & 15, got >> 4], axis=-1).reshape(E, C, R)   # element (c, r)
+    assert np.array_equal(got_codes, codes.transpose(0, 2, 1))
+    s = qt.s.cpu().numpy().view(np.uint16).reshape(E, R, C // 128).astype(np.uint32)
+    z = qt.z.cpu().numpy().view(np.uint16).reshape(E, R, C // 128).astype(np.uint32)
+    words = sz_t.cpu().numpy().view(np.uint32).reshape(E, C // 128, R // 2, 2)
+    exp_s = (s[:, 0::2, :] | (s[:, 1::2, :] << 16)).transpose(0, 2, 1)
+    exp_z = (z[:, 0::2, :] | (z[:, 1::2, :] << 16)).transpose(0, 2, 1)
+    assert np.array_equal(words[..., 0], exp_s)
+    assert np.array_equal(words[..., 1], exp_z)
+
+
+@pytest.mark.parametrize("E,H,I,T,k", [(128, 2048, 768, 4096, 8), (3, 384, 384, 333, 2)])
+def test_backward_transposed_vs_direct(gpu_device, E, H, I, T, k):
+    """The grad-input GEMMs on the transposed copies against the kernels that read
+    the original layout (same dequantized weights; fp32 summation order differs)."""
+    _say(f"bwd transposed vs direct E={E} H={H} I={I} T={T} k={k}")
+    from usaf_amd import _native as N
+    dev, dt = gpu_device, torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(5)
+    qg = G.Q4Tensor.quantize((torch.randn(E, 2 * I, H, device=dev, generator=g) * 0.02).half())
+    qd = G.Q4Tensor.quantize((torch.randn(E, H, I, device=dev, generator=g) * 0.02).half())
+    ew = G.ExpertWeights(qg, qd)
+    w, _ = G.route_topk(torch.randn(T, E, device=dev, generator=g), k, False, dt, with_probs=False)
+    b = G.bucket_by_expert(w)
+    S = b.n_slots
+    dcur = torch.randn(S, H, device=dev, generator=g).to(dt)
+    gu = torch.randn(S, 2 * I, device=dev, generator=g).to(dt)
+    st, code = N.stream_ptr(dev), N.dtype_code(dt)
+    dgu_a, dgu_b = torch.empty(S, 2 * I, dtype=dt, device=dev), torch.empty(S, 2 * I, dtype=dt, device=dev)
+    N.call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
+           *ew._ptrs("down", dt), code, dgu_a.data_ptr(), st)
+    tq = ew._ptrs_t("down")
+    assert tq is not None
+    N.call("usaf_hip_moe_down_bwd_t", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I, *tq,
+           code, dgu_b.data_ptr(), st)
+    dx_a, dx_b = torch.empty(S, H, dtype=dt, device=dev), torch.empty(S, H, dtype=dt, device=dev)
+    N.call("usaf_hip_moe_gate_up_bwd", dgu_a.data_ptr(), I, b.offsets.data_ptr(), S, E, H,
+           *ew._ptrs("gate_up", dt), code, dx_a.data_ptr(), st)
+    tq = ew._ptrs_t("gate_up")
+    assert tq is not None
+    N.call("usaf_hip_moe_gate_up_bwd_t", dgu_a.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *tq, code,
+           dx_b.data_ptr(), st)
+    torch.cuda.synchronize()
+    assert rel_err(dgu_b, dgu_a) <= 1e-2
+    assert rel_err(dx_b, dx_a) <= 1e-2
+    # most elements agree exactly after the bf16 rounding
+    assert float((dx_b == dx_a).float().mean()) > 0.9

@@ -35,6 +35,7 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_dequant_q4": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i32, _c_p],
     "usaf_hip_quantize_q4": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],
     "usaf_hip_pack_scale_zero": [_c_p, _c_p, _c_i64, _c_p, _c_p],
+    "usaf_hip_q4_transpose": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p],
     "usaf_hip_route_topk": [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p, _c_p],
     "usaf_hip_route_topk_bwd": [_c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p],
     "usaf_hip_bucket_by_expert": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p],
@@ -47,6 +48,8 @@ _SIGNATURES: dict[str, list] = {
                               _c_p],
     "usaf_hip_moe_gate_up_bwd": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p,
                                  _c_p],
+    "usaf_hip_moe_down_bwd_t": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_p],
+    "usaf_hip_moe_gate_up_bwd_t": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_p],
     "usaf_hip_gather_transpose": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
     "usaf_hip_sddmm_masked": [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p,
                               _c_p],

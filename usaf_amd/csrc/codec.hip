@@ -237,8 +237,71 @@ __global__ __launch_bounds__(256) void pack_scale_zero_kernel(const uint16_t* __
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     sz[i] = (uint32_t)s[i] | ((uint32_t)z[i] << 16);
 }
+
+// Transposed copy of a [E, rows, cols] 4-bit tensor (groups of 128 along cols)
+// for the grad-input GEMMs, which contract over rows:
+//   qT[e][c][r]        the code of element (r, c); two per byte along r, even r
+//                      in the low nibble (the reference's nibble order, on W^T)
+//   szT[e][c/128][r/2] = { s(r) | s(r+1) << 16, z(r) | z(r+1) << 16 }
+// with s(r), z(r) the fp16 scale/zero of the group holding (r, c).  Codes and
+// scale/zero bits are copied unchanged, so W^T dequantizes to exactly the
+// transposed values of W.  One block: 64 rows x 128 columns of one expert.
+__global__ __launch_bounds__(256) void q4_transpose_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
+                                                           const uint16_t* __restrict__ z, int64_t rows, int64_t cols,
+                                                           uint8_t* __restrict__ qT, uint32_t* __restrict__ szT) {
+  __shared__ __align__(16) uint8_t tile[64][80];  // 64 rows x 64 code bytes (128 columns), padded
+  const int64_t e = blockIdx.z, r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 128;
+  const int t = threadIdx.x;
+  {
+    const int row = t >> 2, part = t & 3;
+    const uint4 v = *reinterpret_cast<const uint4*>(q + (((e * rows + r0 + row) * cols + c0) >> 1) + part * 16);
+    *reinterpret_cast<uint4*>(&tile[row][part * 16]) = v;
+  }
+  __syncthreads();
+  {
+    // column c0 + c, rows r0 + 32 half + [0, 32): 16 output bytes
+    const int c = t >> 1, half = t & 1, sh = (c & 1) * 4;
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int r = 32 * half + 8 * k + 2 * b;
+        const uint32_t lo = (tile[r][c >> 1] >> sh) & 0xFu, hi = (tile[r + 1][c >> 1] >> sh) & 0xFu;
+        acc |= (lo | (hi << 4)) << (8 * b);
+      }
+      w[k] = acc;
+    }
+    *reinterpret_cast<uint4*>(qT + (((e * cols + c0 + c) * rows + r0) >> 1) + half * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  if (t < 32) {
+    const int64_t gpr = cols / 128, gc = c0 / 128;
+    const int64_t ga = (e * rows + r0 + 2 * t) * gpr + gc, gb = ga + gpr;  // groups of rows r, r + 1
+    uint32_t* dst = szT + ((e * gpr + gc) * (rows / 2) + r0 / 2 + t) * 2;
+    dst[0] = (uint32_t)s[ga] | ((uint32_t)s[gb] << 16);
+    dst[1] = (uint32_t)z[ga] | ((uint32_t)z[gb] << 16);
+  }
+}
 }  // namespace
 }  // namespace usaf
+
+extern "C" int usaf_hip_q4_transpose(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
+                                     int64_t E, int64_t rows, int64_t cols, int8_t* packed_t, uint32_t* sz_t,
+                                     void* stream) {
+  if (E <= 0 || rows <= 0 || cols <= 0) return set_error(USAF_ERR_INVALID, "q4_transpose: need E, rows, cols > 0");
+  if (cols % 128 != 0 || rows % 64 != 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "q4_transpose: needs cols %% 128 == 0 and rows %% 64 == 0 (rows=%lld, cols=%lld)",
+                     (long long)rows, (long long)cols);
+  if (!packed || !scale_f16 || !zero_f16 || !packed_t || !sz_t) return set_error(USAF_ERR_INVALID, "q4_transpose: null pointer");
+  if (((uintptr_t)packed & 15) || ((uintptr_t)packed_t & 15))
+    return set_error(USAF_ERR_INVALID, "q4_transpose: code buffers must be 16-byte aligned");
+  if (E > 65535 || rows / 64 > 65535) return set_error(USAF_ERR_INVALID, "q4_transpose: too large");
+  const dim3 grid((unsigned)(cols / 128), (unsigned)(rows / 64), (unsigned)E);
+  q4_transpose_kernel<<<grid, 256, 0, as_stream(stream)>>>((const uint8_t*)packed, scale_f16, zero_f16, rows, cols,
+                                                          (uint8_t*)packed_t, sz_t);
+  return check_launch("q4_transpose");
+}
 
 extern "C" int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
                                    int64_t n_groups, int64_t packed_cols, int64_t group_size, int64_t numel,

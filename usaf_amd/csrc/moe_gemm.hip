@@ -1138,7 +1138,10 @@ struct QTile {
   int e, valid, m_beg, nt;  // all wave-uniform
 };
 
-template <int EPI, int DT>
+// BT: the weight is a transposed copy (usaf_hip_q4_transpose): codes along k as
+// usual, but every k has its own scale/zero, read as {s(k) | s(k+1) << 16,
+// z(k) | z(k+1) << 16} pairs from wsz (one 128-column group of n per 256 B per k-step).
+template <int EPI, int DT, bool BT>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
   __shared__ __attribute__((aligned(16))) uint16_t q_ep[4 * Q_EP_ELEMS];
@@ -1158,6 +1161,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   }
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
   const TileWalk walk(s_h[E] + s_l[E], n_nt);
+  const int n_grp = (int)(g.N / 128);  // BT: 128-column groups of n
   const int64_t first = walk.first(), stride = walk.step(), wend = walk.end();
   const int n_my = first < wend ? (int)((wend - first + stride - 1) / stride) : 0;
   if (n_my == 0) return;  // block-uniform
@@ -1211,7 +1215,15 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     const int64_t base = (int64_t)t.e * g.w_rows;
     c_off0 = (uint32_t)((((base + wrow(t, b0)) * g.K) >> 1) + 16 * (tid & 1));
     c_off1 = (uint32_t)((((base + wrow(t, b1)) * g.K) >> 1) + 16 * (tid & 1));
-    z_off = (uint32_t)((((base + wrow(t, tid)) * g.K) >> 7) * 4);
+    if constexpr (BT) {
+      // thread t fetches word t & 63 of group (tile's first group + ((t >> 6) & 1));
+      // threads 128..255 repeat 0..127 into the unused upper half
+      int grp = t.nt * (Q_BN / 128) + ((tid >> 6) & 1);
+      grp = grp < n_grp ? grp : n_grp - 1;
+      z_off = (uint32_t)((((int64_t)t.e * n_grp + grp) * (g.K / 2) * 2 + (tid & 63)) * 4);
+    } else {
+      z_off = (uint32_t)((((base + wrow(t, tid)) * g.K) >> 7) * 4);
+    }
   };
   // with a row map, the activation rows of tile t are fetched into token buffer
   // buf by a DMA (visible to all threads after the next barrier); without one
@@ -1248,7 +1260,8 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       dma16(base + (d ? c_off1 : c_off0), sc + (d * 256 + wave * 64) * 16);
     } else if (d == 2) {
       uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
-      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wsz) + (c_kt_u >> 1) * 4;
+      // per k-step: one scale|zero word per weight row, or (BT) 32 k-pairs x 2 words per group
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wsz) + (BT ? c_kt_u * 256 : (c_kt_u >> 1) * 4);
       dma4(base + z_off, sc + Q_C_BYTES + wave * 64 * 4);
     } else {
       const int c = d - 3;
@@ -1297,26 +1310,49 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // ---- weight fragments: wf[slot][column block][sub-step j]; lane half h holds
   //      k = 32h + 8j + [0, 8) of weight row 32cb + l32 of the wave ----
   u32x4 wf[2][2][4];
-  auto codes_read = [&](int stage, u32x4 (&cq)[2], uint32_t (&csz)[2]) {
+  // codes of the lane's weight rows and their scale|zero: one pair per row, or
+  // (BT) the 16 k-pairs {s2, z2} of k = 32 half + [0, 32) of the wave's group
+  // (a wave's 64 columns never straddle a 128-column group)
+  auto codes_read = [&](int stage, u32x4 (&cq)[2], uint32_t (&csz)[2], u32x4 (&kz)[8]) {
     const uint8_t* sc = qsm + stage * Q_STAGE + Q_A_BYTES;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int b = 64 * wave + 32 * cb + l32;
       cq[cb] = *reinterpret_cast<const u32x4*>(sc + (2 * b + half) * 16);
-      csz[cb] = *reinterpret_cast<const uint32_t*>(sc + Q_C_BYTES + b * 4);
+      if constexpr (!BT) csz[cb] = *reinterpret_cast<const uint32_t*>(sc + Q_C_BYTES + b * 4);
     }
+    if constexpr (BT) {
+      const uint8_t* zg = sc + Q_C_BYTES + ((wave >> 1) * 64 + 32 * half) * 4;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kz[i] = *reinterpret_cast<const u32x4*>(zg + 16 * i);
+    }
+  };
+  // k-pair p4 (= 4 wd + q, k = 32 half + 2 p4) of the BT words: {s2, z2}
+  auto kz_pair = [&](const u32x4 (&kz)[8], int p4, f16x2& s2, f16x2& z2) {
+    const u32x4 w = kz[p4 >> 1];
+    s2 = __builtin_bit_cast(f16x2, (p4 & 1) ? w.z : w.x);
+    z2 = __builtin_bit_cast(f16x2, (p4 & 1) ? w.w : w.y);
   };
   auto dequant_all = [&](auto bs_c, int stage) {
     constexpr int BS = decltype(bs_c)::value;
-    u32x4 cq[2];
+    u32x4 cq[2], kz[8];
     uint32_t csz[2];
-    codes_read(stage, cq, csz);
+    codes_read(stage, cq, csz, kz);
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const f16x2 s2 = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
-      const f16x2 z2 = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
+      if constexpr (BT) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wf[BS][cb][j] = dq8<DT>(cq[cb][j], s2, z2);
+        for (int p = 0; p < 16; ++p) {
+          f16x2 s2, z2;
+          kz_pair(kz, p, s2, z2);
+          wf[BS][cb][p >> 2][p & 3] = dq_pair<DT>(cq[cb][p >> 2], p & 3, s2, z2);
+        }
+      } else {
+        const f16x2 s2 = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
+        const f16x2 z2 = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wf[BS][cb][j] = dq8<DT>(cq[cb][j], s2, z2);
+      }
     }
   };
 
@@ -1333,9 +1369,9 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     constexpr int PPR = (32 + R - 2) / (R - 1);  // weight pairs dequantized per region (regions 1..R-1)
     constexpr int DPR = (Q_DMAS + R - 1) / R;    // DMAs issued per region
     pre_step();
-    u32x4 cq[2];
+    u32x4 cq[2], kz[8];
     uint32_t csz[2];
-    codes_read(s1, cq, csz);
+    codes_read(s1, cq, csz, kz);
     const uint8_t* sa = qsm + s0 * Q_STAGE;
     auto frag = [&](int f) -> u32x4 {
       const int i = f % NRB, j = f / NRB;
@@ -1364,11 +1400,18 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
           const int p = (r - 1) * PPR + pp;
           if (p < 32) {
             const int cb = p >> 4, wd = (p >> 2) & 3, q = p & 3;
-            if ((p & 15) == 0) {
-              s2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
-              z2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
+            uint32_t v;
+            if constexpr (BT) {
+              f16x2 s2, z2;
+              kz_pair(kz, p & 15, s2, z2);
+              v = dq_pair<DT>(cq[cb][wd], q, s2, z2);
+            } else {
+              if ((p & 15) == 0) {
+                s2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
+                z2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
+              }
+              v = dq_pair<DT>(cq[cb][wd], q, s2v[cb], z2v[cb]);
             }
-            uint32_t v = dq_pair<DT>(cq[cb][wd], q, s2v[cb], z2v[cb]);
             asm volatile("" : "+v"(v));  // computed here, next to the MFMAs, not sunk to its first use
             wf[BS ^ 1][cb][wd][q] = v;
           }
@@ -1440,6 +1483,56 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
           }
         }
       }
+    } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+      // acc = d(act) for columns n of [0, I): with the saved gu (g = gate, u = up),
+      //   d(up)   = DT(da * DT(silu(g)))
+      //   d(gate) = DT(DT(da * u) * sig * (1 + g (1 - sig))),  da = DT(acc), sig = sigmoid(g)
+      // into dgu[m, n] and dgu[m, I + n].  da goes through the LDS tile; the
+      // math then runs on 16-byte row chunks (8 columns) next to coalesced gu
+      // loads and dgu stores, in a loop that is not unrolled (code size)
+      const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 64;
+      if (n0 >= g.N) return;  // N % 64 == 0
+#pragma unroll
+      for (int i = 0; i < NRB; ++i) {
+        if (32 * i >= t.valid) break;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            stage4(32 * cb + 8 * q + 4 * half, pack2<DT>(acc[i][cb][4 * q], acc[i][cb][4 * q + 1]),
+                   pack2<DT>(acc[i][cb][4 * q + 2], acc[i][cb][4 * q + 3]));
+        const int rows_left = t.valid - 32 * i;
+        const int ch = (lane & 7) * 8;
+#pragma unroll 1
+        for (int p = 0; p < 4; ++p) {
+          const int rr = (lane >> 3) + 8 * p;
+          if (rr < rows_left) {
+            const int64_t m = t.m_beg + 32 * i + rr;
+            const u32x4 dv = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
+            const u32x4 gv = *reinterpret_cast<const u32x4*>(g.aux + m * g.ld_aux + n0 + ch);
+            const u32x4 uv = *reinterpret_cast<const u32x4*>(g.aux + m * g.ld_aux + g.inter + n0 + ch);
+            uint32_t dgw[4], duw[4];
+#pragma unroll
+            for (int w2 = 0; w2 < 4; ++w2) {
+              const f32x2 da = unpack2<DT>(dv[w2]), gt = unpack2<DT>(gv[w2]), up = unpack2<DT>(uv[w2]);
+              float dg[2], du[2];
+#pragma unroll
+              for (int c = 0; c < 2; ++c) {
+                const float gx = c ? gt.y : gt.x, ux = c ? up.y : up.x, ax = c ? da.y : da.x;
+                const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * gx));
+                const float sg = round_to<DT>(gx * sig);
+                const float dsil = round_to<DT>(ax * ux);
+                dg[c] = (dsil * sig) * (1.0f + gx * (1.0f - sig));
+                du[c] = ax * sg;
+              }
+              dgw[w2] = pack2<DT>(dg[0], dg[1]);
+              duw[w2] = pack2<DT>(du[0], du[1]);
+            }
+            *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n0 + ch) = u32x4{dgw[0], dgw[1], dgw[2], dgw[3]};
+            *reinterpret_cast<u32x4*>(g.out + m * g.ldo + g.inter + n0 + ch) = u32x4{duw[0], duw[1], duw[2], duw[3]};
+          }
+        }
+      }
     } else {
       const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 64;
       if (n0 >= g.N) return;  // N % 64 == 0: a wave's 64 columns are all valid or none
@@ -1453,14 +1546,16 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
             stage4(32 * cb + 8 * q + 4 * half, pack2<DT>(acc[i][cb][4 * q], acc[i][cb][4 * q + 1]),
                    pack2<DT>(acc[i][cb][4 * q + 2], acc[i][cb][4 * q + 3]));
         // 32 rows x 128 B: lane l takes 16-byte chunk l & 7 of row (l >> 3) + 8p
+        // (a wave-uniform row base plus one 32-bit lane offset)
+        uint8_t* const rowbase = reinterpret_cast<uint8_t*>(g.out + ((int64_t)t.m_beg + 32 * i) * g.ldo + n0);
+        const uint32_t loff = (uint32_t)(((lane >> 3) * g.ldo + (lane & 7) * 8) * 2);
+        const int rows_left = t.valid - 32 * i;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const int rr = (lane >> 3) + 8 * p;
-          if (32 * i + rr < t.valid) {
-            const int ch = (lane & 7) * 8;
-            *reinterpret_cast<u32x4*>(g.out + ((int64_t)t.m_beg + 32 * i + rr) * g.ldo + n0 + ch) =
-                *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
-          }
+          if (rr < rows_left)
+            *reinterpret_cast<u32x4*>(rowbase + (size_t)p * 16 * g.ldo + loff) =
+                *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + (lane & 7) * 8);
         }
       }
     }
@@ -1544,17 +1639,36 @@ int launch_nk_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   return USAF_OK;
 }
 
-template <int EPI, int DT>
+template <int EPI, int DT, bool BT = false>
 int launch_q4_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT, BT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQSmemBytes);
     (void)hipGetLastError();
     attr_set = true;
   }
-  moe_gemm_q4_kernel<EPI, DT><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
+  moe_gemm_q4_kernel<EPI, DT, BT><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
   return USAF_OK;
+}
+
+// grad-input GEMMs on transposed 4-bit weights (always the LDS-DMA kernel)
+template <int EPI>
+int launch_q4t(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_total, hipStream_t st, const char* what) {
+  if (g.E > Q_MAX_E) return set_error(USAF_ERR_UNSUPPORTED, "%s: needs E <= %d", what, Q_MAX_E);
+  if (((uintptr_t)g.A & 15) || g.lda % 8 != 0)
+    return set_error(USAF_ERR_INVALID, "%s: activations must be 16-byte aligned rows", what);
+  if (a_rows_total * g.lda * 2 >= ((int64_t)1 << 32) || (int64_t)g.E * g.w_rows * g.w_cols / 2 >= ((int64_t)1 << 32))
+    return set_error(USAF_ERR_UNSUPPORTED, "%s: operands beyond 4 GiB", what);
+  int64_t blocks = (int64_t)device_cu_count();
+  if (blocks > max_tiles) blocks = max_tiles;
+  if (blocks < 1) blocks = 1;
+  int rc;
+  if (dt == USAF_BF16) rc = launch_q4_one<EPI, USAF_BF16, true>(g, (unsigned)blocks, st);
+  else if (dt == USAF_F16) rc = launch_q4_one<EPI, USAF_F16, true>(g, (unsigned)blocks, st);
+  else return set_error(USAF_ERR_INVALID, "%s: dtype must be fp16 or bf16", what);
+  if (rc) return rc;
+  return check_launch(what);
 }
 
 template <int EPI>
@@ -1716,4 +1830,42 @@ extern "C" int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_
   g.out = (uint16_t*)dx_slots; g.ldo = H;
   const int64_t max_tiles = (S / BM + E) * (H / BN);
   return launch_gemm<BMODE_KN, EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_gate_up_bwd");
+}
+
+// dgu from dcur @ W_down[e] on the transposed copy W_down^T [E, I, H].
+extern "C" int usaf_hip_moe_down_bwd_t(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S,
+                                       int64_t E, int64_t I, const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype,
+                                       void* dgu, void* stream) {
+  if (int rc = check_common("moe_down_bwd_t", S, E, offsets, wq_t, wsz_t, nullptr)) return rc;
+  if (I % 128 != 0 || I <= 0 || H % 128 != 0 || H <= 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_down_bwd_t: needs I %% 128 == 0 and H %% 128 == 0 (I=%lld, H=%lld)",
+                     (long long)I, (long long)H);
+  if (S == 0) return clear_error();
+  if (!dcur || !gu || !dgu) return set_error(USAF_ERR_INVALID, "moe_down_bwd_t: null pointer");
+  GemmArgs g{};
+  g.A = (const uint16_t*)dcur; g.lda = H; g.a_rows = nullptr;
+  g.wq = (const uint8_t*)wq_t; g.wsz = wsz_t; g.w16 = nullptr; g.w_rows = I; g.w_cols = H;
+  g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
+  g.out = (uint16_t*)dgu; g.ldo = 2 * I; g.aux = (const uint16_t*)gu; g.ld_aux = 2 * I;
+  const int64_t max_tiles = (S / Q_BM + E) * ((I + Q_BN - 1) / Q_BN);
+  return launch_q4t<EPI_SWIGLU_BWD>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_bwd_t");
+}
+
+// dx_slots from dgu @ W_gate_up[e] on the transposed copy W_gate_up^T [E, H, 2I].
+extern "C" int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E,
+                                          int64_t H, const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype,
+                                          void* dx_slots, void* stream) {
+  if (int rc = check_common("moe_gate_up_bwd_t", S, E, offsets, wq_t, wsz_t, nullptr)) return rc;
+  if (H % 128 != 0 || H <= 0 || I % 64 != 0 || I <= 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_bwd_t: needs H %% 128 == 0 and I %% 64 == 0 (H=%lld, I=%lld)",
+                     (long long)H, (long long)I);
+  if (S == 0) return clear_error();
+  if (!dgu || !dx_slots) return set_error(USAF_ERR_INVALID, "moe_gate_up_bwd_t: null pointer");
+  GemmArgs g{};
+  g.A = (const uint16_t*)dgu; g.lda = 2 * I; g.a_rows = nullptr;
+  g.wq = (const uint8_t*)wq_t; g.wsz = wsz_t; g.w16 = nullptr; g.w_rows = H; g.w_cols = 2 * I;
+  g.N = H; g.K = 2 * I; g.inter = I; g.offsets = offsets; g.E = (int)E;
+  g.out = (uint16_t*)dx_slots; g.ldo = H;
+  const int64_t max_tiles = (S / Q_BM + E) * ((H + Q_BN - 1) / Q_BN);
+  return launch_q4t<EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_gate_up_bwd_t");
 }

@@ -31,6 +31,7 @@ class Q4Tensor:
     shape: torch.Size
     group_size: int = 128
     _sz: Optional[torch.Tensor] = field(default=None, repr=False, compare=False)
+    _t: Optional[Tuple[torch.Tensor, torch.Tensor]] = field(default=None, repr=False, compare=False)
 
     @classmethod
     def from_entry(cls, entry: Any, device=None, group_size: int = 128) -> "Q4Tensor":
@@ -84,11 +85,32 @@ class Q4Tensor:
             self._sz = sz
         return self._sz
 
+    def transposed(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(codes int8 [E, cols, rows/2], scale/zero int32 [E, cols/128, rows/2, 2]):
+        the copy of W^T per expert that the grad-input GEMMs read (usaf_hip_q4_transpose),
+        built once on the tensor's device and kept with it."""
+        if self._t is None or self._t[0].device != self.q.device:
+            E, rows, cols = (int(d) for d in self.shape)
+            qt = torch.empty(E * cols * rows // 2, dtype=torch.int8, device=self.q.device)
+            szt = torch.empty(E * (cols // 128) * (rows // 2) * 2, dtype=torch.int32, device=self.q.device)
+            N.call("usaf_hip_q4_transpose", self.q.data_ptr(), self.s.data_ptr(), self.z.data_ptr(), E, rows, cols,
+                   qt.data_ptr(), szt.data_ptr(), N.stream_ptr(self.q.device))
+            self._t = (qt, szt)
+        return self._t
+
+    def transposed_ok(self) -> bool:
+        """True when the transposed copy exists for this shape (rows % 64 == 0 on top of fused_ok)."""
+        return self.fused_ok() and int(self.shape[1]) % 64 == 0
+
     def fused_ok(self) -> bool:
         """True when the layout is the one the fused GEMMs read directly:
         group size 128 along whole rows (last dim % 128 == 0)."""
         return self.group_size == 128 and len(self.shape) == 3 and int(self.shape[-1]) % 128 == 0 \
             and self.q.shape[1] == 64
+
+
+# grad-input GEMMs on the transposed copies: shapes and expert counts they serve
+_T_MAX_E = 512
 
 
 class ExpertWeights:
@@ -108,6 +130,20 @@ class ExpertWeights:
     @property
     def is_q4(self) -> bool:
         return isinstance(self.gate_up, Q4Tensor)
+
+    def _ptrs_t(self, which):
+        """(codes, scale/zero) pointers of the transposed 4-bit copy for the
+        grad-input GEMM of `which`, or None when that path does not apply
+        (dense weights, unsupported shapes)."""
+        w = self.gate_up if which == "gate_up" else self.down
+        if not isinstance(w, Q4Tensor) or not w.transposed_ok() or self.E > _T_MAX_E:
+            return None
+        # down_bwd_t: N = I, K = H; gate_up_bwd_t: N = H, K = 2I
+        n, k = (self.I, self.H) if which == "down" else (self.H, 2 * self.I)
+        if n % 128 or k % 128:
+            return None
+        qt, szt = w.transposed()
+        return qt.data_ptr(), szt.data_ptr()
 
     def _ptrs(self, which, dtype: torch.dtype):
         w = self.gate_up if which == "gate_up" else self.down
@@ -294,17 +330,27 @@ class RoutedExpertsFn(torch.autograd.Function):
         N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
                b.slot_w.data_ptr(), b.offsets.data_ptr(), S, E, H, code, dcur.data_ptr(), dweights.data_ptr(), st)
         dgu = torch.empty(S, 2 * I, dtype=dt, device=dev)
-        q, sz, w16 = ew._ptrs("down", dt)
-        _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
-                   q, sz, w16, code, dgu.data_ptr(), st)
+        tq = ew._ptrs_t("down")
+        if tq is not None:
+            _gemm_call("usaf_hip_moe_down_bwd_t", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
+                       *tq, code, dgu.data_ptr(), st)
+        else:
+            q, sz, w16 = ew._ptrs("down", dt)
+            _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
+                       q, sz, w16, code, dgu.data_ptr(), st)
         if capture is not None:
             _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt)
         if want_dn:
             _dense_weight_grad(d_wdn, dcur, act, None, b)
         dx_slots = torch.empty(S, H, dtype=dt, device=dev)
-        q, sz, w16 = ew._ptrs("gate_up", dt)
-        _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
-                   code, dx_slots.data_ptr(), st)
+        tq = ew._ptrs_t("gate_up")
+        if tq is not None:
+            _gemm_call("usaf_hip_moe_gate_up_bwd_t", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *tq,
+                       code, dx_slots.data_ptr(), st)
+        else:
+            q, sz, w16 = ew._ptrs("gate_up", dt)
+            _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
+                       code, dx_slots.data_ptr(), st)
         if capture is not None:
             _capture(capture, "gate_up_proj", dgu, hs, b.token_idx, b, (E, 2 * I, H), dt)
         if want_gu:
