@@ -211,6 +211,36 @@ int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offset
 
 /* ---- sparse gradient path and optimizer ----------------------------------- */
 
+/*
+ * Per-expert blocked slot-major operands for the sampled gradient: expert e's
+ * slots form a contiguous block of C rows of ld_e = round_up(S_e, 8) elements at
+ * element offset C * sum_{e' < e} ld_e', padding columns zero:
+ *   out_blk[C * P[e] + c * ld_e + j] = in[rows ? rows[s0_e + j] : s0_e + j, c]   (j < S_e)
+ * usaf_hip_blocked_elems bounds the element count (C * (S + 7 E)).  Needs C, ld_in
+ * % 8 == 0, 16-byte aligned bases, E <= 1024.  A layout of this build: the
+ * operands of the dense per-expert weight grads qwen3moe_dml.py:44-47 reads.
+ */
+int64_t usaf_hip_blocked_elems(int64_t S, int64_t E, int64_t C);
+/* The layout table of one bucketing of S slots, int32 [usaf_hip_blocked_table_elems(S, E)]:
+ * P[e] (padded slots before expert e), the 64-slot chunk counts before e, then the
+ * owning expert of each 64-slot chunk; built once and shared by every blocked
+ * operand and sampled gradient of that bucketing. */
+int64_t usaf_hip_blocked_table_elems(int64_t S, int64_t E);
+int usaf_hip_blocked_layout(const int32_t* offsets, int64_t E, int64_t S, int32_t* table, void* stream);
+int usaf_hip_gather_transpose_blocked(const void* in, int64_t ld_in, const int32_t* rows, const int32_t* offsets,
+                                      const int32_t* table, int64_t S, int64_t E, int64_t C, void* out_blk,
+                                      void* stream);
+
+/*
+ * usaf_hip_sddmm_masked on blocked operands (row_blk: R rows per expert block,
+ * col_blk: C rows per expert block, both from usaf_hip_gather_transpose_blocked
+ * with the same layout table).  Replaces the same reference steps (qwen3moe_dml.py:44-56,
+ * moe_loader.py:564-578).
+ */
+int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, const int32_t* table, int64_t E, int64_t R,
+                           int64_t C, int64_t n_pos, const int32_t* row_code, const int32_t* col_idx,
+                           const int64_t* pos_map, int32_t dtype, float* compact, void* stream);
+
 /* out[c, s] = in[rows ? rows[s] : s, c] for 16-bit [.., C] -> [C, S] (slot-major operands).
  * When C, ld_in and ld_out are multiples of 8 and both bases 16-byte aligned, the
  * transposed rows are written as 16-byte vectors and out[c, S .. round_up(S, 8)) is

@@ -468,3 +468,82 @@ def test_backward_transposed_vs_direct(gpu_device, E, H, I, T, k):
     assert rel_err(dx_b, dx_a) <= 1e-2
     # most elements agree exactly after the bf16 rounding
     assert float((dx_b == dx_a).float().mean()) > 0.9
+
+
+# ---- per-expert blocked operands for the sampled gradient ---------------------------
+
+@pytest.mark.parametrize("gathered", [False, True])
+def test_gather_transpose_blocked_bit_exact(gpu_device, gathered):
+    _say(f"gather_transpose_blocked gathered={gathered}")
+    g = torch.Generator().manual_seed(21)
+    counts = [0, 3, 700, 129, 8, 1, 256, 0]
+    E, C = len(counts), 136
+    offs = [0]
+    for c in counts:
+        offs.append(offs[-1] + c)
+    S = offs[-1]
+    T = S + 9 if gathered else S
+    x = torch.randn(T, C, generator=g).bfloat16()
+    rows = torch.randint(0, T, (S,), generator=g, dtype=torch.int32) if gathered else None
+    offsets = torch.tensor(offs, dtype=torch.int32, device=gpu_device)
+    blk = G.slot_blocked(x.to(gpu_device), offsets, S, None if rows is None else rows.to(gpu_device))
+    torch.cuda.synchronize()
+    # layout table: padded-slot prefix, 64-slot chunk prefix, chunk -> expert map
+    lds = [(offs[e + 1] - offs[e] + 7) // 8 * 8 for e in range(E)]
+    pre, cpre, owner = [0], [0], []
+    for e in range(E):
+        pre.append(pre[-1] + lds[e])
+        cpre.append(cpre[-1] + (lds[e] + 63) // 64)
+        owner += [e] * ((lds[e] + 63) // 64)
+    table = blk.table.cpu().tolist()
+    assert table[: 2 * (E + 1)] == pre + cpre
+    n_map = len(table) - 2 * (E + 1)
+    assert table[2 * (E + 1):] == owner + [-1] * (n_map - len(owner))
+    got = blk.data.cpu().view(torch.int16)
+    src = x[rows.long()] if gathered else x[:S]
+    pos = 0
+    for e in range(E):
+        s0, s1 = offs[e], offs[e + 1]
+        ld = (s1 - s0 + 7) // 8 * 8
+        block = got[pos: pos + C * ld].reshape(C, ld)
+        assert torch.equal(block[:, : s1 - s0], src[s0:s1].t().contiguous().view(torch.int16))
+        assert torch.all(block[:, s1 - s0:] == 0)
+        pos += C * ld
+    assert pos <= got.numel()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sddmm_blocked_ragged_experts(gpu_device, dtype):
+    _say(f"sddmm blocked ragged experts {dtype}")
+    g = torch.Generator().manual_seed(12)
+    counts = [0, 3, 700, 129, 8, 1, 256]
+    E, R, C = len(counts), 40, 48
+    offs = [0]
+    for c in counts:
+        offs.append(offs[-1] + c)
+    S = offs[-1]
+    dy = torch.randn(S, R, generator=g).to(dtype)
+    x = torch.randn(S + 4, C, generator=g).to(dtype)
+    rows = torch.randperm(S + 4, generator=g)[:S].to(torch.int32)          # gathered column operand
+    numel = E * R * C
+    act = torch.randperm(numel, generator=g)[: numel // 5]                 # unsorted: pos_map path
+    store = SparseGradStore({"L.w": act}, {"L.w": (E, R, C)}, device=gpu_device)
+    init = torch.randn(act.numel(), generator=g)
+    store.compact["L.w"].copy_(init)
+    offsets = torch.tensor(offs, dtype=torch.int32, device=gpu_device)
+    tb = G.blocked_layout(offsets, S)
+    rb = G.slot_blocked(dy.to(gpu_device), offsets, S, table=tb)
+    cb = G.slot_blocked(x.to(gpu_device), offsets, S, rows.to(gpu_device), table=tb)
+    store.add_sampled("L.w", rb, cb, offsets, dtype)
+    torch.cuda.synchronize()
+    xs = x[rows.long()]
+    dw = torch.zeros(E, R, C, dtype=torch.float64)
+    for e in range(E):
+        s0, s1 = offs[e], offs[e + 1]
+        dw[e] = dy[s0:s1].double().t() @ xs[s0:s1].double()
+    ref = init.double() + dw.reshape(-1)[act].to(dtype).double()
+    got = store.compact["L.w"].cpu().double()
+    assert torch.isfinite(got).all()
+    assert rel_err(got - init.double(), ref - init.double()) <= TOL[dtype]
+    e0 = (act // (R * C)) == 0
+    assert torch.equal(got[e0], init.double()[e0])

@@ -276,9 +276,18 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
         acc[j] = acc[j] + prod;
       }
     }
+    uint16_t* const orow = out + t * H + h0;
+    if (full && (((uintptr_t)orow & 15) == 0)) {
+      uint16_t b[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (h0 + j < H) store_from_f32<DT>(out, t * H + h0 + j, acc[j]);
+      for (int j = 0; j < 8; ++j) store_from_f32<DT>(b, j, acc[j]);
+      *reinterpret_cast<uint4*>(orow) = make_uint4(b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16),
+                                                   b[4] | ((uint32_t)b[5] << 16), b[6] | ((uint32_t)b[7] << 16));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (h0 + j < H) store_from_f32<DT>(out, t * H + h0 + j, acc[j]);
+    }
   }
 }
 
@@ -298,10 +307,32 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __rest
   const int64_t t = token_idx[m];
   const float wm = slot_w[m];
   float part = 0.f;
-  for (int64_t h = threadIdx.x; h < H; h += blockDim.x) {
-    const float g = load_as_f32<DT>(dout, t * H + h);
-    store_from_f32<DT>(dcur, m * H + h, g * wm);
-    part += g * load_as_f32<DT>(y, m * H + h);
+  if (H % 8 == 0 && ((((uintptr_t)dout | (uintptr_t)y | (uintptr_t)dcur) & 15) == 0)) {
+    // 8 consecutive features per thread per pass: 16-byte loads of dout and y, one 16-byte store of dcur
+    for (int64_t h = (int64_t)threadIdx.x * 8; h < H; h += (int64_t)blockDim.x * 8) {
+      const uint4 gq = *reinterpret_cast<const uint4*>(dout + t * H + h);
+      const uint4 yq = *reinterpret_cast<const uint4*>(y + m * H + h);
+      const uint16_t gv[8] = {(uint16_t)gq.x, (uint16_t)(gq.x >> 16), (uint16_t)gq.y, (uint16_t)(gq.y >> 16),
+                              (uint16_t)gq.z, (uint16_t)(gq.z >> 16), (uint16_t)gq.w, (uint16_t)(gq.w >> 16)};
+      const uint16_t yv[8] = {(uint16_t)yq.x, (uint16_t)(yq.x >> 16), (uint16_t)yq.y, (uint16_t)(yq.y >> 16),
+                              (uint16_t)yq.z, (uint16_t)(yq.z >> 16), (uint16_t)yq.w, (uint16_t)(yq.w >> 16)};
+      uint16_t dv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float g = load_as_f32<DT>(gv, j);
+        store_from_f32<DT>(dv, j, g * wm);
+        part += g * load_as_f32<DT>(yv, j);
+      }
+      *reinterpret_cast<uint4*>(dcur + m * H + h) =
+          make_uint4(dv[0] | ((uint32_t)dv[1] << 16), dv[2] | ((uint32_t)dv[3] << 16), dv[4] | ((uint32_t)dv[5] << 16),
+                     dv[6] | ((uint32_t)dv[7] << 16));
+    }
+  } else {
+    for (int64_t h = threadIdx.x; h < H; h += blockDim.x) {
+      const float g = load_as_f32<DT>(dout, t * H + h);
+      store_from_f32<DT>(dcur, m * H + h, g * wm);
+      part += g * load_as_f32<DT>(y, m * H + h);
+    }
   }
   part = wave_sum(part);
   if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = part;

@@ -145,6 +145,168 @@ __global__ __launch_bounds__(256) void sddmm_kernel(const uint16_t* __restrict__
   }
 }
 
+
+// ---- per-expert blocked slot-major operands -------------------------------------
+// Expert e's slots [s0_e, s0_e + S_e) form a contiguous block of C rows of
+// ld_e = round_up(S_e, 8) elements at element offset C * P[e], P[e] = sum of
+// ld_e' over e' < e; the padding columns [S_e, ld_e) are zero.  A weight
+// position's dot product then reads one contiguous, zero-padded run of its
+// expert, and one expert's operands are one contiguous region (TLB and L2
+// friendly).  P and the per-expert 64-slot chunk counts come from a layout
+// table built once per bucketing (blocked_layout_kernel).
+constexpr int BLK_MAX_E = 1024;
+
+// Number of 64-slot chunks the blocked layout of S slots over E experts can
+// need: sum_e ceil(round_up(S_e, 8) / 64) <= (S + 7E) / 64 + E.
+__host__ __device__ inline int64_t blk_chunk_bound(int64_t S, int64_t E) { return (S + 8 * E) / 64 + E + 1; }
+
+// table[e] = P[e] (padded slots before expert e), table[E + 1 + e] = 64-slot
+// chunks before expert e (e <= E), table[2(E + 1) + k] = the expert that owns
+// chunk k, -1 past the last (k < n_map); one block of 256 threads.
+__global__ __launch_bounds__(256) void blocked_layout_kernel(const int32_t* __restrict__ offsets, int E,
+                                                             int32_t* __restrict__ table, int64_t S, int64_t n_map) {
+  __shared__ int32_t s_tmp[512];
+  const int tid = threadIdx.x;
+  const int per = (E + 255) / 256;
+  int sp = 0, sc = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < E) {
+      const int ld = (offsets[e + 1] - offsets[e] + 7) & ~7;
+      sp += ld;
+      sc += (ld + 63) >> 6;
+    }
+  }
+  s_tmp[tid] = sp;
+  s_tmp[256 + tid] = sc;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int a = tid >= off ? s_tmp[tid - off] : 0, b = tid >= off ? s_tmp[256 + tid - off] : 0;
+    __syncthreads();
+    s_tmp[tid] += a;
+    s_tmp[256 + tid] += b;
+    __syncthreads();
+  }
+  int rp = s_tmp[tid] - sp, rc = s_tmp[256 + tid] - sc;
+  int32_t* const map = table + 2 * (E + 1);
+  // offsets[E] above the S the table was sized for: map no chunk, so no
+  // blocked transpose writes past a buffer of usaf_hip_blocked_elems(S, E)
+  const bool fits = offsets[0] == 0 && offsets[E] <= S;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < E) {
+      const int ld = (offsets[e + 1] - offsets[e] + 7) & ~7;
+      const int nc = (ld + 63) >> 6;
+      table[e] = rp;
+      table[E + 1 + e] = rc;
+      for (int k = 0; k < nc && rc + k < n_map; ++k) map[rc + k] = fits ? e : -1;
+      rp += ld;
+      rc += nc;
+    }
+  }
+  for (int64_t k = (int64_t)s_tmp[511] + tid; k < n_map; k += 256) map[k] = -1;
+  if (tid == 255) {
+    table[E] = s_tmp[255];
+    table[2 * E + 1] = s_tmp[511];
+  }
+}
+
+// out (blocked) from in[rows ? rows[s] : s, c]: a block transposes 64 slots of
+// one expert x 64 columns through LDS; grid.x enumerates the (expert, 64-slot
+// chunk) pairs (surplus blocks exit), grid.y the 64-column chunks.  16-byte
+// loads and stores: C, ld_in multiples of 8, bases 16-byte aligned.
+__global__ __launch_bounds__(256) void gather_transpose_blocked_kernel(const uint16_t* __restrict__ in, int64_t ld_in,
+                                                                       const int32_t* __restrict__ rows,
+                                                                       const int32_t* __restrict__ offsets,
+                                                                       const int32_t* __restrict__ table, int E,
+                                                                       int64_t C, uint16_t* __restrict__ out) {
+  constexpr int LDT = 72;
+  __shared__ __align__(16) uint16_t tile[64 * LDT];
+  const int64_t chunk = blockIdx.x;
+  const int e = table[2 * (E + 1) + chunk];
+  if (e < 0) return;  // block-uniform
+  const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = (se + 7) & ~7;
+  const int j0 = (int)(chunk - table[E + 1 + e]) * 64;  // first slot of the chunk within the expert
+  const int64_t c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int v = threadIdx.x + 256 * it;
+    const int sl = v >> 3, cg = v & 7;
+    const int j = j0 + sl;
+    const int64_t c = c0 + 8 * cg;
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (j < se && c < C) {
+      const int64_t row = rows ? (int64_t)rows[s0 + j] : (int64_t)(s0 + j);
+      w = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
+    }
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      tile[(8 * cg + 2 * q) * LDT + sl] = (uint16_t)(ww[q] & 0xffffu);
+      tile[(8 * cg + 2 * q + 1) * LDT + sl] = (uint16_t)(ww[q] >> 16);
+    }
+  }
+  __syncthreads();
+  uint16_t* const blk = out + C * (int64_t)table[e];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int v = threadIdx.x + 256 * it;
+    const int cl = v >> 3, sg = v & 7;
+    const int64_t c = c0 + cl;
+    const int j = j0 + 8 * sg;
+    if (c < C && j < ld)
+      *reinterpret_cast<uint4*>(blk + c * ld + j) = *reinterpret_cast<const uint4*>(&tile[cl * LDT + 8 * sg]);
+  }
+}
+
+// Sampled gradient on blocked operands: as sddmm_kernel, with expert e's rows
+// rowB[e][o] and colB[e][i] contiguous, zero-padded runs of ld_e elements, so
+// no masking is needed; the position list is cut into one contiguous slice
+// per die, positions sorted by expert keep a die on one expert's operands.
+template <int DT>
+__global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __restrict__ rowB,
+                                                            const uint16_t* __restrict__ colB,
+                                                            const int32_t* __restrict__ table, int32_t E,
+                                                            int32_t R, int32_t C, int64_t n_pos,
+                                                            const int32_t* __restrict__ rcode,
+                                                            const int32_t* __restrict__ col_idx,
+                                                            const int64_t* __restrict__ pos_map,
+                                                            float* __restrict__ compact) {
+  __shared__ int32_t s_pre[BLK_MAX_E + 1];
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) s_pre[e] = table[e];
+  __syncthreads();
+  const int gl = threadIdx.x & 15;
+  const int dies = gridDim.x < 8 ? (int)gridDim.x : 8;
+  const int die = (int)(blockIdx.x % dies);
+  const int64_t die_blocks = ((int64_t)gridDim.x + dies - 1 - die) / dies;
+  const int64_t lo = n_pos * die / dies, hi = n_pos * (die + 1) / dies;
+  const int64_t n_grp = die_blocks * (blockDim.x >> 4);
+  for (int64_t p = lo + (int64_t)(blockIdx.x / dies) * (blockDim.x >> 4) + (threadIdx.x >> 4); p < hi; p += n_grp) {
+    const uint32_t code = (uint32_t)rcode[p];
+    const uint32_t i = (uint32_t)col_idx[p];
+    const uint32_t e = code >> 21, o = code & 0x1FFFFFu;
+    if (e >= (uint32_t)E || o >= (uint32_t)R || i >= (uint32_t)C) continue;
+    const int ld = s_pre[e + 1] - s_pre[e];
+    const uint16_t* rv = rowB + (int64_t)R * s_pre[e] + (int64_t)o * ld;
+    const uint16_t* cv = colB + (int64_t)C * s_pre[e] + (int64_t)i * ld;
+    float acc = 0.f;
+    for (int w = 8 * gl; w < ld; w += 128) {
+      const uint4 a = *reinterpret_cast<const uint4*>(rv + w);
+      const uint4 c = *reinterpret_cast<const uint4*>(cv + w);
+      acc = dot2<DT>(a.x, c.x, acc);
+      acc = dot2<DT>(a.y, c.y, acc);
+      acc = dot2<DT>(a.z, c.z, acc);
+      acc = dot2<DT>(a.w, c.w, acc);
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+    if (gl == 0) {
+      const int64_t pos = pos_map ? pos_map[p] : p;
+      compact[pos] += round_to<DT>(acc);
+    }
+  }
+}
+
 // SparseAdam.step for one compact vector (sparse_optim.py:96-130), with the
 // rounding of torch's vectorized CPU kernels the reference runs:
 //   g = g + wd*p                       mul, add
@@ -256,6 +418,62 @@ extern "C" int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t
                                                              offsets, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
                                                              row_code, col_idx, pos_map, compact);
   return check_launch("sddmm_masked");
+}
+
+extern "C" int64_t usaf_hip_blocked_elems(int64_t S, int64_t E, int64_t C) { return C * (S + 7 * E); }
+
+extern "C" int64_t usaf_hip_blocked_table_elems(int64_t S, int64_t E) { return 2 * (E + 1) + blk_chunk_bound(S, E); }
+
+extern "C" int usaf_hip_blocked_layout(const int32_t* offsets, int64_t E, int64_t S, int32_t* table, void* stream) {
+  if (E <= 0 || E > BLK_MAX_E) return set_error(USAF_ERR_INVALID, "blocked_layout: needs 0 < E <= %d", BLK_MAX_E);
+  if (S < 0 || blk_chunk_bound(S, E) > 0x7fffffff) return set_error(USAF_ERR_INVALID, "blocked_layout: bad S");
+  if (!offsets || !table) return set_error(USAF_ERR_INVALID, "blocked_layout: null pointer");
+  blocked_layout_kernel<<<1, 256, 0, as_stream(stream)>>>(offsets, (int)E, table, S, blk_chunk_bound(S, E));
+  return check_launch("blocked_layout");
+}
+
+extern "C" int usaf_hip_gather_transpose_blocked(const void* in, int64_t ld_in, const int32_t* rows,
+                                                 const int32_t* offsets, const int32_t* table, int64_t S, int64_t E,
+                                                 int64_t C, void* out, void* stream) {
+  if (S < 0 || C < 0 || E <= 0 || ld_in < C) return set_error(USAF_ERR_INVALID, "gather_transpose_blocked: bad sizes");
+  if (E > BLK_MAX_E) return set_error(USAF_ERR_UNSUPPORTED, "gather_transpose_blocked: needs E <= %d", BLK_MAX_E);
+  if (S == 0 || C == 0) return clear_error();
+  if (!in || !out || !offsets || !table) return set_error(USAF_ERR_INVALID, "gather_transpose_blocked: null pointer");
+  if (C % 8 != 0 || ld_in % 8 != 0 || ((uintptr_t)in & 15) || ((uintptr_t)out & 15))
+    return set_error(USAF_ERR_UNSUPPORTED, "gather_transpose_blocked: needs C, ld_in %% 8 == 0 and 16-byte aligned bases");
+  const int64_t gx = blk_chunk_bound(S, E), gy = (C + 63) / 64;
+  if (gx > 0x7fffffff || gy > 65535) return set_error(USAF_ERR_INVALID, "gather_transpose_blocked: too large");
+  gather_transpose_blocked_kernel<<<dim3((unsigned)gx, (unsigned)gy), 256, 0, as_stream(stream)>>>(
+      (const uint16_t*)in, ld_in, rows, offsets, table, (int)E, C, (uint16_t*)out);
+  return check_launch("gather_transpose_blocked");
+}
+
+extern "C" int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, const int32_t* table, int64_t E,
+                                      int64_t R, int64_t C, int64_t n_pos, const int32_t* row_code,
+                                      const int32_t* col_idx, const int64_t* pos_map, int32_t dtype, float* compact,
+                                      void* stream) {
+  if (E <= 0 || R <= 0 || C <= 0 || n_pos < 0) return set_error(USAF_ERR_INVALID, "sddmm_blocked: bad sizes");
+  if (E > BLK_MAX_E || R >= (1 << 21) || C > 0x7fffffff)
+    return set_error(USAF_ERR_INVALID, "sddmm_blocked: needs E <= %d, R < 2^21, C < 2^31", BLK_MAX_E);
+  if (n_pos == 0) return clear_error();
+  if (!row_blk || !col_blk || !table || !row_code || !col_idx || !compact)
+    return set_error(USAF_ERR_INVALID, "sddmm_blocked: null pointer");
+  if (((uintptr_t)row_blk & 15) || ((uintptr_t)col_blk & 15))
+    return set_error(USAF_ERR_INVALID, "sddmm_blocked: operands must be 16-byte aligned");
+  if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "sddmm_blocked: dtype must be 16-bit");
+  int64_t blocks = (n_pos + 15) / 16;
+  const int64_t cap = (int64_t)device_cu_count() * 16;
+  if (blocks > cap) blocks = cap;
+  hipStream_t st = as_stream(stream);
+  if (dtype == USAF_BF16)
+    sddmm_blocked_kernel<USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)row_blk, (const uint16_t*)col_blk,
+                                                                      table, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
+                                                                      row_code, col_idx, pos_map, compact);
+  else
+    sddmm_blocked_kernel<USAF_F16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)row_blk, (const uint16_t*)col_blk,
+                                                                     table, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
+                                                                     row_code, col_idx, pos_map, compact);
+  return check_launch("sddmm_blocked");
 }
 
 extern "C" int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, float* v, int64_t n, double lr,

@@ -187,6 +187,7 @@ class Buckets:
     slot_w: torch.Tensor     # fp32 [S]
     pair_slot: torch.Tensor  # int32 [T, E]
     n_slots: int
+    blk_table: Optional[torch.Tensor] = None  # layout table of the blocked sampled-gradient operands (lazy)
 
 
 def bucket_by_expert(weights: torch.Tensor) -> Buckets:
@@ -240,7 +241,13 @@ def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Opt
     store, prefix = capture
     name = f"{prefix}.{which}"
     if hasattr(store, "add_sampled"):
-        store.add_sampled(name, slot_major(dy), slot_major(x, rows=x_rows), b.offsets, dtype)
+        if _blocked_ok(dy) and _blocked_ok(x) and b.offsets.numel() - 1 <= 1024:
+            if b.blk_table is None:
+                b.blk_table = blocked_layout(b.offsets, b.n_slots)
+            store.add_sampled(name, slot_blocked(dy, b.offsets, b.n_slots, table=b.blk_table),
+                              slot_blocked(x, b.offsets, b.n_slots, rows=x_rows, table=b.blk_table), b.offsets, dtype)
+        else:
+            store.add_sampled(name, slot_major(dy), slot_major(x, rows=x_rows), b.offsets, dtype)
         return
     offs = b.offsets.tolist()
     for ei in range(len(offs) - 1):
@@ -371,6 +378,47 @@ def _dense_weight_grad(out: torch.Tensor, dy: torch.Tensor, x: torch.Tensor, x_r
             continue
         xe = x.index_select(0, x_rows[s0:s1].long()) if x_rows is not None else x[s0:s1]
         out[ei] = torch.mm(dy[s0:s1].t().float(), xe.float()).to(out.dtype)
+
+
+@dataclass
+class BlockedSlots:
+    """Per-expert blocked slot-major operand (usaf_hip_gather_transpose_blocked):
+    expert e's slots form a contiguous block of `cols` rows of round_up(S_e, 8)
+    elements, zero-padded, at element offset cols * sum of the padded counts of
+    the experts before e."""
+    data: torch.Tensor       # flat, 16-bit
+    cols: int                # C: rows per expert block (features of the operand)
+    offsets: torch.Tensor    # int32 [E+1] the blocks were built with
+    table: torch.Tensor      # int32 layout table of those offsets (blocked_layout)
+
+
+def blocked_layout(offsets: torch.Tensor, n_slots: int) -> torch.Tensor:
+    """Layout table (usaf_hip_blocked_layout) of one bucketing of n_slots slots."""
+    E = offsets.numel() - 1
+    lib = N.load()
+    table = torch.empty(int(lib.usaf_hip_blocked_table_elems(n_slots, E)), dtype=torch.int32, device=offsets.device)
+    N.call("usaf_hip_blocked_layout", offsets.data_ptr(), E, n_slots, table.data_ptr(), N.stream_ptr(offsets.device))
+    return table
+
+
+def slot_blocked(x: torch.Tensor, offsets: torch.Tensor, n_slots: int,
+                 rows: Optional[torch.Tensor] = None, table: Optional[torch.Tensor] = None) -> BlockedSlots:
+    """[S or T, C] -> BlockedSlots (rows gathered by `rows` when given)."""
+    C = x.shape[1]
+    E = offsets.numel() - 1
+    if table is None:
+        table = blocked_layout(offsets, n_slots)
+    elif table.numel() < int(N.load().usaf_hip_blocked_table_elems(n_slots, E)):
+        raise ValueError("slot_blocked: layout table built for fewer slots")
+    lib = N.load()
+    out = torch.empty(max(1, int(lib.usaf_hip_blocked_elems(n_slots, E, C))), dtype=x.dtype, device=x.device)
+    N.call("usaf_hip_gather_transpose_blocked", x.data_ptr(), x.stride(0), N.ptr(rows), offsets.data_ptr(),
+           table.data_ptr(), n_slots, E, C, out.data_ptr(), N.stream_ptr(x.device))
+    return BlockedSlots(out, C, offsets, table)
+
+
+def _blocked_ok(x: torch.Tensor) -> bool:
+    return x.shape[1] % 8 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
 
 
 def slot_major(x: torch.Tensor, rows: Optional[torch.Tensor] = None) -> torch.Tensor:

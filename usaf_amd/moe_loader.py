@@ -368,11 +368,24 @@ class SparseGradStore:
 
     def add_sampled(self, full_name: str, rowT: torch.Tensor, colT: torch.Tensor, offsets: torch.Tensor,
                     dtype: torch.dtype) -> None:
-        """compact[name] += dtype(rowT[o, slots_e] . colT[i, slots_e]) at each active (e, o, i)."""
+        """compact[name] += dtype(rowT[o, slots_e] . colT[i, slots_e]) at each active (e, o, i).
+
+        rowT / colT: slot-major operands [R or C, >= S] (usaf_amd.moe.slot_major), or
+        usaf_amd.moe.BlockedSlots built with the same offsets (usaf_amd.moe.slot_blocked)."""
         csr = self._csr.get(full_name)
         if csr is None:
             return
         _, row_code, cols, pos_map, E, R, C = csr
+        if not isinstance(rowT, torch.Tensor):  # BlockedSlots
+            if rowT.cols != R or colT.cols != C:
+                raise ValueError(f"{full_name}: blocked operands of {rowT.cols} / {colT.cols} rows do not match "
+                                 f"the weight rows {R} x cols {C}")
+            if rowT.offsets.data_ptr() != offsets.data_ptr() or colT.offsets.data_ptr() != offsets.data_ptr():
+                raise ValueError(f"{full_name}: blocked operands were built with other expert offsets")
+            N.call("usaf_hip_sddmm_blocked", rowT.data.data_ptr(), colT.data.data_ptr(), rowT.table.data_ptr(), E, R, C,
+                   cols.numel(), row_code.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
+                   self.compact[full_name].data_ptr(), N.stream_ptr(self.device))
+            return
         if rowT.shape[0] != R or colT.shape[0] != C or rowT.shape[1] != colT.shape[1]:
             raise ValueError(f"{full_name}: operands {tuple(rowT.shape)} / {tuple(colT.shape)} do not match "
                              f"the weight rows {R} x cols {C}")
