@@ -157,47 +157,67 @@ def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfl
     opt = SparseAdam(masters, active_idx=active, lr=2e-4, weight_decay=0.005, compact_params=True)
     hs = torch.randn(T, H, device=dev, generator=gen).to(dtype).requires_grad_(True)
     router_w = (torch.randn(E, H, device=dev, generator=gen) / H ** 0.5).to(dtype).requires_grad_(True)
-    sgd = torch.optim.SGD([router_w], lr=2e-4, momentum=0.9, weight_decay=0.005)
+    sgd = torch.optim.SGD([router_w], lr=2e-4, momentum=0.9, weight_decay=0.005, fused=True)
     dy = torch.randn(T, H, device=dev, generator=gen).to(dtype)
     n_act = {n.rsplit(".", 1)[1]: int(i.numel()) for n, i in active.items()}
     return dict(experts=experts, store=store, opt=opt, hs=hs, router_w=router_w, sgd=sgd, dy=dy, k=k,
                 prefix=prefix, T=T, H=H, I=I, E=E, n_act=n_act, active=active)
 
 
-def moe_train_step(L) -> bool:
-    """One step; returns whether the gradients were finite (step applied)."""
+def _fwd_bwd_check(L, flag, static_slots: bool) -> dict:
+    """Forward + backward with grad capture, then the reference's finite check
+    (train.py:649-651) into flag[0]; static_slots buckets the experts into
+    T * (top_k + 1) slots without a host read, flag[1] = 1 if that overflowed."""
     from usaf_amd import _native as N
     from usaf_amd import moe as G
     store = L["store"]
     store.zero_()
     L["hs"].grad = None
     L["router_w"].grad = None
-    out = G.moe_block(L["hs"], L["router_w"], L["k"], False, L["experts"], capture=(store, L["prefix"]))
+    flag.fill_(1)       # finite
+    flag[1:].fill_(0)   # overflow
+    out = G.moe_block(L["hs"], L["router_w"], L["k"], False, L["experts"], capture=(store, L["prefix"]),
+                      overflow=flag[1:] if static_slots else None)
     out.backward(L["dy"])
     dev = L["hs"].device
-    flag = L.setdefault("flag", torch.ones(1, dtype=torch.int32, device=dev))
-    flag.fill_(1)
     cg = {}
     for name, v in store.compact.items():
         o = L.setdefault(f"cg:{name}", torch.empty_like(v))
         N.call("usaf_hip_scale_check", v.data_ptr(), o.data_ptr(), v.numel(), 1.0, flag.data_ptr(),
                N.stream_ptr(dev))
         cg[name] = o
-    finite = bool(flag.item())
+    return cg
+
+
+def moe_train_step(L) -> bool:
+    """One step; returns whether the gradients were finite (step applied).
+    One host read per step (the finite flag, as the reference's loop); the
+    slot count stays on the GPU unless the routing overflowed T * (top_k + 1)
+    slots, in which case the step is recomputed with exact bucketing."""
+    dev = L["hs"].device
+    flag = L.setdefault("flag", torch.ones(2, dtype=torch.int32, device=dev))
+    cg = _fwd_bwd_check(L, flag, static_slots=True)
+    finite, overflow = flag.tolist()
+    L["overflows"] = L.get("overflows", 0) + overflow
+    if overflow:
+        cg = _fwd_bwd_check(L, flag, static_slots=False)
+        finite = flag.tolist()[0]
     if finite:
         L["opt"].step(compact_grads=cg)
         L["sgd"].step()
-    return finite
+    return bool(finite)
 
 
 def bench_moe_step(dev, steps: int, warmup: int) -> dict:
     L = build_moe(dev)
     for _ in range(warmup):
         moe_train_step(L)
+    L["overflows"] = 0
     with _Timer() as t:
         for _ in range(steps):
             moe_train_step(L)
     ms = t.ms / steps
+    _log(f"moe step: {L['overflows']} of {steps} timed steps overflowed the static slot capacity (recomputed)")
     fl = moe_step_flops(L["T"], L["H"], L["I"], L["E"], L["k"], L["n_act"]["gate_up_proj"],
                         L["n_act"]["down_proj"])
     kern = bench_moe_kernels(L, max(3, steps))

@@ -130,13 +130,17 @@ int64_t usaf_hip_bucket_workspace_ints(int64_t T, int64_t E);
  *   counts     [E] int32 out; offsets [E+1] int32 out (offsets[E] = S, the pair count)
  *   token_idx  [capacity] int32 out: slot s -> token, tokens ascending within each expert
  *   slot_w     [capacity] fp32 out: fp32 of the routing weight of slot s
- *   pair_slot  [T, E] int32 out: slot of (t, e), -1 if not routed
- * Pairs beyond `capacity` are counted in offsets but not stored; callers size
- * capacity >= T*E or check offsets[E] <= capacity.
+ *   pair_slot  [T, E] int32 out: slot of (t, e), -1 if not routed (or beyond capacity)
+ * counts are the true per-expert pair counts; offsets are clamped to `capacity`,
+ * so pairs beyond it are dropped and every offset indexes the slot buffers.
+ * overflow == NULL: callers size capacity >= T*E (nothing is dropped) and read
+ * the slot count S = offsets[E].  overflow != NULL (capacity mode, no host read
+ * of S needed): the slots [offsets[E], capacity) are filled with token 0 and
+ * weight 0, and *overflow is set to 1 (never cleared) when pairs were dropped.
  */
 int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dtype, int64_t T, int64_t E, int32_t* workspace,
                               int32_t* counts, int32_t* offsets, int32_t* token_idx, float* slot_w,
-                              int32_t* pair_slot, int64_t capacity, void* stream);
+                              int32_t* pair_slot, int64_t capacity, int32_t* overflow, void* stream);
 
 /*
  * Expert-ordered combine.  Replaces usaf/qwen3moe_dml.py:62-64:
@@ -154,6 +158,7 @@ int usaf_hip_moe_combine(const void* y_slots, const void* weights, const int32_t
  *   dcur[s]          = dtype(fp32(dout[t]) * w_s)                 [S, H]
  *   dweights[t, e]   = dtype(sum_h fp32(dout[t,h]) * fp32(y[s,h])) (routed pairs only;
  *                      other entries are left untouched -- callers zero them)
+ * Slots s >= offsets[E] (the padding of a capacity-mode bucketing) are skipped.
  */
 int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_t* token_idx, const float* slot_w,
                              const int32_t* offsets, int64_t S, int64_t E, int64_t H, int32_t dtype, void* dcur,

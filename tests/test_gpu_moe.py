@@ -114,6 +114,37 @@ def test_bucket_empty_and_ragged(gpu_device):
     assert b0.n_slots == 0
 
 
+@pytest.mark.parametrize("T,E,k", [(4096, 128, 8), (37, 12, 3), (1000, 1000, 1)])
+def test_bucket_capacity_mode(gpu_device, T, E, k):
+    _say(f"bucket capacity mode T={T} E={E} k={k}")
+    g = torch.Generator().manual_seed(T + E)
+    w_ref, _, _ = M.route(torch.randn(T, E, generator=g), k, False, torch.bfloat16)
+    counts, offsets, tok, sw = M.bucket(w_ref)
+    S = int(offsets[-1])
+    w = w_ref.to(gpu_device)
+    # capacity above the routed pairs: same buckets, zero padding, no overflow
+    ovf = torch.zeros(1, dtype=torch.int32, device=gpu_device)
+    cap = S + 77
+    b = G.bucket_by_expert(w, cap, ovf)
+    torch.cuda.synchronize()
+    assert b.n_slots == cap and int(ovf) == 0
+    assert torch.equal(b.counts.cpu().long(), counts) and torch.equal(b.offsets.cpu().long(), offsets)
+    assert torch.equal(b.token_idx.cpu()[:S].long(), tok) and torch.equal(b.slot_w.cpu()[:S], sw)
+    assert torch.all(b.token_idx.cpu()[S:] == 0) and torch.all(b.slot_w.cpu()[S:] == 0)
+    assert torch.equal(b.pair_slot.cpu(), G.bucket_by_expert(w).pair_slot.cpu())
+    # capacity below: offsets clamped, later pairs dropped, overflow raised
+    cap = S - S // 3 - 1
+    b = G.bucket_by_expert(w, cap, ovf)
+    torch.cuda.synchronize()
+    assert int(ovf) == 1
+    assert torch.equal(b.counts.cpu().long(), counts)
+    assert torch.equal(b.offsets.cpu().long(), offsets.clamp(max=cap))
+    assert torch.equal(b.token_idx.cpu().long(), tok[:cap]) and torch.equal(b.slot_w.cpu(), sw[:cap])
+    ps = b.pair_slot.cpu()
+    assert torch.equal(torch.sort(ps[ps >= 0]).values, torch.arange(cap, dtype=torch.int32))
+    assert int((ps >= 0).sum()) == cap
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_combine_bit_exact(gpu_device, dtype):
     _say(f"combine bit-exact {dtype}")
@@ -290,6 +321,34 @@ def test_moe_block_router_backward(gpu_device):
     assert rel_err(out, ref) <= 1e-2
     assert rel_err(xg.grad, x.grad) <= 1e-2
     assert rel_err(wg.grad, wr_c.grad) <= 1e-2
+
+
+def test_moe_block_capacity_mode_matches_exact(gpu_device):
+    _say("moe block with capacity-mode bucketing (no host read) == exact bucketing, bit for bit")
+    E, H, I, T, k = 16, 256, 128, 200, 4
+    dt = torch.bfloat16
+    L = make_layer(gpu_device, E, H, I, T, k, dt, seed=7)
+    g = torch.Generator().manual_seed(70)
+    wr = (torch.randn(E, H, generator=g) / H ** 0.5).to(dt).to(gpu_device)
+    dout = torch.randn(T, H, generator=g).to(dt).to(gpu_device)
+    nG, nD = E * 2 * I * H, E * H * I
+    act = {"L.gate_up_proj": torch.randperm(nG, generator=g)[: nG // 200].sort().values,
+           "L.down_proj": torch.randperm(nD, generator=g)[: nD // 200].sort().values}
+    shapes = {"L.gate_up_proj": (E, 2 * I, H), "L.down_proj": (E, H, I)}
+    res = []
+    for mode in ("exact", "capacity"):
+        store = SparseGradStore(act, shapes, device=gpu_device)
+        xg = L["hs"].to(gpu_device).requires_grad_(True)
+        wg = wr.clone().requires_grad_(True)
+        ovf = torch.zeros(1, dtype=torch.int32, device=gpu_device) if mode == "capacity" else None
+        out = G.moe_block(xg, wg, k, False, L["ew"], capture=(store, "L"), overflow=ovf)
+        out.backward(dout)
+        torch.cuda.synchronize()
+        if ovf is not None:
+            assert int(ovf) == 0
+        res.append([out, xg.grad, wg.grad] + [store.compact[n] for n in sorted(act)])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
 
 
 # ---- optimizer path ------------------------------------------------------------------

@@ -38,7 +38,8 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_q4_transpose": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p],
     "usaf_hip_route_topk": [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p, _c_p],
     "usaf_hip_route_topk_bwd": [_c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p],
-    "usaf_hip_bucket_by_expert": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p],
+    "usaf_hip_bucket_by_expert": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p,
+                                  _c_p],
     "usaf_hip_moe_combine": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p],
     "usaf_hip_moe_combine_bwd": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p],
     "usaf_hip_moe_gate_up_fwd": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,

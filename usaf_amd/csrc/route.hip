@@ -166,50 +166,101 @@ __global__ __launch_bounds__(256) void route_topk_bwd_kernel(const void* __restr
 //  scan : per-expert totals -> counts, offsets; per (chunk, expert) base slot
 //  fill : token ids in ascending order within each expert (a stable sort by
 //         expert), slot weights, and the [T, E] token/expert -> slot map.
-constexpr int kChunk = 64;
+// Count and fill issue a chunk's kChunk loads per thread before using them;
+// the scan splits each expert's chunk list over 1024 / E threads.
+constexpr int kChunk = 16;
 
 template <int WDT>
 __global__ __launch_bounds__(256) void bucket_count_kernel(const void* __restrict__ w, int64_t T, int E,
                                                            int32_t* __restrict__ chunk_cnt) {
   const int64_t c = blockIdx.x;
   const int64_t t0 = c * kChunk;
-  const int64_t t1 = (t0 + kChunk < T) ? t0 + kChunk : T;
+  const int nt = (T - t0 < kChunk) ? (int)(T - t0) : kChunk;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float v[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) v[j] = j < nt ? load_as_f32<WDT>(w, (t0 + j) * E + e) : 0.f;
     int n = 0;
-    for (int64_t t = t0; t < t1; ++t) n += load_as_f32<WDT>(w, t * E + e) != 0.f;
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) n += v[j] != 0.f;
     chunk_cnt[c * E + e] = n;
   }
 }
 
-// Single block of 1024 threads; E <= 1024.
+// Single block of 1024 threads; E <= 1024.  Thread (e, seg) owns expert e's
+// chunks [seg * per, (seg + 1) * per).  Offsets are clamped to `capacity`;
+// with `overflow` set (capacity mode) the slots [offsets[E], capacity) get
+// token 0 and weight 0, and *overflow becomes 1 when the pairs exceed capacity.
 __global__ __launch_bounds__(1024) void bucket_scan_kernel(int32_t* __restrict__ chunk_cnt, int64_t n_chunks, int E,
-                                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
+                                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                           int64_t capacity, int32_t* __restrict__ token_idx,
+                                                           float* __restrict__ slot_w, int32_t* __restrict__ overflow) {
+  __shared__ int32_t s_seg[1024];
   __shared__ int32_t s_tot[1024];
-  const int e = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int nseg = 1024 / E;
+  const int e = tid % E, seg = tid / E;
+  const bool active = seg < nseg;
+  const int64_t per = (n_chunks + nseg - 1) / nseg;
+  const int64_t c0 = active ? (int64_t)seg * per : 0;
+  const int64_t c1 = active ? (c0 + per < n_chunks ? c0 + per : n_chunks) : 0;
+  int sum = 0;
+  for (int64_t c = c0; c < c1; c += 8) {
+    int v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = c + j < c1 ? chunk_cnt[(c + j) * E + e] : 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += v[j];
+  }
+  s_seg[tid] = sum;
+  __syncthreads();
   int tot = 0;
-  if (e < E) {
-    for (int64_t c = 0; c < n_chunks; ++c) {
-      const int v = chunk_cnt[c * E + e];
-      chunk_cnt[c * E + e] = tot;  // exclusive within expert
+  if (tid < E) {  // exclusive prefix over the expert's segments, in place
+    for (int q = 0; q < nseg; ++q) {
+      const int v = s_seg[q * E + tid];
+      s_seg[q * E + tid] = tot;
       tot += v;
     }
-    counts[e] = tot;
+    counts[tid] = tot;
   }
-  s_tot[e] = (e < E) ? tot : 0;
+  s_tot[tid] = tid < E ? tot : 0;
   __syncthreads();
-  // inclusive Hillis-Steele scan over 1024 entries
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int v = (e >= off) ? s_tot[e - off] : 0;
+  for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan over the experts
+    const int v = (tid >= off) ? s_tot[tid - off] : 0;
     __syncthreads();
-    s_tot[e] += v;
+    s_tot[tid] += v;
     __syncthreads();
   }
-  const int base = s_tot[e] - ((e < E) ? tot : 0);  // exclusive
-  if (e < E) {
-    offsets[e] = base;
-    for (int64_t c = 0; c < n_chunks; ++c) chunk_cnt[c * E + e] += base;
+  const int64_t total = s_tot[E - 1];
+  const int64_t s_end = total < capacity ? total : capacity;
+  __shared__ int32_t s_base[1024];
+  if (tid < E) {
+    const int64_t base = s_tot[tid] - tot;
+    s_base[tid] = (int32_t)base;
+    offsets[tid] = (int32_t)(base < capacity ? base : capacity);
   }
-  if (e == E - 1) offsets[E] = s_tot[e];
+  if (tid == 0) {
+    offsets[E] = (int32_t)s_end;
+    if (overflow && total > capacity) overflow[0] = 1;
+  }
+  __syncthreads();
+  // chunk bases (unclamped: the fill stores only slots below capacity)
+  int run = active ? s_base[e] + s_seg[seg * E + e] : 0;
+  for (int64_t c = c0; c < c1; c += 8) {
+    int v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = c + j < c1 ? chunk_cnt[(c + j) * E + e] : 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (c + j < c1) chunk_cnt[(c + j) * E + e] = run;
+      run += v[j];
+    }
+  }
+  if (overflow)
+    for (int64_t i = s_end + tid; i < capacity; i += 1024) {
+      token_idx[i] = 0;
+      slot_w[i] = 0.f;
+    }
 }
 
 template <int WDT>
@@ -219,21 +270,26 @@ __global__ __launch_bounds__(256) void bucket_fill_kernel(const void* __restrict
                                                           float* __restrict__ slot_w, int32_t* __restrict__ pair_slot) {
   const int64_t c = blockIdx.x;
   const int64_t t0 = c * kChunk;
-  const int64_t t1 = (t0 + kChunk < T) ? t0 + kChunk : T;
+  const int nt = (T - t0 < kChunk) ? (int)(T - t0) : kChunk;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float v[kChunk];
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) v[j] = j < nt ? load_as_f32<WDT>(w, (t0 + j) * E + e) : 0.f;
     int64_t pos = chunk_base[c * E + e];
-    for (int64_t t = t0; t < t1; ++t) {
-      const float v = load_as_f32<WDT>(w, t * E + e);
-      int32_t s = -1;
-      if (v != 0.f) {
-        if (pos < capacity) {
-          token_idx[pos] = (int32_t)t;
-          slot_w[pos] = v;
-          s = (int32_t)pos;
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) {
+      if (j < nt) {
+        int32_t sl = -1;
+        if (v[j] != 0.f) {
+          if (pos < capacity) {
+            token_idx[pos] = (int32_t)(t0 + j);
+            slot_w[pos] = v[j];
+            sl = (int32_t)pos;
+          }
+          ++pos;
         }
-        ++pos;
+        pair_slot[(t0 + j) * E + e] = sl;
       }
-      pair_slot[t * E + e] = s;
     }
   }
 }
@@ -304,6 +360,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const uint16_t* __rest
 #pragma clang fp contract(off)
   __shared__ float s_part[4];
   const int64_t m = blockIdx.x;
+  if (m >= offsets[E]) return;  // padding slots of a capacity-mode bucketing (block-uniform)
   const int64_t t = token_idx[m];
   const float wm = slot_w[m];
   float part = 0.f;
@@ -417,12 +474,16 @@ extern "C" int64_t usaf_hip_bucket_workspace_ints(int64_t T, int64_t E) {
 
 extern "C" int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dtype, int64_t T, int64_t E,
                                          int32_t* workspace, int32_t* counts, int32_t* offsets, int32_t* token_idx,
-                                         float* slot_w, int32_t* pair_slot, int64_t capacity, void* stream) {
+                                         float* slot_w, int32_t* pair_slot, int64_t capacity, int32_t* overflow,
+                                         void* stream) {
   if (T < 0 || E <= 0 || E > 1024) return set_error(USAF_ERR_INVALID, "bucket_by_expert: need 0 < E <= 1024");
   if (T > 0x7fffffff) return set_error(USAF_ERR_INVALID, "bucket_by_expert: token ids must fit int32");
   if (!counts || !offsets) return set_error(USAF_ERR_INVALID, "bucket_by_expert: null counts/offsets");
   if (T > 0 && (!weights || !workspace || !pair_slot || (capacity > 0 && (!token_idx || !slot_w))))
     return set_error(USAF_ERR_INVALID, "bucket_by_expert: null pointer");
+  if (capacity < 0 || capacity > 0x7fffffff) return set_error(USAF_ERR_INVALID, "bucket_by_expert: bad capacity");
+  if (overflow && capacity > 0 && (!token_idx || !slot_w))
+    return set_error(USAF_ERR_INVALID, "bucket_by_expert: capacity mode needs token_idx and slot_w");
   hipStream_t st = as_stream(stream);
   const int64_t n_chunks = (T + kChunk - 1) / kChunk;
   const int e = (int)E;
@@ -431,7 +492,8 @@ extern "C" int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dt
                      bucket_count_kernel<WDT><<<(unsigned)n_chunks, 256, 0, st>>>(weights, T, e, workspace));
     if (int rc = check_launch("bucket_by_expert/count")) return rc;
   }
-  bucket_scan_kernel<<<1, 1024, 0, st>>>(workspace, n_chunks, e, counts, offsets);
+  bucket_scan_kernel<<<1, 1024, 0, st>>>(workspace, n_chunks, e, counts, offsets, capacity, token_idx, slot_w,
+                                          overflow);
   if (int rc = check_launch("bucket_by_expert/scan")) return rc;
   if (n_chunks > 0) {
     USAF_DISPATCH_DT(weights_dtype, WDT,

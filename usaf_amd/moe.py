@@ -190,27 +190,39 @@ class Buckets:
     blk_table: Optional[torch.Tensor] = None  # layout table of the blocked sampled-gradient operands (lazy)
 
 
-def bucket_by_expert(weights: torch.Tensor) -> Buckets:
+def bucket_by_expert(weights: torch.Tensor, capacity: Optional[int] = None,
+                     overflow: Optional[torch.Tensor] = None) -> Buckets:
     """Stable bucketing of routed pairs by expert (kaggle_t4_bench.py:293-306).
 
-    Reads back the slot count once (the reference's batched path also syncs,
-    on `counts.max().item()`) to size the slot buffers.
+    Default: reads back the slot count once (the reference's batched path also
+    syncs, on `counts.max().item()`) to size the slot buffers exactly.
+
+    capacity + overflow (int32 [>= 1] device tensor): no host read.  The slot
+    buffers hold `capacity` slots, n_slots = capacity, and the slots past the
+    routed pairs carry token 0 and weight 0; pairs beyond capacity are dropped
+    and set overflow[0] = 1, which the caller must check before trusting the
+    step (e.g. capacity = T * top_k, exceeded only by ties at the top-k
+    threshold).
     """
     weights = weights.contiguous()
     T, E = weights.shape
     dev = weights.device
     lib = N.load()
+    if (capacity is None) != (overflow is None):
+        raise ValueError("bucket_by_expert: give both capacity and overflow, or neither")
+    if overflow is not None and (overflow.dtype != torch.int32 or overflow.device != dev or overflow.numel() < 1):
+        raise ValueError("bucket_by_expert: overflow must be an int32 tensor on the weights' device")
     ws = torch.empty(max(1, int(lib.usaf_hip_bucket_workspace_ints(T, E))), dtype=torch.int32, device=dev)
     counts = torch.empty(E, dtype=torch.int32, device=dev)
     offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
-    cap = T * E
+    cap = T * E if capacity is None else int(capacity)
     token_idx = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
     slot_w = torch.empty(max(cap, 1), dtype=torch.float32, device=dev)
     pair_slot = torch.empty(T, E, dtype=torch.int32, device=dev)
     N.call("usaf_hip_bucket_by_expert", weights.data_ptr(), N.dtype_code(weights.dtype), T, E, ws.data_ptr(),
            counts.data_ptr(), offsets.data_ptr(), token_idx.data_ptr(), slot_w.data_ptr(), pair_slot.data_ptr(),
-           cap, N.stream_ptr(dev))
-    S = int(offsets[E].item())
+           cap, N.ptr(overflow), N.stream_ptr(dev))
+    S = int(offsets[E].item()) if capacity is None else cap
     return Buckets(counts, offsets, token_idx[:S], slot_w[:S], pair_slot, S)
 
 
@@ -279,9 +291,11 @@ class RoutedExpertsFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hs: torch.Tensor, weights: torch.Tensor, ew: ExpertWeights, capture,
-                w_gate_up: Optional[torch.Tensor] = None, w_down: Optional[torch.Tensor] = None):
+                w_gate_up: Optional[torch.Tensor] = None, w_down: Optional[torch.Tensor] = None,
+                slots: Optional[Tuple[int, torch.Tensor]] = None):
         # w_gate_up / w_down: the dense expert Parameters the kernels' weights were
-        # taken from, passed only so that autograd delivers their gradients
+        # taken from, passed only so that autograd delivers their gradients;
+        # slots: (capacity, overflow) for bucketing without a host read (bucket_by_expert)
         dt = hs.dtype
         if dt not in (torch.float16, torch.bfloat16):
             raise TypeError(f"activations must be fp16 or bf16, got {dt}")
@@ -295,7 +309,7 @@ class RoutedExpertsFn(torch.autograd.Function):
         dev = hs.device
         st = N.stream_ptr(dev)
         code = N.dtype_code(dt)
-        b = bucket_by_expert(weights)
+        b = bucket_by_expert(weights) if slots is None else bucket_by_expert(weights, *slots)
         S = b.n_slots
         gu = torch.empty(S, 2 * I, dtype=dt, device=dev)
         act = torch.empty(S, I, dtype=dt, device=dev)
@@ -332,7 +346,7 @@ class RoutedExpertsFn(torch.autograd.Function):
         d_wgu = torch.zeros(E, 2 * I, H, dtype=ctx.wdt[0], device=dev) if want_gu else None
         d_wdn = torch.zeros(E, H, I, dtype=ctx.wdt[1], device=dev) if want_dn else None
         if S == 0:
-            return torch.zeros_like(hs), dweights, None, None, d_wgu, d_wdn
+            return torch.zeros_like(hs), dweights, None, None, d_wgu, d_wdn, None
         dcur = torch.empty(S, H, dtype=dt, device=dev)
         N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
                b.slot_w.data_ptr(), b.offsets.data_ptr(), S, E, H, code, dcur.data_ptr(), dweights.data_ptr(), st)
@@ -363,7 +377,7 @@ class RoutedExpertsFn(torch.autograd.Function):
         if want_gu:
             _dense_weight_grad(d_wgu, dgu, hs, b.token_idx, b)
         dhs = combine(dx_slots, None, b.pair_slot, dt)
-        return dhs, dweights, None, None, d_wgu, d_wdn
+        return dhs, dweights, None, None, d_wgu, d_wdn, None
 
 
 def _dense_weight_grad(out: torch.Tensor, dy: torch.Tensor, x: torch.Tensor, x_rows: Optional[torch.Tensor],
@@ -435,14 +449,18 @@ def slot_major(x: torch.Tensor, rows: Optional[torch.Tensor] = None) -> torch.Te
 
 
 def routed_experts(hs: torch.Tensor, weights: torch.Tensor, experts: ExpertWeights, capture=None,
-                   weight_params: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+                   weight_params: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+                   slot_capacity: Optional[int] = None, overflow: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Experts forward with the reference signature's data: hs [T, H], weights [T, E].
 
     weight_params: optional (gate_up, down) dense Parameters that ``experts``
     holds (possibly as converted copies); when they require grad they receive
-    dense gradients, as the reference's autograd through the expert loop."""
+    dense gradients, as the reference's autograd through the expert loop.
+    slot_capacity / overflow: bucket without reading the slot count back to the
+    host (graph capture, no stall before the GEMMs); see bucket_by_expert."""
     wg, wd = weight_params if weight_params is not None else (None, None)
-    return RoutedExpertsFn.apply(hs, weights, experts, capture, wg, wd)
+    slots = None if slot_capacity is None and overflow is None else (slot_capacity, overflow)
+    return RoutedExpertsFn.apply(hs, weights, experts, capture, wg, wd, slots)
 
 
 class RouteTopKFn(torch.autograd.Function):
@@ -467,12 +485,21 @@ class RouteTopKFn(torch.autograd.Function):
 
 
 def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_topk_prob: bool,
-              experts: ExpertWeights, capture=None) -> torch.Tensor:
+              experts: ExpertWeights, capture=None, overflow: Optional[torch.Tensor] = None) -> torch.Tensor:
     """qwen3moe_dml.py:67-86: router F.linear (library GEMM), routing kernel,
-    routed experts; hs [B, S, H] or [T, H]."""
+    routed experts; hs [B, S, H] or [T, H].
+
+    overflow: optional int32 device tensor.  Given, the experts are bucketed
+    into T * (top_k + 1) slots with no host read of the slot count, and
+    overflow[0] is set to 1 if the routing selected more pairs: the caller
+    checks it and recomputes without `overflow`.  The threshold mask selects
+    more than top_k experts for a token whose k-th and (k+1)-th probabilities
+    tie, which 16-bit logits make common; the spare T slots absorb that, and
+    slots past the routed pairs cost no GEMM work."""
     shape = hs.shape
     x = hs.reshape(-1, shape[-1])
     logits = torch.nn.functional.linear(x, router_weight)
     weights = RouteTopKFn.apply(logits, top_k, norm_topk_prob, x.dtype)
-    out = routed_experts(x, weights, experts, capture)
+    cap = None if overflow is None else x.shape[0] * min(top_k + 1, router_weight.shape[0])
+    out = routed_experts(x, weights, experts, capture, slot_capacity=cap, overflow=overflow)
     return out.view(shape)
