@@ -148,7 +148,7 @@ int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dtype, int64_
  * accumulated in fp32 with each product rounded before the add, as the
  * reference's `final = final + cur.float() * w.float()`.  weights == NULL: the
  * unweighted sum (used for the grad-input accumulation over experts).
- *   y_slots [S, H], weights [T, E], out [T, H]; dtype fp16 or bf16.
+ *   y_slots [S, H], weights [T, E], out [T, H]; dtype fp16 or bf16; E <= 1024.
  */
 int usaf_hip_moe_combine(const void* y_slots, const void* weights, const int32_t* pair_slot, int64_t T, int64_t E,
                          int64_t H, int32_t dtype, void* out, void* stream);

@@ -304,36 +304,73 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
                                                       const int32_t* __restrict__ pair_slot, int64_t T, int E,
                                                       int64_t H, uint16_t* __restrict__ out) {
 #pragma clang fp contract(off)
+  // The token's routed slots, in expert order, are listed in LDS first (wave 0,
+  // ballot-compacted), so the row loads of up to 8 experts are issued together
+  // instead of one expert's load at a time behind the scan of pair_slot.
+  __shared__ int32_t s_slot[1024];
+  __shared__ float s_w[1024];
+  __shared__ int32_t s_n;
   const int64_t t = blockIdx.x;
-  // 8 consecutive features per thread per pass (one 128-bit load of y)
-  for (int64_t h0 = (int64_t)threadIdx.x * 8; h0 < H; h0 += (int64_t)blockDim.x * 8) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    int base = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + tid;
+      const int32_t sl = e < E ? pair_slot[t * E + e] : -1;
+      const uint64_t mask = __ballot(sl >= 0);
+      if (sl >= 0) {
+        const int pos = base + __popcll(mask & ((1ull << tid) - 1ull));
+        s_slot[pos] = sl;
+        s_w[pos] = w ? load_as_f32<DT>(w, t * E + e) : 1.0f;
+      }
+      base += __popcll(mask);
+    }
+    if (tid == 0) s_n = base;
+  }
+  __syncthreads();
+  const int n = s_n;
+  // 8 consecutive features per thread per pass (one 128-bit load of each row)
+  for (int64_t h0 = (int64_t)tid * 8; h0 < H; h0 += (int64_t)blockDim.x * 8) {
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-    const bool full = h0 + 8 <= H;
-    for (int e = 0; e < E; ++e) {
-      const int32_t s = pair_slot[t * E + e];
-      if (s < 0) continue;
-      const float we = w ? load_as_f32<DT>(w, t * E + e) : 1.0f;
-      const uint16_t* yr = y + (int64_t)s * H + h0;
-      uint16_t v[8];
-      if (full && (((uintptr_t)yr & 15) == 0)) {
-        const uint4 q = *reinterpret_cast<const uint4*>(yr);
-        v[0] = q.x & 0xFFFF; v[1] = q.x >> 16; v[2] = q.y & 0xFFFF; v[3] = q.y >> 16;
-        v[4] = q.z & 0xFFFF; v[5] = q.z >> 16; v[6] = q.w & 0xFFFF; v[7] = q.w >> 16;
-      } else {
+    const bool vec = h0 + 8 <= H && H % 8 == 0 && (((uintptr_t)y & 15) == 0);
+    for (int i0 = 0; i0 < n; i0 += 8) {
+      uint4 q[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (h0 + j < H) ? yr[j] : 0;
+      for (int i = 0; i < 8; ++i) {
+        q[i] = make_uint4(0, 0, 0, 0);
+        if (i0 + i < n) {
+          const uint16_t* yr = y + (int64_t)s_slot[i0 + i] * H + h0;
+          if (vec) {
+            q[i] = *reinterpret_cast<const uint4*>(yr);
+          } else {
+            uint16_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = (h0 + j < H) ? yr[j] : 0;
+            q[i] = make_uint4(v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16),
+                              v[4] | ((uint32_t)v[5] << 16), v[6] | ((uint32_t)v[7] << 16));
+          }
+        }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float yv = load_as_f32<DT>(v, j);
-        const float prod = w ? yv * we : yv;
-        acc[j] = acc[j] + prod;
+      for (int i = 0; i < 8; ++i) {
+        if (i0 + i < n) {
+          const float we = s_w[i0 + i];
+          const uint16_t v[8] = {(uint16_t)q[i].x, (uint16_t)(q[i].x >> 16), (uint16_t)q[i].y,
+                                 (uint16_t)(q[i].y >> 16), (uint16_t)q[i].z, (uint16_t)(q[i].z >> 16),
+                                 (uint16_t)q[i].w, (uint16_t)(q[i].w >> 16)};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float yv = load_as_f32<DT>(v, j);
+            const float prod = w ? yv * we : yv;
+            acc[j] = acc[j] + prod;
+          }
+        }
       }
     }
     uint16_t* const orow = out + t * H + h0;
-    if (full && (((uintptr_t)orow & 15) == 0)) {
+    if (vec && (((uintptr_t)out & 15) == 0)) {
       uint16_t b[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) store_from_f32<DT>(b, j, acc[j]);
@@ -511,6 +548,7 @@ extern "C" int usaf_hip_moe_combine(const void* y_slots, const void* weights, co
   if (T == 0) return clear_error();
   if (!y_slots || !pair_slot || !out) return set_error(USAF_ERR_INVALID, "moe_combine: null pointer");
   if (T > 0x7fffffff) return set_error(USAF_ERR_INVALID, "moe_combine: too many tokens");
+  if (E > 1024) return set_error(USAF_ERR_UNSUPPORTED, "moe_combine: needs E <= 1024");
   hipStream_t st = as_stream(stream);
   if (dtype == USAF_F16)
     combine_kernel<USAF_F16><<<(unsigned)T, 256, 0, st>>>((const uint16_t*)y_slots, weights, pair_slot, T, (int)E, H,
