@@ -246,6 +246,19 @@ int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, const int32
                            int64_t C, int64_t n_pos, const int32_t* row_code, const int32_t* col_idx,
                            const int64_t* pos_map, int32_t dtype, float* compact, void* stream);
 
+/* Backward of the weighted combine (as usaf_hip_moe_combine_bwd) that also writes
+ * dcur in the blocked slot-major layout of `table` (usaf_hip_blocked_layout of the
+ * same offsets and S), the row operand of the down projection's sampled gradient:
+ *   dcur [S, H] row-major, dcur_blk [usaf_hip_blocked_elems(S, E, H)],
+ *   dweights [T, E] (routed pairs only, as usaf_hip_moe_combine_bwd),
+ *   workspace fp32 [usaf_hip_combine_bwd_blocked_ws_floats(S, H)].
+ * Needs H % 8 == 0 and 16-byte aligned dout, y_slots, dcur and dcur_blk. */
+int64_t usaf_hip_combine_bwd_blocked_ws_floats(int64_t S, int64_t H);
+int usaf_hip_moe_combine_bwd_blocked(const void* dout, const void* y_slots, const int32_t* token_idx,
+                                     const float* slot_w, const int32_t* offsets, const int32_t* table, int64_t S,
+                                     int64_t E, int64_t H, int32_t dtype, void* dcur, void* dcur_blk, void* dweights,
+                                     float* workspace, void* stream);
+
 /* out[c, s] = in[rows ? rows[s] : s, c] for 16-bit [.., C] -> [C, S] (slot-major operands).
  * When C, ld_in and ld_out are multiples of 8 and both bases 16-byte aligned, the
  * transposed rows are written as 16-byte vectors and out[c, S .. round_up(S, 8)) is

@@ -572,6 +572,60 @@ def test_gather_transpose_blocked_bit_exact(gpu_device, gathered):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,E,k,H", [(300, 12, 3, 1032), (64, 5, 2, 8), (2048, 128, 8, 2048)])
+def test_combine_bwd_blocked_matches_plain(gpu_device, dtype, T, E, k, H):
+    _say(f"fused combine backward + blocked transpose T={T} E={E} k={k} H={H} {dtype}")
+    from usaf_amd import _native as N
+    g = torch.Generator().manual_seed(T + H)
+    w_ref, _, _ = M.route(torch.randn(T, E, generator=g), k, False, dtype)
+    w = w_ref.to(gpu_device)
+    b = G.bucket_by_expert(w, T * (k + 1), torch.zeros(1, dtype=torch.int32, device=gpu_device))
+    S = b.n_slots
+    dout = torch.randn(T, H, generator=g).to(dtype).to(gpu_device)
+    y = torch.randn(S, H, generator=g).to(dtype).to(gpu_device)
+    code, st = N.dtype_code(dtype), N.stream_ptr(gpu_device)
+    # plain: combine_bwd, then the blocked gather-transpose of dcur
+    dcur0 = torch.empty(S, H, dtype=dtype, device=gpu_device)
+    dw0 = torch.zeros(T, E, dtype=dtype, device=gpu_device)
+    N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(), b.slot_w.data_ptr(),
+           b.offsets.data_ptr(), S, E, H, code, dcur0.data_ptr(), dw0.data_ptr(), st)
+    table = G.blocked_layout(b.offsets, S)
+    blk0 = G.slot_blocked(dcur0, b.offsets, S, table=table)
+    # fused
+    lib = N.load()
+    dcur1 = torch.empty(S, H, dtype=dtype, device=gpu_device)
+    dw1 = torch.zeros(T, E, dtype=dtype, device=gpu_device)
+    blk1 = torch.full((int(lib.usaf_hip_blocked_elems(S, E, H)),), 7, dtype=torch.int16, device=gpu_device)
+    ws = torch.empty(int(lib.usaf_hip_combine_bwd_blocked_ws_floats(S, H)), dtype=torch.float32, device=gpu_device)
+    N.call("usaf_hip_moe_combine_bwd_blocked", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
+           b.slot_w.data_ptr(), b.offsets.data_ptr(), table.data_ptr(), S, E, H, code, dcur1.data_ptr(),
+           blk1.data_ptr(), dw1.data_ptr(), ws.data_ptr(), st)
+    torch.cuda.synchronize()
+    n_real = int(b.offsets[-1])
+    assert torch.equal(dcur1[:n_real].view(torch.int16), dcur0[:n_real].view(torch.int16))
+    used = int(table[E]) * H  # padded slots of all experts x H rows
+    assert torch.equal(blk1[:used], blk0.data[:used].view(torch.int16))
+    # dweights: same products, another fp32 summation order -> within one ulp of the dtype
+    routed = w != 0
+    assert torch.all(dw1[~routed] == 0)
+    ref = torch.zeros(T, E, dtype=torch.float64)
+    mag = torch.zeros(T, E, dtype=torch.float64)
+    tok = b.token_idx.cpu().long()[:n_real]
+    offs = b.offsets.cpu().long()
+    for e in range(E):
+        s0, s1 = int(offs[e]), int(offs[e + 1])
+        if s1 > s0:
+            p = dout.cpu().double()[tok[s0:s1]] * y.cpu().double()[s0:s1]
+            ref[tok[s0:s1], e] = p.sum(1)
+            mag[tok[s0:s1], e] = p.abs().sum(1)
+    got = dw1.cpu().double()
+    # rounding to the dtype (one ulp) plus the fp32 summation error bound
+    tol = torch.finfo(dtype).eps * ref.abs() + H * 2.0 ** -23 * mag
+    r = routed.cpu()
+    assert torch.all((got - ref).abs()[r] <= tol[r])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_sddmm_blocked_ragged_experts(gpu_device, dtype):
     _say(f"sddmm blocked ragged experts {dtype}")
     g = torch.Generator().manual_seed(12)

@@ -10,6 +10,30 @@
 namespace usaf {
 namespace {
 
+// ---- 64-slot x 64-feature transposes through LDS ---------------------------------
+// The tile is stored feature-major, 32 dwords (64 slots) per feature row; a dword
+// holds two consecutive slots.  Writer thread (sp, cg) = (tid >> 3, tid & 7) has
+// the 16-byte chunks of features [8 cg, 8 cg + 8) of slots 2 sp and 2 sp + 1 and
+// writes 8 dwords, one per feature; reader (cl, sg) fetches the 16 bytes of
+// feature cl, slots [8 sg, 8 sg + 8).  The 16-byte groups of a row are XOR
+// swizzled by the feature's group of 8 (cl >> 3), which keeps the writes of a
+// wave at two lanes per bank and the reads at full 16-byte vectors.
+constexpr int TT_DWORDS = 64 * 32;
+__device__ __forceinline__ int tt_index(int col, int slot_pair) {
+  return col * 32 + ((((slot_pair >> 2) ^ (col >> 3)) & 7) << 2) + (slot_pair & 3);
+}
+__device__ __forceinline__ void tt_write(uint32_t* tile, int sp, int cg, uint4 a, uint4 b) {
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    tile[tt_index(8 * cg + 2 * q, sp)] = __builtin_amdgcn_perm(bw[q], aw[q], 0x05040100u);      // low halves
+    tile[tt_index(8 * cg + 2 * q + 1, sp)] = __builtin_amdgcn_perm(bw[q], aw[q], 0x07060302u);  // high halves
+  }
+}
+__device__ __forceinline__ uint4 tt_read(const uint32_t* tile, int cl, int sg) {
+  return *reinterpret_cast<const uint4*>(&tile[tt_index(cl, 4 * sg)]);
+}
+
 // out[c, s] = in[rows ? rows[s] : s, c] for c < C, s < S; 16-bit elements.
 // A 64 (s) x 64 (c) tile goes through LDS stored column-major, so that the row
 // reads and the column writes are both 16-byte vectors over contiguous runs.
@@ -19,27 +43,21 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void gather_transpose_kernel(const uint16_t* __restrict__ in, int64_t ld_in,
                                                                const int32_t* __restrict__ rows, int64_t S, int64_t C,
                                                                uint16_t* __restrict__ out, int64_t ld_out) {
-  constexpr int LDT = 72;  // 64 slots + 8: rows stay 16-byte aligned
-  __shared__ __align__(16) uint16_t tile[64 * LDT];
+  constexpr int LDT = 72;  // scalar path: 64 slots + 8, 64 * 72 halfwords
+  __shared__ __align__(16) uint32_t tile32[64 * LDT / 2 > TT_DWORDS ? 64 * LDT / 2 : TT_DWORDS];
+  uint16_t* const tile = reinterpret_cast<uint16_t*>(tile32);
   const int64_t s0 = (int64_t)blockIdx.x * 64;
   const int64_t c0 = (int64_t)blockIdx.y * 64;
   if constexpr (VEC) {
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int v = threadIdx.x + 256 * it;
-      const int sl = v >> 3, cg = v & 7;
-      const int64_t s = s0 + sl, c = c0 + 8 * cg;
-      uint4 w = make_uint4(0, 0, 0, 0);
-      if (s < S && c < C) {
-        const int64_t row = rows ? (int64_t)rows[s] : s;
-        w = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
+    {
+      const int sp = threadIdx.x >> 3, cg = threadIdx.x & 7;
+      const int64_t sa = s0 + 2 * sp, c = c0 + 8 * cg;
+      uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+      if (c < C) {
+        if (sa < S) a = *reinterpret_cast<const uint4*>(in + (rows ? (int64_t)rows[sa] : sa) * ld_in + c);
+        if (sa + 1 < S) b = *reinterpret_cast<const uint4*>(in + (rows ? (int64_t)rows[sa + 1] : sa + 1) * ld_in + c);
       }
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        tile[(8 * cg + 2 * j) * LDT + sl] = (uint16_t)(ww[j] & 0xffffu);
-        tile[(8 * cg + 2 * j + 1) * LDT + sl] = (uint16_t)(ww[j] >> 16);
-      }
+      tt_write(tile32, sp, cg, a, b);
     }
     __syncthreads();
 #pragma unroll
@@ -47,8 +65,7 @@ __global__ __launch_bounds__(256) void gather_transpose_kernel(const uint16_t* _
       const int v = threadIdx.x + 256 * it;
       const int cl = v >> 3, sg = v & 7;
       const int64_t c = c0 + cl, s = s0 + 8 * sg;
-      if (c < C && s < S)
-        *reinterpret_cast<uint4*>(out + c * ld_out + s) = *reinterpret_cast<const uint4*>(&tile[cl * LDT + 8 * sg]);
+      if (c < C && s < S) *reinterpret_cast<uint4*>(out + c * ld_out + s) = tt_read(tile32, cl, sg);
     }
   } else {
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
@@ -220,31 +237,29 @@ __global__ __launch_bounds__(256) void gather_transpose_blocked_kernel(const uin
                                                                        const int32_t* __restrict__ offsets,
                                                                        const int32_t* __restrict__ table, int E,
                                                                        int64_t C, uint16_t* __restrict__ out) {
-  constexpr int LDT = 72;
-  __shared__ __align__(16) uint16_t tile[64 * LDT];
+  __shared__ __align__(16) uint32_t tile32[TT_DWORDS];
   const int64_t chunk = blockIdx.x;
   const int e = table[2 * (E + 1) + chunk];
   if (e < 0) return;  // block-uniform
   const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = (se + 7) & ~7;
   const int j0 = (int)(chunk - table[E + 1 + e]) * 64;  // first slot of the chunk within the expert
   const int64_t c0 = (int64_t)blockIdx.y * 64;
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int v = threadIdx.x + 256 * it;
-    const int sl = v >> 3, cg = v & 7;
-    const int j = j0 + sl;
+  {
+    const int sp = threadIdx.x >> 3, cg = threadIdx.x & 7;
+    const int ja = j0 + 2 * sp;
     const int64_t c = c0 + 8 * cg;
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (j < se && c < C) {
-      const int64_t row = rows ? (int64_t)rows[s0 + j] : (int64_t)(s0 + j);
-      w = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
+    uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+    if (c < C) {
+      if (ja < se) {
+        const int64_t row = rows ? (int64_t)rows[s0 + ja] : (int64_t)(s0 + ja);
+        a = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
+      }
+      if (ja + 1 < se) {
+        const int64_t row = rows ? (int64_t)rows[s0 + ja + 1] : (int64_t)(s0 + ja + 1);
+        b = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
+      }
     }
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      tile[(8 * cg + 2 * q) * LDT + sl] = (uint16_t)(ww[q] & 0xffffu);
-      tile[(8 * cg + 2 * q + 1) * LDT + sl] = (uint16_t)(ww[q] >> 16);
-    }
+    tt_write(tile32, sp, cg, a, b);
   }
   __syncthreads();
   uint16_t* const blk = out + C * (int64_t)table[e];
@@ -254,9 +269,114 @@ __global__ __launch_bounds__(256) void gather_transpose_blocked_kernel(const uin
     const int cl = v >> 3, sg = v & 7;
     const int64_t c = c0 + cl;
     const int j = j0 + 8 * sg;
-    if (c < C && j < ld)
-      *reinterpret_cast<uint4*>(blk + c * ld + j) = *reinterpret_cast<const uint4*>(&tile[cl * LDT + 8 * sg]);
+    if (c < C && j < ld) *reinterpret_cast<uint4*>(blk + c * ld + j) = tt_read(tile32, cl, sg);
   }
+}
+
+// Backward of the weighted combine (route.hip's combine_bwd_kernel) fused with
+// the blocked transpose of its output.  A block covers one 64-slot chunk of one
+// expert (the layout table's chunk map) and a 512-feature range (blockIdx.y):
+//   dcur[s, h]   = dtype(fp32(dout[t_s, h]) * w_s)            row-major [S, H]
+//   dcurB        = the same values in the blocked slot-major layout (H rows per
+//                  expert block, zero padding up to round_up(S_e, 8))
+//   part[y][s]   = sum over the range of fp32(dout[t_s, h]) * fp32(y[s, h])
+// combine_bwd_finish_kernel adds the ranges: dweights[t_s, e] = dtype(sum_y part).
+// Needs H % 8 == 0 and 16-byte aligned rows.
+template <int DT>
+__global__ __launch_bounds__(256) void combine_bwd_blocked_kernel(
+    const uint16_t* __restrict__ dout, const uint16_t* __restrict__ y, const int32_t* __restrict__ token_idx,
+    const float* __restrict__ slot_w, const int32_t* __restrict__ offsets, const int32_t* __restrict__ table, int E,
+    int64_t H, int64_t S_cap, uint16_t* __restrict__ dcur, uint16_t* __restrict__ dcurB, float* __restrict__ part) {
+#pragma clang fp contract(off)
+  __shared__ __align__(16) uint32_t tile32[TT_DWORDS];
+  const int64_t chunk = blockIdx.x;
+  const int e = table[2 * (E + 1) + chunk];
+  if (e < 0) return;  // block-uniform
+  const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = (se + 7) & ~7;
+  const int j0 = (int)(chunk - table[E + 1 + e]) * 64;  // first slot of the chunk within the expert
+  uint16_t* const blk = dcurB + H * (int64_t)table[e];
+  const int64_t hbeg = (int64_t)blockIdx.y * 512;
+  const int64_t hend = hbeg + 512 < H ? hbeg + 512 : H;
+  const int tid = threadIdx.x;
+  // this thread's cell: slots 2 sp, 2 sp + 1, features [8 cg, 8 cg + 8) of each 64-feature step
+  const int sp = tid >> 3, cg = tid & 7;
+  bool ok[2];
+  int64_t srow[2], trow[2];
+  float wv[2], acc[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int j = j0 + 2 * sp + u;
+    ok[u] = j < se;
+    srow[u] = (int64_t)(s0 + j);
+    trow[u] = ok[u] ? (int64_t)token_idx[s0 + j] : 0;
+    wv[u] = ok[u] ? slot_w[s0 + j] : 0.f;
+    acc[u] = 0.f;
+  }
+  for (int64_t c0 = hbeg; c0 < hend; c0 += 64) {
+    const int64_t c = c0 + 8 * cg;
+    uint4 d[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      d[u] = make_uint4(0, 0, 0, 0);
+      if (ok[u] && c < hend) {
+        const uint4 gq = *reinterpret_cast<const uint4*>(dout + trow[u] * H + c);
+        const uint4 yq = *reinterpret_cast<const uint4*>(y + srow[u] * H + c);
+        const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w}, yw[4] = {yq.x, yq.y, yq.z, yq.w};
+        uint32_t dw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint16_t g2[2] = {(uint16_t)gw[q], (uint16_t)(gw[q] >> 16)};
+          const uint16_t y2[2] = {(uint16_t)yw[q], (uint16_t)(yw[q] >> 16)};
+          uint16_t d2[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float g = load_as_f32<DT>(g2, h);
+            store_from_f32<DT>(d2, h, g * wv[u]);
+            acc[u] += g * load_as_f32<DT>(y2, h);
+          }
+          dw[q] = d2[0] | ((uint32_t)d2[1] << 16);
+        }
+        d[u] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+        *reinterpret_cast<uint4*>(dcur + srow[u] * H + c) = d[u];
+      }
+    }
+    tt_write(tile32, sp, cg, d[0], d[1]);
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int v = tid + 256 * it;
+      const int cl = v >> 3, sg = v & 7;
+      const int64_t cc = c0 + cl;
+      const int j = j0 + 8 * sg;
+      if (cc < hend && j < ld) *reinterpret_cast<uint4*>(blk + cc * ld + j) = tt_read(tile32, cl, sg);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    float a = acc[u];
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) a += __shfl_xor(a, off, 8);
+    if (cg == 0 && ok[u]) part[(int64_t)blockIdx.y * S_cap + srow[u]] = a;
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void combine_bwd_finish_kernel(const float* __restrict__ part, int n_split,
+                                                                 int64_t S_cap, const int32_t* __restrict__ token_idx,
+                                                                 const int32_t* __restrict__ offsets, int E,
+                                                                 void* __restrict__ dweights) {
+#pragma clang fp contract(off)
+  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= S_cap || s >= offsets[E]) return;
+  float a = 0.f;
+  for (int q = 0; q < n_split; ++q) a += part[(int64_t)q * S_cap + s];
+  int lo = 0, hi = E - 1;  // expert of slot s: largest e with offsets[e] <= s
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offsets[mid] <= s) lo = mid; else hi = mid - 1;
+  }
+  store_from_f32<DT>(dweights, (int64_t)token_idx[s] * E + lo, a);
 }
 
 // Sampled gradient on blocked operands: as sddmm_kernel, with expert e's rows
@@ -446,6 +566,46 @@ extern "C" int usaf_hip_gather_transpose_blocked(const void* in, int64_t ld_in, 
   gather_transpose_blocked_kernel<<<dim3((unsigned)gx, (unsigned)gy), 256, 0, as_stream(stream)>>>(
       (const uint16_t*)in, ld_in, rows, offsets, table, (int)E, C, (uint16_t*)out);
   return check_launch("gather_transpose_blocked");
+}
+
+extern "C" int64_t usaf_hip_combine_bwd_blocked_ws_floats(int64_t S, int64_t H) {
+  if (S < 0 || H <= 0) return -1;
+  return ((H + 511) / 512) * S;
+}
+
+extern "C" int usaf_hip_moe_combine_bwd_blocked(const void* dout, const void* y_slots, const int32_t* token_idx,
+                                                const float* slot_w, const int32_t* offsets, const int32_t* table,
+                                                int64_t S, int64_t E, int64_t H, int32_t dtype, void* dcur,
+                                                void* dcur_blk, void* dweights, float* workspace, void* stream) {
+  if (S < 0 || E <= 0 || H <= 0) return set_error(USAF_ERR_INVALID, "moe_combine_bwd_blocked: bad sizes");
+  if (E > BLK_MAX_E) return set_error(USAF_ERR_UNSUPPORTED, "moe_combine_bwd_blocked: needs E <= %d", BLK_MAX_E);
+  if (dtype != USAF_F16 && dtype != USAF_BF16)
+    return set_error(USAF_ERR_INVALID, "moe_combine_bwd_blocked: dtype must be fp16/bf16");
+  if (S == 0) return clear_error();
+  if (!dout || !y_slots || !token_idx || !slot_w || !offsets || !table || !dcur || !dcur_blk || !dweights || !workspace)
+    return set_error(USAF_ERR_INVALID, "moe_combine_bwd_blocked: null pointer");
+  if (H % 8 != 0 || (((uintptr_t)dout | (uintptr_t)y_slots | (uintptr_t)dcur | (uintptr_t)dcur_blk) & 15))
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_combine_bwd_blocked: needs H %% 8 == 0 and 16-byte aligned buffers");
+  const int64_t gx = blk_chunk_bound(S, E), gy = (H + 511) / 512;
+  if (gx > 0x7fffffff || gy > 65535 || S > 0x7fffffff)
+    return set_error(USAF_ERR_INVALID, "moe_combine_bwd_blocked: too large");
+  hipStream_t st = as_stream(stream);
+  const dim3 grid((unsigned)gx, (unsigned)gy);
+  const unsigned fin = (unsigned)((S + 255) / 256);
+  if (dtype == USAF_BF16) {
+    combine_bwd_blocked_kernel<USAF_BF16><<<grid, 256, 0, st>>>(
+        (const uint16_t*)dout, (const uint16_t*)y_slots, token_idx, slot_w, offsets, table, (int)E, H, S,
+        (uint16_t*)dcur, (uint16_t*)dcur_blk, workspace);
+    combine_bwd_finish_kernel<USAF_BF16><<<fin, 256, 0, st>>>(workspace, (int)gy, S, token_idx, offsets, (int)E,
+                                                              dweights);
+  } else {
+    combine_bwd_blocked_kernel<USAF_F16><<<grid, 256, 0, st>>>(
+        (const uint16_t*)dout, (const uint16_t*)y_slots, token_idx, slot_w, offsets, table, (int)E, H, S,
+        (uint16_t*)dcur, (uint16_t*)dcur_blk, workspace);
+    combine_bwd_finish_kernel<USAF_F16><<<fin, 256, 0, st>>>(workspace, (int)gy, S, token_idx, offsets, (int)E,
+                                                             dweights);
+  }
+  return check_launch("moe_combine_bwd_blocked");
 }
 
 extern "C" int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, const int32_t* table, int64_t E,

@@ -239,8 +239,13 @@ def combine(y_slots: torch.Tensor, weights: Optional[torch.Tensor], pair_slot: t
 # grad capture (usaf/qwen3moe_dml.py:30-56 protocol)
 # ---------------------------------------------------------------------------
 
+def _sampled_blocked(capture, b: "Buckets") -> bool:
+    """Whether _capture takes the blocked sampled-gradient path for this store."""
+    return capture is not None and hasattr(capture[0], "add_sampled") and b.offsets.numel() - 1 <= 1024
+
+
 def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Optional[torch.Tensor],
-             b: "Buckets", full_shape, dtype) -> None:
+             b: "Buckets", full_shape, dtype, dy_blocked: Optional["BlockedSlots"] = None) -> None:
     """Deliver the weight gradient of ``{prefix}.{which}`` (dW_e = dy_e^T @ x_e over
     expert e's slots; x_e = x[x_rows] when x_rows is given) to the capture store.
 
@@ -253,10 +258,12 @@ def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Opt
     store, prefix = capture
     name = f"{prefix}.{which}"
     if hasattr(store, "add_sampled"):
-        if _blocked_ok(dy) and _blocked_ok(x) and b.offsets.numel() - 1 <= 1024:
+        if _sampled_blocked(capture, b) and _blocked_ok(dy) and _blocked_ok(x):
             if b.blk_table is None:
                 b.blk_table = blocked_layout(b.offsets, b.n_slots)
-            store.add_sampled(name, slot_blocked(dy, b.offsets, b.n_slots, table=b.blk_table),
+            if dy_blocked is None:
+                dy_blocked = slot_blocked(dy, b.offsets, b.n_slots, table=b.blk_table)
+            store.add_sampled(name, dy_blocked,
                               slot_blocked(x, b.offsets, b.n_slots, rows=x_rows, table=b.blk_table), b.offsets, dtype)
         else:
             store.add_sampled(name, slot_major(dy), slot_major(x, rows=x_rows), b.offsets, dtype)
@@ -348,8 +355,22 @@ class RoutedExpertsFn(torch.autograd.Function):
         if S == 0:
             return torch.zeros_like(hs), dweights, None, None, d_wgu, d_wdn, None
         dcur = torch.empty(S, H, dtype=dt, device=dev)
-        N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
-               b.slot_w.data_ptr(), b.offsets.data_ptr(), S, E, H, code, dcur.data_ptr(), dweights.data_ptr(), st)
+        dcur_blk = None
+        if _sampled_blocked(capture, b) and _blocked_ok(dout) and _blocked_ok(y):
+            # the down projection's sampled gradient reads dcur slot-major: written here, with dcur
+            if b.blk_table is None:
+                b.blk_table = blocked_layout(b.offsets, S)
+            lib = N.load()
+            blk = torch.empty(max(1, int(lib.usaf_hip_blocked_elems(S, E, H))), dtype=dt, device=dev)
+            ws = torch.empty(max(1, int(lib.usaf_hip_combine_bwd_blocked_ws_floats(S, H))), dtype=torch.float32,
+                             device=dev)
+            N.call("usaf_hip_moe_combine_bwd_blocked", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
+                   b.slot_w.data_ptr(), b.offsets.data_ptr(), b.blk_table.data_ptr(), S, E, H, code,
+                   dcur.data_ptr(), blk.data_ptr(), dweights.data_ptr(), ws.data_ptr(), st)
+            dcur_blk = BlockedSlots(blk, H, b.offsets, b.blk_table)
+        else:
+            N.call("usaf_hip_moe_combine_bwd", dout.data_ptr(), y.data_ptr(), b.token_idx.data_ptr(),
+                   b.slot_w.data_ptr(), b.offsets.data_ptr(), S, E, H, code, dcur.data_ptr(), dweights.data_ptr(), st)
         dgu = torch.empty(S, 2 * I, dtype=dt, device=dev)
         tq = ew._ptrs_t("down")
         if tq is not None:
@@ -360,7 +381,7 @@ class RoutedExpertsFn(torch.autograd.Function):
             _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
                        q, sz, w16, code, dgu.data_ptr(), st)
         if capture is not None:
-            _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt)
+            _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt, dy_blocked=dcur_blk)
         if want_dn:
             _dense_weight_grad(d_wdn, dcur, act, None, b)
         dx_slots = torch.empty(S, H, dtype=dt, device=dev)
