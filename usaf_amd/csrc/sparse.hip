@@ -401,29 +401,77 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
   const int64_t die_blocks = ((int64_t)gridDim.x + dies - 1 - die) / dies;
   const int64_t lo = n_pos * die / dies, hi = n_pos * (die + 1) / dies;
   const int64_t n_grp = die_blocks * (blockDim.x >> 4);
-  for (int64_t p = lo + (int64_t)(blockIdx.x / dies) * (blockDim.x >> 4) + (threadIdx.x >> 4); p < hi; p += n_grp) {
-    const uint32_t code = (uint32_t)rcode[p];
-    const uint32_t i = (uint32_t)col_idx[p];
-    const uint32_t e = code >> 21, o = code & 0x1FFFFFu;
-    if (e >= (uint32_t)E || o >= (uint32_t)R || i >= (uint32_t)C) continue;
-    const int ld = s_pre[e + 1] - s_pre[e];
-    const uint16_t* rv = rowB + (int64_t)R * s_pre[e] + (int64_t)o * ld;
-    const uint16_t* cv = colB + (int64_t)C * s_pre[e] + (int64_t)i * ld;
-    float acc = 0.f;
-    for (int w = 8 * gl; w < ld; w += 128) {
-      const uint4 a = *reinterpret_cast<const uint4*>(rv + w);
-      const uint4 c = *reinterpret_cast<const uint4*>(cv + w);
-      acc = dot2<DT>(a.x, c.x, acc);
-      acc = dot2<DT>(a.y, c.y, acc);
-      acc = dot2<DT>(a.z, c.z, acc);
-      acc = dot2<DT>(a.w, c.w, acc);
+  // Two positions per iteration (p, p + n_grp), their operand loads issued
+  // together with the old compact values; the indices of the next two are
+  // fetched one iteration ahead, so each iteration waits on one round trip.
+  struct Idx {
+    uint32_t code, col;
+    int64_t pos;
+  };
+  auto fetch = [&](int64_t q) {
+    Idx r{0xFFFFFFFFu, 0u, 0};
+    if (q < hi) {
+      r.code = (uint32_t)rcode[q];
+      r.col = (uint32_t)col_idx[q];
+      r.pos = pos_map ? pos_map[q] : q;
+    }
+    return r;
+  };
+  const int64_t first = lo + (int64_t)(blockIdx.x / dies) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  Idx cur0 = fetch(first), cur1 = fetch(first + n_grp);
+  for (int64_t p = first; p < hi; p += 2 * n_grp) {
+    const Idx nx0 = fetch(p + 2 * n_grp), nx1 = fetch(p + 3 * n_grp);
+    const Idx cur[2] = {cur0, cur1};
+    bool ok[2];
+    int ld[2];
+    const uint16_t* rv[2];
+    const uint16_t* cv[2];
+    float old[2], acc[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t e = cur[u].code >> 21, o = cur[u].code & 0x1FFFFFu, i = cur[u].col;
+      ok[u] = cur[u].code != 0xFFFFFFFFu && e < (uint32_t)E && o < (uint32_t)R && i < (uint32_t)C;
+      const int pe = ok[u] ? s_pre[e] : 0;
+      ld[u] = ok[u] ? s_pre[e + 1] - pe : 0;
+      rv[u] = rowB + (int64_t)R * pe + (int64_t)(ok[u] ? o : 0) * ld[u];
+      cv[u] = colB + (int64_t)C * pe + (int64_t)(ok[u] ? i : 0) * ld[u];
+      old[u] = (ok[u] && gl == 0) ? compact[cur[u].pos] : 0.f;
+      acc[u] = 0.f;
+    }
+    const int ldm = ld[0] > ld[1] ? ld[0] : ld[1];
+    for (int w = 8 * gl; w < ldm; w += 256) {
+      uint4 a[2][2], c[2][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          a[u][h] = make_uint4(0, 0, 0, 0);
+          c[u][h] = make_uint4(0, 0, 0, 0);
+          if (w + 128 * h < ld[u]) {
+            a[u][h] = *reinterpret_cast<const uint4*>(rv[u] + w + 128 * h);
+            c[u][h] = *reinterpret_cast<const uint4*>(cv[u] + w + 128 * h);
+          }
+        }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (w + 128 * h < ld[u]) {
+            acc[u] = dot2<DT>(a[u][h].x, c[u][h].x, acc[u]);
+            acc[u] = dot2<DT>(a[u][h].y, c[u][h].y, acc[u]);
+            acc[u] = dot2<DT>(a[u][h].z, c[u][h].z, acc[u]);
+            acc[u] = dot2<DT>(a[u][h].w, c[u][h].w, acc[u]);
+          }
     }
 #pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
-    if (gl == 0) {
-      const int64_t pos = pos_map ? pos_map[p] : p;
-      compact[pos] += round_to<DT>(acc);
+    for (int u = 0; u < 2; ++u) {
+      float v = acc[u];
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
+      if (gl == 0 && ok[u]) compact[cur[u].pos] = old[u] + round_to<DT>(v);
     }
+    cur0 = nx0;
+    cur1 = nx1;
   }
 }
 
@@ -492,6 +540,21 @@ int grid_for(int64_t n, int per_cu = 8) {
 
 using namespace usaf;
 
+namespace {
+// Blocks of 256 threads of `kernel` that stay resident on one CU (at least 1).
+// The position-list kernels launch exactly that many per CU: a second round of
+// blocks would walk the per-die slices of the list again from the start and
+// fetch every expert's operands into L2 a second time.
+int resident_blocks_per_cu(const void* kernel) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  return n;
+}
+}  // namespace
+
 extern "C" int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const int32_t* rows, int64_t S, int64_t C,
                                          void* out, int64_t ld_out, void* stream) {
   if (S < 0 || C < 0 || ld_in < C || ld_out < S) return set_error(USAF_ERR_INVALID, "gather_transpose: bad sizes");
@@ -525,8 +588,10 @@ extern "C" int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t
   if (((uintptr_t)rowT & 15) || ((uintptr_t)colT & 15))
     return set_error(USAF_ERR_INVALID, "sddmm_masked: rowT and colT must be 16-byte aligned");
   if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "sddmm_masked: dtype must be 16-bit");
+  static const int per_cu_b = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_kernel<USAF_BF16>));
+  static const int per_cu_h = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_kernel<USAF_F16>));
   int64_t blocks = (n_pos + 15) / 16;
-  const int64_t cap = (int64_t)device_cu_count() * 16;
+  const int64_t cap = (int64_t)device_cu_count() * (dtype == USAF_BF16 ? per_cu_b : per_cu_h);
   if (blocks > cap) blocks = cap;
   hipStream_t st = as_stream(stream);
   if (dtype == USAF_BF16)
@@ -621,8 +686,10 @@ extern "C" int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, 
   if (((uintptr_t)row_blk & 15) || ((uintptr_t)col_blk & 15))
     return set_error(USAF_ERR_INVALID, "sddmm_blocked: operands must be 16-byte aligned");
   if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "sddmm_blocked: dtype must be 16-bit");
+  static const int per_cu_b = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_blocked_kernel<USAF_BF16>));
+  static const int per_cu_h = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_blocked_kernel<USAF_F16>));
   int64_t blocks = (n_pos + 15) / 16;
-  const int64_t cap = (int64_t)device_cu_count() * 16;
+  const int64_t cap = (int64_t)device_cu_count() * (dtype == USAF_BF16 ? per_cu_b : per_cu_h);
   if (blocks > cap) blocks = cap;
   hipStream_t st = as_stream(stream);
   if (dtype == USAF_BF16)
