@@ -119,6 +119,17 @@ int usaf_hip_route_topk_bwd(const void* dweights, int32_t weights_dtype, const f
                             int64_t top_k, int32_t norm_topk_prob, void* dlogits, int32_t logits_dtype,
                             void* stream);
 
+/*
+ * Weight gradient of the router's linear layer (autograd of qwen3moe_dml.py:72,
+ * router_logits = F.linear(hs, router.weight)):
+ *   dw[e, h] = dtype( sum_t fp32(dlogits[t, e]) * fp32(x[t, h]) )      [E, H]
+ * dlogits [T, E] and x [T, H] row-major 16-bit; E and H multiples of 8, 16-byte
+ * aligned; workspace fp32 [usaf_hip_router_dw_ws_floats(T, E, H)].
+ */
+int64_t usaf_hip_router_dw_ws_floats(int64_t T, int64_t E, int64_t H);
+int usaf_hip_router_dw(const void* dlogits, const void* x, int64_t T, int64_t E, int64_t H, int32_t dtype, void* dw,
+                       float* workspace, void* stream);
+
 /* int32 workspace entries usaf_hip_bucket_by_expert needs for T tokens, E experts. */
 int64_t usaf_hip_bucket_workspace_ints(int64_t T, int64_t E);
 

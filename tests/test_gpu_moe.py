@@ -660,3 +660,26 @@ def test_sddmm_blocked_ragged_experts(gpu_device, dtype):
     assert rel_err(got - init.double(), ref - init.double()) <= TOL[dtype]
     e0 = (act // (R * C)) == 0
     assert torch.equal(got[e0], init.double()[e0])
+
+
+@pytest.mark.parametrize("T,E,H", [(4096, 128, 2048), (100, 16, 264), (1, 8, 8), (1000, 256, 136), (0, 8, 16)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_router_dw_vs_fp64(gpu_device, T, E, H, dtype):
+    _say(f"router weight gradient T={T} E={E} H={H} {dtype}")
+    from usaf_amd import _native as N
+    g = torch.Generator().manual_seed(T + E + H)
+    dl = torch.randn(T, E, generator=g).to(dtype)
+    x = torch.randn(T, H, generator=g).to(dtype)
+    lib = N.load()
+    ws = torch.empty(max(1, int(lib.usaf_hip_router_dw_ws_floats(T, E, H))), dtype=torch.float32, device=gpu_device)
+    dw = torch.full((E, H), 3.0, dtype=dtype, device=gpu_device)
+    dl_d, x_d = dl.to(gpu_device), x.to(gpu_device)  # held until the kernel has run
+    N.call("usaf_hip_router_dw", dl_d.data_ptr(), x_d.data_ptr(), T, E, H, N.dtype_code(dtype), dw.data_ptr(),
+           ws.data_ptr(), N.stream_ptr(gpu_device))
+    torch.cuda.synchronize()
+    ref = dl.double().t() @ x.double()
+    mag = dl.double().abs().t() @ x.double().abs()
+    got = dw.cpu().double()
+    # one rounding to the dtype plus the fp32 summation bound
+    tol = torch.finfo(dtype).eps * ref.abs() + max(T, 1) * 2.0 ** -23 * mag
+    assert torch.all((got - ref).abs() <= tol)

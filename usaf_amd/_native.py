@@ -55,6 +55,7 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_blocked_layout": [_c_p, _c_i64, _c_i64, _c_p, _c_p],
     "usaf_hip_gather_transpose_blocked": [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p],
     "usaf_hip_sddmm_blocked": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p],
+    "usaf_hip_router_dw": [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p],
     "usaf_hip_moe_combine_bwd_blocked": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p,
                                          _c_p, _c_p, _c_p],
     "usaf_hip_sddmm_masked": [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p,
@@ -69,6 +70,7 @@ _VALUE_FUNCS: dict[str, tuple] = {
     "usaf_hip_blocked_elems": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "usaf_hip_blocked_table_elems": (_c_i64, [_c_i64, _c_i64]),
     "usaf_hip_combine_bwd_blocked_ws_floats": (_c_i64, [_c_i64, _c_i64]),
+    "usaf_hip_router_dw_ws_floats": (_c_i64, [_c_i64, _c_i64, _c_i64]),
 }
 
 _lock = threading.Lock()

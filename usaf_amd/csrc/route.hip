@@ -469,6 +469,104 @@ int check_route_args(const char* what, int64_t T, int64_t E, int64_t k) {
   return USAF_OK;
 }
 
+// ---- router weight gradient ---------------------------------------------------------
+// dW[e, h] = dtype( sum_t fp32(dl[t, e]) * fp32(x[t, h]) ): the weight gradient of
+// the router's F.linear (qwen3moe_dml.py:72), a GEMM whose contraction runs over
+// the tokens -- the slow index of both operands.  A block computes a 128 (e) x
+// 128 (h) tile over one split of the tokens with v_mfma_f32_32x32x16; 64-token
+// chunks of both operands are transposed through LDS (tt_write) so that each
+// MFMA fragment (8 consecutive tokens) is one 16-byte LDS read.  The fp32 tile
+// goes to ws[split]; router_dw_reduce_kernel adds the splits in order and rounds.
+// Wave w owns experts [32 w, 32 w + 32) x all 128 columns (4 accumulator blocks).
+typedef float rdw_f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 rdw_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 rdw_f16x8 __attribute__((ext_vector_type(8)));
+
+template <int DT>
+__device__ __forceinline__ rdw_f32x16 rdw_mfma(uint4 a, uint4 b, rdw_f32x16 c) {
+  if constexpr (DT == USAF_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(rdw_bf16x8, a), __builtin_bit_cast(rdw_bf16x8, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(rdw_f16x8, a), __builtin_bit_cast(rdw_f16x8, b),
+                                                  c, 0, 0, 0);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void router_dw_kernel(const uint16_t* __restrict__ dl, const uint16_t* __restrict__ x,
+                                                        int64_t T, int E, int64_t H, int64_t t_per_split,
+                                                        float* __restrict__ ws) {
+  __shared__ __align__(16) uint32_t sA[2][TT_DWORDS];  // experts e0 + [0, 64), e0 + [64, 128)
+  __shared__ __align__(16) uint32_t sB[2][TT_DWORDS];  // columns h0 + [0, 64), h0 + [64, 128)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t h0 = (int64_t)blockIdx.x * 128;
+  const int e0 = (int)blockIdx.y * 128;
+  const int64_t t_beg = (int64_t)blockIdx.z * t_per_split;
+  const int64_t t_end = t_beg + t_per_split < T ? t_beg + t_per_split : T;
+  const int sp = tid >> 3, cg = tid & 7;  // writer cell: tokens 2 sp, 2 sp + 1; 8 columns at 8 cg
+  rdw_f32x16 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = rdw_f32x16{};
+  uint4 ra[2][2], rb[2][2];  // [half][token of the pair]
+  auto load = [&](int64_t c0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int64_t t = c0 + 2 * sp + u;
+        const int e = e0 + 64 * q + 8 * cg;
+        const int64_t h = h0 + 64 * q + 8 * cg;
+        ra[q][u] = (t < t_end && e < E) ? *reinterpret_cast<const uint4*>(dl + t * E + e) : make_uint4(0, 0, 0, 0);
+        rb[q][u] = (t < t_end && h < H) ? *reinterpret_cast<const uint4*>(x + t * H + h) : make_uint4(0, 0, 0, 0);
+      }
+  };
+  load(t_beg);
+  for (int64_t c0 = t_beg; c0 < t_end; c0 += 64) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      tt_write(sA[q], sp, cg, ra[q][0], ra[q][1]);
+      tt_write(sB[q], sp, cg, rb[q][0], rb[q][1]);
+    }
+    __syncthreads();
+    if (c0 + 64 < t_end) load(c0 + 64);  // next chunk in flight during this chunk's MFMAs
+    const int ea = 32 * wave + (lane & 31);  // this lane's A row (expert within the tile)
+#pragma unroll
+    for (int kb = 0; kb < 64; kb += 16) {
+      const int sg = (kb >> 3) + (lane >> 5);
+      const uint4 a = tt_read(sA[ea >> 6], ea & 63, sg);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int hb = 32 * j + (lane & 31);
+        const uint4 b = tt_read(sB[hb >> 6], hb & 63, sg);
+        acc[j] = rdw_mfma<DT>(a, b, acc[j]);
+      }
+    }
+    __syncthreads();
+  }
+  // acc[j][r]: expert e0 + 32 wave + 8 (r >> 2) + 4 (lane >> 5) + (r & 3), column h0 + 32 j + (lane & 31)
+  float* const out = ws + (int64_t)blockIdx.z * E * H;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t h = h0 + 32 * j + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int e = e0 + 32 * wave + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (e < E && h < H) out[(int64_t)e * H + h] = acc[j][r];
+    }
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void router_dw_reduce_kernel(const float* __restrict__ ws, int n_split, int64_t n,
+                                                               uint16_t* __restrict__ dw) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float a = 0.f;
+  for (int q = 0; q < n_split; ++q) a += ws[(int64_t)q * n + i];
+  store_from_f32<DT>(dw, i, a);
+}
+
 }  // namespace
 }  // namespace usaf
 
@@ -579,4 +677,45 @@ extern "C" int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, c
                                                               token_idx, slot_w, offsets, (int)E, H, (uint16_t*)dcur,
                                                               dweights);
   return check_launch("moe_combine_bwd");
+}
+
+extern "C" int64_t usaf_hip_router_dw_ws_floats(int64_t T, int64_t E, int64_t H) {
+  if (T < 0 || E <= 0 || H <= 0) return -1;
+  const int64_t tiles = ((H + 127) / 128) * ((E + 127) / 128);
+  const int64_t chunks = (T + 63) / 64;
+  int64_t ks = (256 + tiles - 1) / tiles;
+  if (ks > chunks) ks = chunks;
+  if (ks < 1) ks = 1;
+  return ks * E * H;
+}
+
+extern "C" int usaf_hip_router_dw(const void* dlogits, const void* x, int64_t T, int64_t E, int64_t H, int32_t dtype,
+                                  void* dw, float* workspace, void* stream) {
+  if (T < 0 || E <= 0 || H <= 0) return set_error(USAF_ERR_INVALID, "router_dw: bad sizes");
+  if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "router_dw: dtype must be fp16/bf16");
+  if (!dw || !workspace || (T > 0 && (!dlogits || !x))) return set_error(USAF_ERR_INVALID, "router_dw: null pointer");
+  if (E % 8 != 0 || H % 8 != 0 || (((uintptr_t)dlogits | (uintptr_t)x) & 15))
+    return set_error(USAF_ERR_UNSUPPORTED, "router_dw: needs E, H %% 8 == 0 and 16-byte aligned operands");
+  if (E > 0x7fffffff || H > 0x7fffffff || T > 0x7fffffff) return set_error(USAF_ERR_INVALID, "router_dw: too large");
+  const int64_t tiles_h = (H + 127) / 128, tiles_e = (E + 127) / 128, chunks = (T + 63) / 64;
+  int64_t ks = (256 + tiles_h * tiles_e - 1) / (tiles_h * tiles_e);
+  if (ks > chunks) ks = chunks;
+  if (ks < 1) ks = 1;
+  const int64_t t_per_split = ((chunks + ks - 1) / ks) * 64;
+  ks = T > 0 ? (T + t_per_split - 1) / t_per_split : 1;  // splits actually holding tokens (<= workspace count)
+  if (tiles_h > 0x7fffffff || tiles_e > 65535 || ks > 65535) return set_error(USAF_ERR_INVALID, "router_dw: too large");
+  hipStream_t st = as_stream(stream);
+  const dim3 grid((unsigned)tiles_h, (unsigned)tiles_e, (unsigned)ks);
+  const int64_t n = E * H;
+  const unsigned rb = (unsigned)((n + 255) / 256);
+  if (dtype == USAF_BF16) {
+    router_dw_kernel<USAF_BF16><<<grid, 256, 0, st>>>((const uint16_t*)dlogits, (const uint16_t*)x, T, (int)E, H,
+                                                      t_per_split, workspace);
+    router_dw_reduce_kernel<USAF_BF16><<<rb, 256, 0, st>>>(workspace, (int)ks, n, (uint16_t*)dw);
+  } else {
+    router_dw_kernel<USAF_F16><<<grid, 256, 0, st>>>((const uint16_t*)dlogits, (const uint16_t*)x, T, (int)E, H,
+                                                     t_per_split, workspace);
+    router_dw_reduce_kernel<USAF_F16><<<rb, 256, 0, st>>>(workspace, (int)ks, n, (uint16_t*)dw);
+  }
+  return check_launch("router_dw");
 }

@@ -10,30 +10,6 @@
 namespace usaf {
 namespace {
 
-// ---- 64-slot x 64-feature transposes through LDS ---------------------------------
-// The tile is stored feature-major, 32 dwords (64 slots) per feature row; a dword
-// holds two consecutive slots.  Writer thread (sp, cg) = (tid >> 3, tid & 7) has
-// the 16-byte chunks of features [8 cg, 8 cg + 8) of slots 2 sp and 2 sp + 1 and
-// writes 8 dwords, one per feature; reader (cl, sg) fetches the 16 bytes of
-// feature cl, slots [8 sg, 8 sg + 8).  The 16-byte groups of a row are XOR
-// swizzled by the feature's group of 8 (cl >> 3), which keeps the writes of a
-// wave at two lanes per bank and the reads at full 16-byte vectors.
-constexpr int TT_DWORDS = 64 * 32;
-__device__ __forceinline__ int tt_index(int col, int slot_pair) {
-  return col * 32 + ((((slot_pair >> 2) ^ (col >> 3)) & 7) << 2) + (slot_pair & 3);
-}
-__device__ __forceinline__ void tt_write(uint32_t* tile, int sp, int cg, uint4 a, uint4 b) {
-  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    tile[tt_index(8 * cg + 2 * q, sp)] = __builtin_amdgcn_perm(bw[q], aw[q], 0x05040100u);      // low halves
-    tile[tt_index(8 * cg + 2 * q + 1, sp)] = __builtin_amdgcn_perm(bw[q], aw[q], 0x07060302u);  // high halves
-  }
-}
-__device__ __forceinline__ uint4 tt_read(const uint32_t* tile, int cl, int sg) {
-  return *reinterpret_cast<const uint4*>(&tile[tt_index(cl, 4 * sg)]);
-}
-
 // out[c, s] = in[rows ? rows[s] : s, c] for c < C, s < S; 16-bit elements.
 // A 64 (s) x 64 (c) tile goes through LDS stored column-major, so that the row
 // reads and the column writes are both 16-byte vectors over contiguous runs.

@@ -505,6 +505,40 @@ class RouteTopKFn(torch.autograd.Function):
         return dlogits, None, None, None
 
 
+class RouterLinearFn(torch.autograd.Function):
+    """router_logits = F.linear(hs, W) (qwen3moe_dml.py:72): forward and grad-input
+    by the library GEMM, the weight gradient (a contraction over the tokens) by
+    usaf_hip_router_dw."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor):
+        ctx.save_for_backward(x, w)
+        return torch.nn.functional.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, dlogits: torch.Tensor):
+        x, w = ctx.saved_tensors
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.mm(dlogits, w)
+        if ctx.needs_input_grad[1]:
+            dlogits = dlogits.contiguous()
+            T, E = dlogits.shape
+            H = x.shape[1]
+            lib = N.load()
+            ws = torch.empty(max(1, int(lib.usaf_hip_router_dw_ws_floats(T, E, H))), dtype=torch.float32,
+                             device=x.device)
+            dw = torch.empty(E, H, dtype=w.dtype, device=x.device)
+            N.call("usaf_hip_router_dw", dlogits.data_ptr(), x.data_ptr(), T, E, H, N.dtype_code(x.dtype),
+                   dw.data_ptr(), ws.data_ptr(), N.stream_ptr(x.device))
+        return dx, dw
+
+
+def _router_dw_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    return (x.dtype in (torch.float16, torch.bfloat16) and w.dtype == x.dtype and x.is_contiguous()
+            and w.shape[0] % 8 == 0 and x.shape[1] % 8 == 0 and x.data_ptr() % 16 == 0)
+
+
 def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_topk_prob: bool,
               experts: ExpertWeights, capture=None, overflow: Optional[torch.Tensor] = None) -> torch.Tensor:
     """qwen3moe_dml.py:67-86: router F.linear (library GEMM), routing kernel,
@@ -519,7 +553,10 @@ def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_to
     slots past the routed pairs cost no GEMM work."""
     shape = hs.shape
     x = hs.reshape(-1, shape[-1])
-    logits = torch.nn.functional.linear(x, router_weight)
+    if _router_dw_ok(x, router_weight):
+        logits = RouterLinearFn.apply(x, router_weight)
+    else:
+        logits = torch.nn.functional.linear(x, router_weight)
     weights = RouteTopKFn.apply(logits, top_k, norm_topk_prob, x.dtype)
     cap = None if overflow is None else x.shape[0] * min(top_k + 1, router_weight.shape[0])
     out = routed_experts(x, weights, experts, capture, slot_capacity=cap, overflow=overflow)
