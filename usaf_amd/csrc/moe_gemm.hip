@@ -1168,9 +1168,13 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
 
   // tile ordinal -> expert, first slot, rows, n-tile (the m-tile list of
   // mtile_decode: every full-size tile before every light remainder; tables in LDS)
+  // Odd blocks of a die walk their tiles in reverse, light remainders first: the
+  // die's blocks then leave their tiles at two phases instead of all at once,
+  // which halves the write burst of the epilogues.
+  const bool rev = (walk.local_b & 1) != 0;
   auto decode = [&](int ord) {
     int64_t mt, nt;
-    walk.decode(first + (int64_t)ord * stride, mt, nt);
+    walk.decode(first + (int64_t)(rev ? n_my - 1 - ord : ord) * stride, mt, nt);
     int e, j;
     if (mt < s_h[E]) {
       e = prefix_owner(s_h, E, mt);

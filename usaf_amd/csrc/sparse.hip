@@ -377,77 +377,63 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
   const int64_t die_blocks = ((int64_t)gridDim.x + dies - 1 - die) / dies;
   const int64_t lo = n_pos * die / dies, hi = n_pos * (die + 1) / dies;
   const int64_t n_grp = die_blocks * (blockDim.x >> 4);
-  // Two positions per iteration (p, p + n_grp), their operand loads issued
-  // together with the old compact values; the indices of the next two are
-  // fetched one iteration ahead, so each iteration waits on one round trip.
-  struct Idx {
-    uint32_t code, col;
-    int64_t pos;
-  };
-  auto fetch = [&](int64_t q) {
-    Idx r{0xFFFFFFFFu, 0u, 0};
-    if (q < hi) {
-      r.code = (uint32_t)rcode[q];
-      r.col = (uint32_t)col_idx[q];
-      r.pos = pos_map ? pos_map[q] : q;
+  // Each group takes runs of RUN consecutive positions; the runs of a die's
+  // groups sweep its slice together (run r of group g starts at
+  // lo + (r * n_grp + g) * RUN), so the die's L2 holds about one expert's
+  // operands at a time.  Positions of one weight row are adjacent, so a run
+  // mostly repeats its row: the row operand's first two 128-slot windows stay
+  // in registers while the row does not change, halving the loads per position.
+  constexpr int RUN = 8;
+  const int64_t gi = (int64_t)(blockIdx.x / dies) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  for (int64_t base = lo + gi * RUN; base < hi; base += n_grp * RUN) {
+    const int64_t end = base + RUN < hi ? base + RUN : hi;
+    uint32_t cached = 0xFFFFFFFFu;
+    int ld = 0;
+    const uint16_t* rv = rowB;
+    uint4 r0 = make_uint4(0, 0, 0, 0), r1 = make_uint4(0, 0, 0, 0);
+    for (int64_t p = base; p < end; ++p) {
+      const uint32_t code = (uint32_t)rcode[p];
+      const uint32_t i = (uint32_t)col_idx[p];
+      const uint32_t e = code >> 21, o = code & 0x1FFFFFu;
+      if (e >= (uint32_t)E || o >= (uint32_t)R || i >= (uint32_t)C) continue;
+      const int64_t pos = pos_map ? pos_map[p] : p;
+      const float old = gl == 0 ? compact[pos] : 0.f;
+      const int pe = s_pre[e];
+      if (code != cached) {  // uniform across the group
+        cached = code;
+        ld = s_pre[e + 1] - pe;
+        rv = rowB + (int64_t)R * pe + (int64_t)o * ld;
+        r0 = 8 * gl < ld ? *reinterpret_cast<const uint4*>(rv + 8 * gl) : make_uint4(0, 0, 0, 0);
+        r1 = 8 * gl + 128 < ld ? *reinterpret_cast<const uint4*>(rv + 8 * gl + 128) : make_uint4(0, 0, 0, 0);
+      }
+      const uint16_t* cv = colB + (int64_t)C * pe + (int64_t)i * ld;
+      float acc = 0.f;
+      if (8 * gl < ld) {
+        const uint4 c = *reinterpret_cast<const uint4*>(cv + 8 * gl);
+        acc = dot2<DT>(r0.x, c.x, acc);
+        acc = dot2<DT>(r0.y, c.y, acc);
+        acc = dot2<DT>(r0.z, c.z, acc);
+        acc = dot2<DT>(r0.w, c.w, acc);
+      }
+      if (8 * gl + 128 < ld) {
+        const uint4 c = *reinterpret_cast<const uint4*>(cv + 8 * gl + 128);
+        acc = dot2<DT>(r1.x, c.x, acc);
+        acc = dot2<DT>(r1.y, c.y, acc);
+        acc = dot2<DT>(r1.z, c.z, acc);
+        acc = dot2<DT>(r1.w, c.w, acc);
+      }
+      for (int w = 8 * gl + 256; w < ld; w += 128) {  // experts past 256 slots
+        const uint4 a = *reinterpret_cast<const uint4*>(rv + w);
+        const uint4 c = *reinterpret_cast<const uint4*>(cv + w);
+        acc = dot2<DT>(a.x, c.x, acc);
+        acc = dot2<DT>(a.y, c.y, acc);
+        acc = dot2<DT>(a.z, c.z, acc);
+        acc = dot2<DT>(a.w, c.w, acc);
+      }
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+      if (gl == 0) compact[pos] = old + round_to<DT>(acc);
     }
-    return r;
-  };
-  const int64_t first = lo + (int64_t)(blockIdx.x / dies) * (blockDim.x >> 4) + (threadIdx.x >> 4);
-  Idx cur0 = fetch(first), cur1 = fetch(first + n_grp);
-  for (int64_t p = first; p < hi; p += 2 * n_grp) {
-    const Idx nx0 = fetch(p + 2 * n_grp), nx1 = fetch(p + 3 * n_grp);
-    const Idx cur[2] = {cur0, cur1};
-    bool ok[2];
-    int ld[2];
-    const uint16_t* rv[2];
-    const uint16_t* cv[2];
-    float old[2], acc[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint32_t e = cur[u].code >> 21, o = cur[u].code & 0x1FFFFFu, i = cur[u].col;
-      ok[u] = cur[u].code != 0xFFFFFFFFu && e < (uint32_t)E && o < (uint32_t)R && i < (uint32_t)C;
-      const int pe = ok[u] ? s_pre[e] : 0;
-      ld[u] = ok[u] ? s_pre[e + 1] - pe : 0;
-      rv[u] = rowB + (int64_t)R * pe + (int64_t)(ok[u] ? o : 0) * ld[u];
-      cv[u] = colB + (int64_t)C * pe + (int64_t)(ok[u] ? i : 0) * ld[u];
-      old[u] = (ok[u] && gl == 0) ? compact[cur[u].pos] : 0.f;
-      acc[u] = 0.f;
-    }
-    const int ldm = ld[0] > ld[1] ? ld[0] : ld[1];
-    for (int w = 8 * gl; w < ldm; w += 256) {
-      uint4 a[2][2], c[2][2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          a[u][h] = make_uint4(0, 0, 0, 0);
-          c[u][h] = make_uint4(0, 0, 0, 0);
-          if (w + 128 * h < ld[u]) {
-            a[u][h] = *reinterpret_cast<const uint4*>(rv[u] + w + 128 * h);
-            c[u][h] = *reinterpret_cast<const uint4*>(cv[u] + w + 128 * h);
-          }
-        }
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          if (w + 128 * h < ld[u]) {
-            acc[u] = dot2<DT>(a[u][h].x, c[u][h].x, acc[u]);
-            acc[u] = dot2<DT>(a[u][h].y, c[u][h].y, acc[u]);
-            acc[u] = dot2<DT>(a[u][h].z, c[u][h].z, acc[u]);
-            acc[u] = dot2<DT>(a[u][h].w, c[u][h].w, acc[u]);
-          }
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      float v = acc[u];
-#pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 16);
-      if (gl == 0 && ok[u]) compact[cur[u].pos] = old[u] + round_to<DT>(v);
-    }
-    cur0 = nx0;
-    cur1 = nx1;
   }
 }
 
