@@ -135,7 +135,7 @@ def moe_step_flops(T, H, I, E, k, n_active_gu, n_active_dn):
 def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfloat16):
     from usaf_amd import moe as G
     from usaf_amd.moe_loader import SparseGradStore
-    from usaf_amd.sparse_optim import SparseAdam
+    from usaf_amd.sparse_optim import MomentumSGD, SparseAdam
     gen = torch.Generator(device=dev).manual_seed(seed)
     q = {}
     for name, shp in (("gate_up_proj", (E, 2 * I, H)), ("down_proj", (E, H, I))):
@@ -157,10 +157,8 @@ def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfl
     opt = SparseAdam(masters, active_idx=active, lr=2e-4, weight_decay=0.005, compact_params=True)
     hs = torch.randn(T, H, device=dev, generator=gen).to(dtype).requires_grad_(True)
     router_w = (torch.randn(E, H, device=dev, generator=gen) / H ** 0.5).to(dtype).requires_grad_(True)
-    # single-tensor SGD (foreach=False): four full-grid elementwise kernels; the fused and
-    # foreach variants split this one 262,144-element tensor into four 65,536-element chunks,
-    # one workgroup each, and take 2-3x longer
-    sgd = torch.optim.SGD([router_w], lr=2e-4, momentum=0.9, weight_decay=0.005, foreach=False)
+    # torch.optim.SGD(momentum=0.9) semantics (train.py:493-498) as one fused kernel
+    sgd = MomentumSGD([router_w], lr=2e-4, momentum=0.9, weight_decay=0.005)
     dy = torch.randn(T, H, device=dev, generator=gen).to(dtype)
     n_act = {n.rsplit(".", 1)[1]: int(i.numel()) for n, i in active.items()}
     return dict(experts=experts, store=store, opt=opt, hs=hs, router_w=router_w, sgd=sgd, dy=dy, k=k,

@@ -301,6 +301,13 @@ int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t ldT, const
 int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, float* v, int64_t n, double lr, double beta1,
                               double beta2, double eps, double weight_decay, int64_t step, void* stream);
 
+/* torch.optim.SGD.step with momentum (dampening 0, no Nesterov) for one tensor, the
+ * router's optimizer in the reference trainer (train.py:493-498, 667-672):
+ * d = grad + wd*p; buf = d on the first step, else buf*momentum + d; p -= lr*buf;
+ * rounded to the tensor dtype after each torch op as the single-tensor path does. */
+int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momentum_buf, int64_t n, int32_t dtype, double lr,
+                               double momentum, double weight_decay, int32_t first_step, void* stream);
+
 /* out = in / denom (fp32) and *finite_flag = 0 if any result is inf/NaN (train.py:661-663);
  * the caller sets *finite_flag = 1 beforehand. */
 int usaf_hip_scale_check(const float* in, float* out, int64_t n, float denom, int32_t* finite_flag, void* stream);

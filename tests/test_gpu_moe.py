@@ -683,3 +683,41 @@ def test_router_dw_vs_fp64(gpu_device, T, E, H, dtype):
     # one rounding to the dtype plus the fp32 summation bound
     tol = torch.finfo(dtype).eps * ref.abs() + max(T, 1) * 2.0 ** -23 * mag
     assert torch.all((got - ref).abs() <= tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_momentum_sgd_matches_torch(gpu_device, dtype):
+    _say(f"MomentumSGD vs torch.optim.SGD single-tensor, 3 steps from equal states, {dtype}")
+    from usaf_amd.sparse_optim import MomentumSGD
+    g = torch.Generator().manual_seed(77)
+    p0 = (torch.randn(128, 2048, generator=g) * 0.05).to(dtype).to(gpu_device)
+    a = p0.clone().requires_grad_(True)
+    b = p0.clone().requires_grad_(True)
+    ours = MomentumSGD([a], lr=2e-4, momentum=0.9, weight_decay=0.005)
+    ref = torch.optim.SGD([b], lr=2e-4, momentum=0.9, weight_decay=0.005, foreach=False)
+    for step in range(3):
+        # every step starts from torch's state, so each step's arithmetic is compared alone
+        with torch.no_grad():
+            a.copy_(b)
+            if step > 0:
+                ours._buf[0].copy_(ref.state[b]["momentum_buffer"])
+        grad = torch.randn(128, 2048, generator=g).to(dtype).to(gpu_device)
+        a.grad = grad.clone()
+        b.grad = grad.clone()
+        p_prev = b.detach().clone()
+        buf_prev = ref.state[b]["momentum_buffer"].clone() if step > 0 else None
+        ours.step()
+        ref.step()
+        torch.cuda.synchronize()
+        for what, x, y in (("p", a.detach(), b.detach()), ("buf", ours._buf[0], ref.state[b]["momentum_buffer"])):
+            diff = (x.float() - y.float()).abs()
+            # equal except where an fp32 multiply-add rounds one way fused and the other
+            # unfused and the 16-bit result flips by one ulp
+            ulp = torch.finfo(dtype).eps * y.float().abs() + 2.0 ** -24
+            k = int(torch.argmax(diff - ulp))
+            assert torch.all(diff <= ulp), (
+                f"step {step} {what}[{k}]: ours {float(x.flatten()[k])!r} torch {float(y.flatten()[k])!r}, "
+                f"grad {float(grad.flatten()[k])!r} p_prev {float(p_prev.flatten()[k])!r} buf_prev "
+                f"{None if buf_prev is None else float(buf_prev.flatten()[k])!r} buf ours "
+                f"{float(ours._buf[0].flatten()[k])!r} torch {float(ref.state[b]['momentum_buffer'].flatten()[k])!r}")
+            assert float((diff > 0).float().mean()) < 1e-3

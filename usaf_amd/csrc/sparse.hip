@@ -462,6 +462,43 @@ __global__ __launch_bounds__(256) void sparse_adam_kernel(float* __restrict__ p,
   }
 }
 
+// torch.optim.SGD's single-tensor step with momentum (dampening 0, no Nesterov)
+// for the router weight (train.py:493-498, 667-672), in one pass:
+//   d = grad + wd * p; buf = d (first step) or buf * momentum + d; p = p - lr * buf
+// with torch's per-op rounding to the tensor dtype: each `a + alpha * b` is one
+// fp32 fused multiply-add, rounded once; mul_ multiplies by the fp32 factor and
+// rounds before the add.
+template <int DT>
+__global__ __launch_bounds__(256) void sgd_momentum_kernel(void* __restrict__ p, const void* __restrict__ grad,
+                                                           void* __restrict__ buf, int64_t n, float lr,
+                                                           float momentum, float wd, int first) {
+#pragma clang fp contract(off)
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  // Each fp32 result is pinned (asm) before its conversion: otherwise the
+  // compiler folds product-then-fp16 into v_fma_mix, which rounds once from the
+  // exact product instead of rounding to fp32 first as torch's kernels do.
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float pf = load_as_f32<DT>(p, i);
+    float d32 = __builtin_fmaf(wd, pf, load_as_f32<DT>(grad, i));
+    asm volatile("" : "+v"(d32));
+    const float d = round_to<DT>(d32);
+    float b;
+    if (first) {
+      b = d;
+    } else {
+      float bm32 = load_as_f32<DT>(buf, i) * momentum;
+      asm volatile("" : "+v"(bm32));
+      float b32 = round_to<DT>(bm32) + d;
+      asm volatile("" : "+v"(b32));
+      b = round_to<DT>(b32);
+    }
+    store_from_f32<DT>(buf, i, b);
+    float p32 = __builtin_fmaf(-lr, b, pf);
+    asm volatile("" : "+v"(p32));
+    store_from_f32<DT>(p, i, p32);
+  }
+}
+
 __global__ __launch_bounds__(256) void scale_check_kernel(const float* __restrict__ in, float* __restrict__ out,
                                                           int64_t n, float denom, int32_t* __restrict__ finite) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -678,6 +715,31 @@ extern "C" int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, 
       p, grad, m, v, n, (float)lr, (float)beta1, (float)(1.0 - beta1), (float)beta2, (float)(1.0 - beta2),
       (float)eps, (float)weight_decay, bias1, bias2);
   return check_launch("sparse_adam_step");
+}
+
+extern "C" int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momentum_buf, int64_t n, int32_t dtype,
+                                          double lr, double momentum, double weight_decay, int32_t first_step,
+                                          void* stream) {
+  if (n < 0) return set_error(USAF_ERR_INVALID, "sgd_momentum_step: negative n");
+  if (n == 0) return clear_error();
+  if (!p || !grad || !momentum_buf) return set_error(USAF_ERR_INVALID, "sgd_momentum_step: null pointer");
+  hipStream_t st = as_stream(stream);
+  const float lr_f = (float)lr, m_f = (float)momentum, wd_f = (float)weight_decay;
+  const int first = first_step ? 1 : 0;
+  switch (dtype) {
+    case USAF_F32:
+      sgd_momentum_kernel<USAF_F32><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first);
+      break;
+    case USAF_F16:
+      sgd_momentum_kernel<USAF_F16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first);
+      break;
+    case USAF_BF16:
+      sgd_momentum_kernel<USAF_BF16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first);
+      break;
+    default:
+      return set_error(USAF_ERR_INVALID, "sgd_momentum_step: dtype must be fp32, fp16 or bf16");
+  }
+  return check_launch("sgd_momentum_step");
 }
 
 extern "C" int usaf_hip_scale_check(const float* in, float* out, int64_t n, float denom, int32_t* finite_flag,

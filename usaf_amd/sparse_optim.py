@@ -167,3 +167,44 @@ class SparseAdam:
         for name in self._active_ids:
             total += self._m[name].numel() * 4 + self._v[name].numel() * 4
         return total / (1024 * 1024)
+
+
+class MomentumSGD:
+    """torch.optim.SGD(params, lr, momentum, weight_decay) -- dampening 0, no
+    Nesterov -- as the reference trainer steps the router (train.py:493-498,
+    667-672), one fused kernel per tensor (usaf_hip_sgd_momentum_step) with the
+    single-tensor path's per-op rounding.  Parameters without a gradient are
+    skipped, as torch does."""
+
+    def __init__(self, params, lr: float, momentum: float = 0.0, weight_decay: float = 0.0):
+        self.params = [p for p in params]
+        if lr < 0 or momentum < 0 or weight_decay < 0:
+            raise ValueError("MomentumSGD: lr, momentum and weight_decay must be >= 0")
+        self.lr, self.momentum, self.weight_decay = float(lr), float(momentum), float(weight_decay)
+        self._buf: dict[int, torch.Tensor] = {}
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        for p in self.params:
+            if set_to_none:
+                p.grad = None
+            elif p.grad is not None:
+                p.grad.zero_()
+
+    @torch.no_grad()
+    def step(self) -> None:
+        for i, p in enumerate(self.params):
+            g = p.grad
+            if g is None:
+                continue
+            if not p.is_cuda or not p.is_contiguous() or not g.is_contiguous() or g.dtype != p.dtype:
+                raise RuntimeError("MomentumSGD: parameters and gradients must be contiguous GPU tensors of one dtype")
+            buf = self._buf.get(i)
+            first = buf is None
+            if first:
+                buf = torch.empty_like(p)
+                self._buf[i] = buf
+            if self.momentum == 0.0:
+                raise NotImplementedError("MomentumSGD: momentum 0 (plain SGD) is not on the fused path")
+            N.call("usaf_hip_sgd_momentum_step", p.data_ptr(), g.data_ptr(), buf.data_ptr(), p.numel(),
+                   N.dtype_code(p.dtype), self.lr, self.momentum, self.weight_decay, 1 if first else 0,
+                   N.stream_ptr(p.device))
