@@ -120,6 +120,16 @@ int usaf_hip_route_topk_bwd(const void* dweights, int32_t weights_dtype, const f
                             void* stream);
 
 /*
+ * The router forward of qwen3moe_dml.py:72-83 from one call:
+ *   logits [T, E] = dtype(x @ W^T)  (x [T, H], W [E, H], 16-bit, H % 256 == 0),
+ * then usaf_hip_route_topk on those logits: weights [T, E] (weights_dtype),
+ * probs fp32 [T, E] (may be NULL).
+ */
+int usaf_hip_router_fwd(const void* x, const void* w, int64_t T, int64_t E, int64_t H, int32_t dtype, int64_t top_k,
+                        int32_t norm_topk_prob, void* logits, void* weights, int32_t weights_dtype, float* probs,
+                        void* stream);
+
+/*
  * Weight gradient of the router's linear layer (autograd of qwen3moe_dml.py:72,
  * router_logits = F.linear(hs, router.weight)):
  *   dw[e, h] = dtype( sum_t fp32(dlogits[t, e]) * fp32(x[t, h]) )      [E, H]

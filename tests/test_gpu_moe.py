@@ -721,3 +721,30 @@ def test_momentum_sgd_matches_torch(gpu_device, dtype):
                 f"{None if buf_prev is None else float(buf_prev.flatten()[k])!r} buf ours "
                 f"{float(ours._buf[0].flatten()[k])!r} torch {float(ref.state[b]['momentum_buffer'].flatten()[k])!r}")
             assert float((diff > 0).float().mean()) < 1e-3
+
+
+@pytest.mark.parametrize("T,E,H,k,norm", [(4096, 128, 2048, 8, False), (333, 60, 768, 4, True), (5, 8, 256, 2, False),
+                                          (77, 200, 512, 6, False)])
+def test_router_fwd_exact_logits(gpu_device, T, E, H, k, norm):
+    _say(f"fused router forward T={T} E={E} H={H} k={k} norm={norm}")
+    from usaf_amd import _native as N
+    g = torch.Generator().manual_seed(T + E)
+    # few-bit operands: every fp32 partial sum is exact, so the logits are the
+    # fp64 result rounded once to bf16 whatever the summation order
+    x = (torch.randint(-4, 5, (T, H), generator=g).float() / 8).to(torch.bfloat16)
+    w = (torch.randint(-4, 5, (E, H), generator=g).float() / 16).to(torch.bfloat16)
+    logits = (x.double() @ w.double().t()).to(torch.bfloat16)
+    w_ref, p_ref, _ = M.route(logits, k, norm, torch.bfloat16)
+    xd, wd = x.to(gpu_device), w.to(gpu_device)
+    weights = torch.empty(T, E, dtype=torch.bfloat16, device=gpu_device)
+    probs = torch.empty(T, E, dtype=torch.float32, device=gpu_device)
+    lg = torch.empty(T, E, dtype=torch.bfloat16, device=gpu_device)
+    N.call("usaf_hip_router_fwd", xd.data_ptr(), wd.data_ptr(), T, E, H, N.BF16, k, 1 if norm else 0,
+           lg.data_ptr(), weights.data_ptr(), N.BF16, probs.data_ptr(), N.stream_ptr(gpu_device))
+    # the same logits through the unfused routing kernel
+    w2, p2 = G.route_topk(logits.to(gpu_device), k, norm, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(lg.cpu().view(torch.int16), logits.view(torch.int16))
+    assert torch.equal(weights.cpu() != 0, w_ref != 0), "routing mask differs from the oracle"
+    assert torch.equal(weights.cpu().view(torch.int16), w2.cpu().view(torch.int16))
+    assert torch.equal(probs.cpu(), p2.cpu())

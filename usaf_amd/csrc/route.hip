@@ -73,22 +73,13 @@ __device__ __forceinline__ void row_softmax(float (&p)[VPL], const bool (&valid)
   for (int j = 0; j < VPL; ++j) p[j] = p[j] / s;
 }
 
-// One wavefront per token.
-template <int VPL, int LDT, int WDT>
-__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int64_t T, int E, int k,
-                                                         int norm, void* __restrict__ weights,
-                                                         float* __restrict__ probs) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;
-  float p[VPL];
-  bool valid[VPL];
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int e = lane + kWave * j;
-    valid[j] = e < E;
-    p[j] = valid[j] ? load_as_f32<LDT>(logits, t * E + e) : -INFINITY;
-  }
+// Routing of one token by one wavefront, from its logits (VPL per lane,
+// element e = lane + 64 j; invalid entries ignored): softmax, top-k threshold
+// mask, optional renormalisation; writes weights[t, :] and probs[t, :].
+template <int VPL, int WDT>
+__device__ __forceinline__ void route_token(float (&p)[VPL], const bool (&valid)[VPL], int64_t t, int E, int k,
+                                            int norm, void* __restrict__ weights, float* __restrict__ probs,
+                                            int lane) {
   row_softmax<VPL>(p, valid);
   const float thr = kth_largest<VPL>(p, valid, k, lane);
   float w[VPL];
@@ -110,6 +101,25 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict_
     store_from_f32<WDT>(weights, i, w[j]);
     if (probs) probs[i] = p[j];
   }
+}
+
+// One wavefront per token.
+template <int VPL, int LDT, int WDT>
+__global__ __launch_bounds__(256) void route_topk_kernel(const void* __restrict__ logits, int64_t T, int E, int k,
+                                                         int norm, void* __restrict__ weights,
+                                                         float* __restrict__ probs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float p[VPL];
+  bool valid[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + kWave * j;
+    valid[j] = e < E;
+    p[j] = valid[j] ? load_as_f32<LDT>(logits, t * E + e) : -INFINITY;
+  }
+  route_token<VPL, WDT>(p, valid, t, E, k, norm, weights, probs, lane);
 }
 
 // Backward of route_topk: d(weights) -> d(logits) through the mask, the
@@ -556,6 +566,83 @@ __global__ __launch_bounds__(256) void router_dw_kernel(const uint16_t* __restri
   }
 }
 
+// ---- router forward: the logits GEMM ------------------------------------------------
+// logits[t, e] = dtype( sum_h x[t, h] * W[e, h] ), the router's F.linear
+// (qwen3moe_dml.py:72).  A block computes 32 tokens x 32 experts with
+// v_mfma_f32_32x32x16; its four waves split the contraction into quarters and
+// add their partial tiles in LDS in wave order.  Both operand fragments (8
+// consecutive h of one token / one expert) come straight from global memory
+// through a ring of RING register slots, the loads of step s + RING issued before
+// the MFMA of step s.
+template <int DT>
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w, int64_t T, int E,
+                                                            int64_t H, uint16_t* __restrict__ logits) {
+#pragma clang fp contract(off)
+  __shared__ float s_part[4][32 * 33];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * 32;
+  const int e0 = (int)blockIdx.y * 32;
+  // rows past T or E read row 0: their results are never stored, and the loads
+  // stay unpredicated (a conditional load joins its branch with a wait)
+  const int64_t ta = t0 + (lane & 31) < T ? t0 + (lane & 31) : 0;
+  const int eb = e0 + (lane & 31) < E ? e0 + (lane & 31) : 0;
+  // A wave's quarter of the contraction goes in 64-wide chunks.  Within a chunk,
+  // lane half c reads 32 consecutive elements [32 c, 32 c + 32) of its row as
+  // four 16-byte vectors and feeds vector q to MFMA step q: A and B use the same
+  // assignment, so the four steps cover the chunk's 64 products exactly once.
+  const int64_t chunks = H / 256;  // 64-wide chunks per wave quarter
+  const int64_t h0 = (int64_t)wave * chunks * 64 + 32 * (lane >> 5);
+  const uint16_t* xa = x + ta * H + h0;
+  const uint16_t* wb = w + (int64_t)eb * H + h0;
+  rdw_f32x16 acc = rdw_f32x16{};
+  constexpr int RING = 2;  // chunks in flight
+  uint4 ra[RING][4], rb[RING][4];
+#pragma unroll
+  for (int c = 0; c < RING; ++c) {
+    const int64_t cq = c < chunks ? c : chunks - 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ra[c][q] = *reinterpret_cast<const uint4*>(xa + 64 * cq + 8 * q);
+      rb[c][q] = *reinterpret_cast<const uint4*>(wb + 64 * cq + 8 * q);
+    }
+  }
+  for (int64_t c0 = 0; c0 < chunks; c0 += RING) {
+#pragma unroll
+    for (int c = 0; c < RING; ++c) {
+      uint4 a[4], b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a[q] = ra[c][q];
+        b[q] = rb[c][q];
+      }
+      const int64_t cn = c0 + RING + c < chunks ? c0 + RING + c : chunks - 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        ra[c][q] = *reinterpret_cast<const uint4*>(xa + 64 * cn + 8 * q);
+        rb[c][q] = *reinterpret_cast<const uint4*>(wb + 64 * cn + 8 * q);
+      }
+      if (c0 + c < chunks)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = rdw_mfma<DT>(a[q], b[q], acc);
+    }
+  }
+  // acc[r]: token 8 (r >> 2) + 4 (lane >> 5) + (r & 3), expert e0 + (lane & 31)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s_part[wave][(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 33 + (lane & 31)] = acc[r];
+  __syncthreads();
+  for (int i = tid; i < 32 * 32; i += 256) {
+    const int tl = i >> 5, el = i & 31;
+    const int64_t t = t0 + tl;
+    const int e = e0 + el;
+    if (t < T && e < E) {
+      const int j = tl * 33 + el;
+      const float v = ((s_part[0][j] + s_part[1][j]) + s_part[2][j]) + s_part[3][j];
+      store_from_f32<DT>(logits, t * E + e, v);
+    }
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void router_dw_reduce_kernel(const float* __restrict__ ws, int n_split, int64_t n,
                                                                uint16_t* __restrict__ dw) {
@@ -718,4 +805,27 @@ extern "C" int usaf_hip_router_dw(const void* dlogits, const void* x, int64_t T,
     router_dw_reduce_kernel<USAF_F16><<<rb, 256, 0, st>>>(workspace, (int)ks, n, (uint16_t*)dw);
   }
   return check_launch("router_dw");
+}
+
+extern "C" int usaf_hip_router_fwd(const void* x, const void* w, int64_t T, int64_t E, int64_t H, int32_t dtype,
+                                   int64_t top_k, int32_t norm_topk_prob, void* logits, void* weights,
+                                   int32_t weights_dtype, float* probs, void* stream) {
+  if (int rc = check_route_args("router_fwd", T, E, top_k)) return rc;
+  if (H <= 0) return set_error(USAF_ERR_INVALID, "router_fwd: bad sizes");
+  if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "router_fwd: dtype must be fp16/bf16");
+  if (T == 0) return clear_error();
+  if (!x || !w || !logits || !weights) return set_error(USAF_ERR_INVALID, "router_fwd: null pointer");
+  if (H % 256 != 0 || (((uintptr_t)x | (uintptr_t)w) & 15))
+    return set_error(USAF_ERR_UNSUPPORTED, "router_fwd: needs H %% 256 == 0 and 16-byte aligned operands");
+  if ((T + 31) / 32 > 0x7fffffff) return set_error(USAF_ERR_INVALID, "router_fwd: too many tokens");
+  hipStream_t st = as_stream(stream);
+  const dim3 grid((unsigned)((T + 31) / 32), (unsigned)((E + 31) / 32));
+  if (dtype == USAF_BF16)
+    router_logits_kernel<USAF_BF16><<<grid, 256, 0, st>>>((const uint16_t*)x, (const uint16_t*)w, T, (int)E, H,
+                                                          (uint16_t*)logits);
+  else
+    router_logits_kernel<USAF_F16><<<grid, 256, 0, st>>>((const uint16_t*)x, (const uint16_t*)w, T, (int)E, H,
+                                                         (uint16_t*)logits);
+  if (int rc = check_launch("router_fwd/logits")) return rc;
+  return usaf_hip_route_topk(logits, dtype, T, E, top_k, norm_topk_prob, weights, weights_dtype, probs, stream);
 }

@@ -522,16 +522,59 @@ class RouterLinearFn(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = torch.mm(dlogits, w)
         if ctx.needs_input_grad[1]:
-            dlogits = dlogits.contiguous()
-            T, E = dlogits.shape
-            H = x.shape[1]
-            lib = N.load()
-            ws = torch.empty(max(1, int(lib.usaf_hip_router_dw_ws_floats(T, E, H))), dtype=torch.float32,
-                             device=x.device)
-            dw = torch.empty(E, H, dtype=w.dtype, device=x.device)
-            N.call("usaf_hip_router_dw", dlogits.data_ptr(), x.data_ptr(), T, E, H, N.dtype_code(x.dtype),
-                   dw.data_ptr(), ws.data_ptr(), N.stream_ptr(x.device))
+            dw = _router_dw(x, dlogits, w.dtype)
         return dx, dw
+
+
+def _router_dw(x: torch.Tensor, dlogits: torch.Tensor, w_dtype: torch.dtype) -> torch.Tensor:
+    dlogits = dlogits.contiguous()
+    T, E = dlogits.shape
+    H = x.shape[1]
+    lib = N.load()
+    ws = torch.empty(max(1, int(lib.usaf_hip_router_dw_ws_floats(T, E, H))), dtype=torch.float32, device=x.device)
+    dw = torch.empty(E, H, dtype=w_dtype, device=x.device)
+    N.call("usaf_hip_router_dw", dlogits.data_ptr(), x.data_ptr(), T, E, H, N.dtype_code(x.dtype), dw.data_ptr(),
+           ws.data_ptr(), N.stream_ptr(x.device))
+    return dw
+
+
+class RouterFn(torch.autograd.Function):
+    """The router of qwen3moe_dml.py:72-83 from one call (usaf_hip_router_fwd):
+    logits = F.linear(hs, W) in the activation dtype, fp32 softmax, top-k
+    threshold mask, optional renormalisation.  Backward: usaf_hip_route_topk_bwd to
+    dlogits, the library GEMM for dhs, usaf_hip_router_dw for dW."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, top_k: int, norm: bool, out_dtype: torch.dtype):
+        T, H = x.shape
+        E = w.shape[0]
+        logits = torch.empty(T, E, dtype=x.dtype, device=x.device)
+        weights = torch.empty(T, E, dtype=out_dtype, device=x.device)
+        probs = torch.empty(T, E, dtype=torch.float32, device=x.device)
+        N.call("usaf_hip_router_fwd", x.data_ptr(), w.data_ptr(), T, E, H, N.dtype_code(x.dtype), int(top_k),
+               1 if norm else 0, logits.data_ptr(), weights.data_ptr(), N.dtype_code(out_dtype), probs.data_ptr(),
+               N.stream_ptr(x.device))
+        ctx.top_k, ctx.norm = top_k, norm
+        ctx.save_for_backward(x, w, probs)
+        return weights
+
+    @staticmethod
+    def backward(ctx, dweights: torch.Tensor):
+        x, w, probs = ctx.saved_tensors
+        T, E = probs.shape
+        dweights = dweights.contiguous()
+        dlogits = torch.empty(T, E, dtype=x.dtype, device=x.device)
+        N.call("usaf_hip_route_topk_bwd", dweights.data_ptr(), N.dtype_code(dweights.dtype), probs.data_ptr(), T, E,
+               ctx.top_k, 1 if ctx.norm else 0, dlogits.data_ptr(), N.dtype_code(x.dtype), N.stream_ptr(x.device))
+        dx = torch.mm(dlogits, w) if ctx.needs_input_grad[0] else None
+        dw = _router_dw(x, dlogits, w.dtype) if ctx.needs_input_grad[1] else None
+        return dx, dw, None, None, None
+
+
+def _router_fused_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    return (x.dtype in (torch.float16, torch.bfloat16) and w.dtype == x.dtype and x.is_contiguous()
+            and w.is_contiguous() and w.shape[0] <= 1024 and x.shape[1] % 256 == 0 and x.data_ptr() % 16 == 0
+            and w.data_ptr() % 16 == 0)
 
 
 def _router_dw_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
@@ -553,11 +596,14 @@ def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_to
     slots past the routed pairs cost no GEMM work."""
     shape = hs.shape
     x = hs.reshape(-1, shape[-1])
-    if _router_dw_ok(x, router_weight):
-        logits = RouterLinearFn.apply(x, router_weight)
+    if _router_fused_ok(x, router_weight):
+        weights = RouterFn.apply(x, router_weight, top_k, norm_topk_prob, x.dtype)
     else:
-        logits = torch.nn.functional.linear(x, router_weight)
-    weights = RouteTopKFn.apply(logits, top_k, norm_topk_prob, x.dtype)
+        if _router_dw_ok(x, router_weight):
+            logits = RouterLinearFn.apply(x, router_weight)
+        else:
+            logits = torch.nn.functional.linear(x, router_weight)
+        weights = RouteTopKFn.apply(logits, top_k, norm_topk_prob, x.dtype)
     cap = None if overflow is None else x.shape[0] * min(top_k + 1, router_weight.shape[0])
     out = routed_experts(x, weights, experts, capture, slot_capacity=cap, overflow=overflow)
     return out.view(shape)
