@@ -239,10 +239,10 @@ int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offset
 
 /*
  * Per-expert blocked slot-major operands for the sampled gradient: expert e's
- * slots form a contiguous block of C rows of ld_e = round_up(S_e, 8) elements at
+ * slots form a contiguous block of C rows of ld_e = round_up(S_e, 16) elements at
  * element offset C * sum_{e' < e} ld_e', padding columns zero:
  *   out_blk[C * P[e] + c * ld_e + j] = in[rows ? rows[s0_e + j] : s0_e + j, c]   (j < S_e)
- * usaf_hip_blocked_elems bounds the element count (C * (S + 7 E)).  Needs C, ld_in
+ * usaf_hip_blocked_elems bounds the element count (C * (S + 15 E)).  Needs C, ld_in
  * % 8 == 0, 16-byte aligned bases, E <= 1024.  A layout of this build: the
  * operands of the dense per-expert weight grads qwen3moe_dml.py:44-47 reads.
  */

@@ -548,7 +548,7 @@ def test_gather_transpose_blocked_bit_exact(gpu_device, gathered):
     blk = G.slot_blocked(x.to(gpu_device), offsets, S, None if rows is None else rows.to(gpu_device))
     torch.cuda.synchronize()
     # layout table: padded-slot prefix, 64-slot chunk prefix, chunk -> expert map
-    lds = [(offs[e + 1] - offs[e] + 7) // 8 * 8 for e in range(E)]
+    lds = [(offs[e + 1] - offs[e] + 15) // 16 * 16 for e in range(E)]
     pre, cpre, owner = [0], [0], []
     for e in range(E):
         pre.append(pre[-1] + lds[e])
@@ -563,7 +563,7 @@ def test_gather_transpose_blocked_bit_exact(gpu_device, gathered):
     pos = 0
     for e in range(E):
         s0, s1 = offs[e], offs[e + 1]
-        ld = (s1 - s0 + 7) // 8 * 8
+        ld = (s1 - s0 + 15) // 16 * 16
         block = got[pos: pos + C * ld].reshape(C, ld)
         assert torch.equal(block[:, : s1 - s0], src[s0:s1].t().contiguous().view(torch.int16))
         assert torch.all(block[:, s1 - s0:] == 0)

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void sddmm_kernel(const uint16_t* __restrict__
 
 // ---- per-expert blocked slot-major operands -------------------------------------
 // Expert e's slots [s0_e, s0_e + S_e) form a contiguous block of C rows of
-// ld_e = round_up(S_e, 8) elements at element offset C * P[e], P[e] = sum of
+// ld_e = round_up(S_e, BLK_PAD) elements at element offset C * P[e], P[e] = sum of
 // ld_e' over e' < e; the padding columns [S_e, ld_e) are zero.  A weight
 // position's dot product then reads one contiguous, zero-padded run of its
 // expert, and one expert's operands are one contiguous region (TLB and L2
@@ -150,8 +150,13 @@ __global__ __launch_bounds__(256) void sddmm_kernel(const uint16_t* __restrict__
 constexpr int BLK_MAX_E = 1024;
 
 // Number of 64-slot chunks the blocked layout of S slots over E experts can
-// need: sum_e ceil(round_up(S_e, 8) / 64) <= (S + 7E) / 64 + E.
-__host__ __device__ inline int64_t blk_chunk_bound(int64_t S, int64_t E) { return (S + 8 * E) / 64 + E + 1; }
+// need: sum_e ceil(blk_ld(S_e) / 64) <= (S + (BLK_PAD - 1) E) / 64 + E.
+// Expert blocks are padded to BLK_PAD slots: a block row then starts on a 32-byte
+// boundary, so the transposes' 128-byte row segments cover whole 32-byte
+// sectors and no write of theirs is a partial-sector read-modify-write.
+constexpr int BLK_PAD = 16;
+__host__ __device__ inline int blk_ld(int se) { return (se + BLK_PAD - 1) & ~(BLK_PAD - 1); }
+__host__ __device__ inline int64_t blk_chunk_bound(int64_t S, int64_t E) { return (S + BLK_PAD * E) / 64 + E + 1; }
 
 // table[e] = P[e] (padded slots before expert e), table[E + 1 + e] = 64-slot
 // chunks before expert e (e <= E), table[2(E + 1) + k] = the expert that owns
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(256) void blocked_layout_kernel(const int32_t* __re
   for (int i = 0; i < per; ++i) {
     const int e = tid * per + i;
     if (e < E) {
-      const int ld = (offsets[e + 1] - offsets[e] + 7) & ~7;
+      const int ld = blk_ld(offsets[e + 1] - offsets[e]);
       sp += ld;
       sc += (ld + 63) >> 6;
     }
@@ -188,7 +193,7 @@ __global__ __launch_bounds__(256) void blocked_layout_kernel(const int32_t* __re
   for (int i = 0; i < per; ++i) {
     const int e = tid * per + i;
     if (e < E) {
-      const int ld = (offsets[e + 1] - offsets[e] + 7) & ~7;
+      const int ld = blk_ld(offsets[e + 1] - offsets[e]);
       const int nc = (ld + 63) >> 6;
       table[e] = rp;
       table[E + 1 + e] = rc;
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(256) void gather_transpose_blocked_kernel(const uin
   const int64_t chunk = blockIdx.x;
   const int e = table[2 * (E + 1) + chunk];
   if (e < 0) return;  // block-uniform
-  const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = (se + 7) & ~7;
+  const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = blk_ld(se);
   const int j0 = (int)(chunk - table[E + 1 + e]) * 64;  // first slot of the chunk within the expert
   const int64_t c0 = (int64_t)blockIdx.y * 64;
   {
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(256) void gather_transpose_blocked_kernel(const uin
 // expert (the layout table's chunk map) and a 512-feature range (blockIdx.y):
 //   dcur[s, h]   = dtype(fp32(dout[t_s, h]) * w_s)            row-major [S, H]
 //   dcurB        = the same values in the blocked slot-major layout (H rows per
-//                  expert block, zero padding up to round_up(S_e, 8))
+//                  expert block, zero padding up to round_up(S_e, BLK_PAD))
 //   part[y][s]   = sum over the range of fp32(dout[t_s, h]) * fp32(y[s, h])
 // combine_bwd_finish_kernel adds the ranges: dweights[t_s, e] = dtype(sum_y part).
 // Needs H % 8 == 0 and 16-byte aligned rows.
@@ -268,7 +273,7 @@ __global__ __launch_bounds__(256) void combine_bwd_blocked_kernel(
   const int64_t chunk = blockIdx.x;
   const int e = table[2 * (E + 1) + chunk];
   if (e < 0) return;  // block-uniform
-  const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = (se + 7) & ~7;
+  const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = blk_ld(se);
   const int j0 = (int)(chunk - table[E + 1 + e]) * 64;  // first slot of the chunk within the expert
   uint16_t* const blk = dcurB + H * (int64_t)table[e];
   const int64_t hbeg = (int64_t)blockIdx.y * 512;
@@ -604,7 +609,7 @@ extern "C" int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t
   return check_launch("sddmm_masked");
 }
 
-extern "C" int64_t usaf_hip_blocked_elems(int64_t S, int64_t E, int64_t C) { return C * (S + 7 * E); }
+extern "C" int64_t usaf_hip_blocked_elems(int64_t S, int64_t E, int64_t C) { return C * (S + (BLK_PAD - 1) * E); }
 
 extern "C" int64_t usaf_hip_blocked_table_elems(int64_t S, int64_t E) { return 2 * (E + 1) + blk_chunk_bound(S, E); }
 

@@ -418,7 +418,7 @@ def _dense_weight_grad(out: torch.Tensor, dy: torch.Tensor, x: torch.Tensor, x_r
 @dataclass
 class BlockedSlots:
     """Per-expert blocked slot-major operand (usaf_hip_gather_transpose_blocked):
-    expert e's slots form a contiguous block of `cols` rows of round_up(S_e, 8)
+    expert e's slots form a contiguous block of `cols` rows of round_up(S_e, 16)
     elements, zero-padded, at element offset cols * sum of the padded counts of
     the experts before e."""
     data: torch.Tensor       # flat, 16-bit
