@@ -574,6 +574,18 @@ struct TileWalk {
     mt = xcd + (int64_t)dies * (u / n_nt);
     nt = u % n_nt;
   }
+  // Snake order: pass p hands units [p * per_xcd, (p + 1) * per_xcd) to the
+  // die's blocks upward when p is even, downward when p is odd.  The unit list
+  // runs heavy tiles before light remainders, so the blocks left one tile short
+  // at the end of the heavy tiles are the first to take the light ones.
+  __device__ int64_t snake_unit(int64_t p) const {
+    return p * per_xcd + ((p & 1) ? per_xcd - 1 - local_b : local_b);
+  }
+  __device__ int snake_count() const {
+    const int64_t tot = end(), full = tot / per_xcd, rem = tot % per_xcd;
+    const int64_t pos = (full & 1) ? per_xcd - 1 - local_b : local_b;
+    return (int)(full + (pos < rem ? 1 : 0));
+  }
 };
 
 template <int BMODE, int EPI, int BQ, int DT>
@@ -1162,8 +1174,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
   const TileWalk walk(s_h[E] + s_l[E], n_nt);
   const int n_grp = (int)(g.N / 128);  // BT: 128-column groups of n
-  const int64_t first = walk.first(), stride = walk.step(), wend = walk.end();
-  const int n_my = first < wend ? (int)((wend - first + stride - 1) / stride) : 0;
+  const int n_my = walk.snake_count();
   if (n_my == 0) return;  // block-uniform
 
   // tile ordinal -> expert, first slot, rows, n-tile (the m-tile list of
@@ -1174,7 +1185,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   const bool rev = (walk.local_b & 1) != 0;
   auto decode = [&](int ord) {
     int64_t mt, nt;
-    walk.decode(first + (int64_t)(rev ? n_my - 1 - ord : ord) * stride, mt, nt);
+    walk.decode(walk.snake_unit(rev ? n_my - 1 - ord : ord), mt, nt);
     int e, j;
     if (mt < s_h[E]) {
       e = prefix_owner(s_h, E, mt);
