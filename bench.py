@@ -165,76 +165,139 @@ def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfl
                 prefix=prefix, T=T, H=H, I=I, E=E, n_act=n_act, active=active)
 
 
-def _fwd_bwd_check(L, flag, static_slots: bool) -> dict:
+def _fwd_bwd_check(L, finite, overflow, slot: int = 0) -> dict:
     """Forward + backward with grad capture, then the reference's finite check
-    (train.py:649-651) into flag[0]; static_slots buckets the experts into
-    T * (top_k + 1) slots without a host read, flag[1] = 1 if that overflowed."""
+    (train.py:649-651) into finite[0].  overflow None buckets the experts
+    exactly (one host read of the slot count); otherwise they go into
+    T * (top_k + 1) static slots without a host read and the int32 GPU flag
+    overflow[0] is set to 1 if that overflowed (it is never cleared here).
+    The compact gradients go to the buffers of `slot` (two slots, so that a
+    step's gradients survive the next step's check until its update reads them)."""
     from usaf_amd import _native as N
     from usaf_amd import moe as G
     store = L["store"]
     store.zero_()
     L["hs"].grad = None
     L["router_w"].grad = None
-    flag.fill_(1)       # finite
-    flag[1:].fill_(0)   # overflow
+    finite.fill_(1)
     out = G.moe_block(L["hs"], L["router_w"], L["k"], False, L["experts"], capture=(store, L["prefix"]),
-                      overflow=flag[1:] if static_slots else None)
-    _flush_adam(L)  # the previous step's SparseAdam, behind this forward's launches
+                      overflow=overflow)
     out.backward(L["dy"])
     dev = L["hs"].device
     cg = {}
     for name, v in store.compact.items():
-        o = L.setdefault(f"cg:{name}", torch.empty_like(v))
-        N.call("usaf_hip_scale_check", v.data_ptr(), o.data_ptr(), v.numel(), 1.0, flag.data_ptr(),
+        o = L.setdefault(f"cg{slot}:{name}", torch.empty_like(v))
+        N.call("usaf_hip_scale_check", v.data_ptr(), o.data_ptr(), v.numel(), 1.0, finite.data_ptr(),
                N.stream_ptr(dev))
         cg[name] = o
     return cg
 
 
-def _flush_adam(L) -> None:
-    cg = L.pop("pending_adam", None)
-    if cg is not None:
-        L["opt"].step(compact_grads=cg)
-
-
-def moe_train_step(L) -> bool:
-    """One step; returns whether the gradients were finite (step applied).
-    One host read per step (the finite flag, as the reference's loop); the
-    slot count stays on the GPU unless the routing overflowed T * (top_k + 1)
-    slots, in which case the step is recomputed with exact bucketing.
-
-    The router's SGD step is launched right after the flag read (the next
-    forward reads the router weight); the SparseAdam step is launched after the
-    next step's forward (_flush_adam), on the same stream, so it still runs
-    before that step's backward rewrites the gradient buffers it reads, and its
-    Python no longer delays the next forward while the GPU idles.  Results are
-    the same as launching it here; the caller flushes the last one."""
+def moe_train_step_sync(L) -> bool:
+    """One step in the reference loop's order (train.py:649-672): the host reads
+    the finite flag, then applies the router's SGD step and SparseAdam if it is
+    set.  The slot count stays on the GPU unless the routing overflowed
+    T * (top_k + 1) slots; the step is then recomputed with exact bucketing."""
     dev = L["hs"].device
-    flag = L.setdefault("flag", torch.ones(2, dtype=torch.int32, device=dev))
-    cg = _fwd_bwd_check(L, flag, static_slots=True)
+    flag = L.setdefault("flag_sync", torch.ones(2, dtype=torch.int32, device=dev))
+    flag[1:].fill_(0)
+    cg = _fwd_bwd_check(L, flag[:1], flag[1:])
     finite, overflow = flag.tolist()
-    L["overflows"] = L.get("overflows", 0) + overflow
     if overflow:
-        cg = _fwd_bwd_check(L, flag, static_slots=False)
+        L["recomputed"] = L.get("recomputed", 0) + 1
+        cg = _fwd_bwd_check(L, flag[:1], None)
         finite = flag.tolist()[0]
     if finite:
         L["sgd"].step()
-        L["pending_adam"] = cg
+        L["opt"].step(compact_grads=cg)
     return bool(finite)
+
+
+class LaggedSteps:
+    """The bench's training loop: step n + 1 is launched before the host reads
+    step n's finite flag, so the GPU never idles on that read.
+
+    Each step launches forward + backward + finite check into its own flag slot
+    (two slots, alternating), the router's SGD step gated on the device by that
+    flag and by a sticky halt flag (capacity-mode bucketing sets it on overflow),
+    and an async copy of both flags to pinned host memory.  After launching step
+    n + 1 the host reads step n's flags and, if the step was finite, launches its
+    SparseAdam update: on the same stream, behind step n + 1's work, which reads
+    neither the masters nor the moments it updates.
+    An overflow halts every gated update from that step on; the host recomputes
+    the step with exact bucketing, applies it and relaunches the step after it.
+    The updates applied, and their order, are those of moe_train_step_sync."""
+
+    def __init__(self, L):
+        dev = L["hs"].device
+        self.L = L
+        self.flags = [torch.ones(2, dtype=torch.int32, device=dev) for _ in range(2)]  # finite, halt snapshot
+        self.halt = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.host = [torch.zeros(2, dtype=torch.int32).pin_memory() for _ in range(2)]
+        self.events = [torch.cuda.Event() for _ in range(2)]
+        self.cg = [None, None]
+        self.pending = None
+        self.slot = 0
+        self.applied = self.skipped = self.recomputed = 0
+
+    def _launch(self, i: int) -> None:
+        f = self.flags[i]
+        self.cg[i] = _fwd_bwd_check(self.L, f[:1], self.halt, slot=i)
+        f[1:].copy_(self.halt)
+        self.host[i].copy_(f, non_blocking=True)
+        self.events[i].record()
+        self.L["sgd"].step(finite=f[:1], halt=self.halt)
+
+    def _resolve(self, j: int, relaunch=None) -> None:
+        self.events[j].synchronize()
+        finite, halted = self.host[j].tolist()
+        if halted:
+            # step j overflowed its static slots: no gated update ran since
+            torch.cuda.synchronize()
+            self.halt.zero_()
+            self.recomputed += 1
+            f = self.flags[j]
+            self.cg[j] = _fwd_bwd_check(self.L, f[:1], None, slot=j)
+            finite = f.tolist()[0]
+            if finite:
+                self.L["sgd"].step()
+            if relaunch is not None:
+                self._launch(relaunch)  # the step after j, on the updated router weight
+        if finite:
+            self.L["opt"].step(compact_grads=self.cg[j])
+            self.applied += 1
+        else:
+            self.skipped += 1
+
+    def step(self) -> None:
+        i = self.slot
+        self._launch(i)
+        if self.pending is not None:
+            self._resolve(self.pending, relaunch=i)
+        self.pending = i
+        self.slot ^= 1
+
+    def flush(self) -> None:
+        """Resolve the last launched step (its update is launched too)."""
+        if self.pending is not None:
+            self._resolve(self.pending)
+            self.pending = None
 
 
 def bench_moe_step(dev, steps: int, warmup: int) -> dict:
     L = build_moe(dev)
+    loop = LaggedSteps(L)
     for _ in range(warmup):
-        moe_train_step(L)
-    _flush_adam(L)
-    L["overflows"] = 0
+        loop.step()
+    loop.flush()
+    loop.applied = loop.skipped = loop.recomputed = 0
     with _Timer() as t:
         for _ in range(steps):
-            moe_train_step(L)
-        _flush_adam(L)
+            loop.step()
+        loop.flush()
     ms = t.ms / steps
-    _log(f"moe step: {L['overflows']} of {steps} timed steps overflowed the static slot capacity (recomputed)")
+    _log(f"moe step: {loop.applied} of {steps} timed steps applied, {loop.skipped} skipped (non-finite), "
+         f"{loop.recomputed} recomputed after overflowing the static slot capacity")
     fl = moe_step_flops(L["T"], L["H"], L["I"], L["E"], L["k"], L["n_act"]["gate_up_proj"],
                         L["n_act"]["down_proj"])
     kern = bench_moe_kernels(L, max(3, steps))

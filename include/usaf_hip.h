@@ -314,9 +314,14 @@ int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, float* v, i
 /* torch.optim.SGD.step with momentum (dampening 0, no Nesterov) for one tensor, the
  * router's optimizer in the reference trainer (train.py:493-498, 667-672):
  * d = grad + wd*p; buf = d on the first step, else buf*momentum + d; p -= lr*buf;
- * rounded to the tensor dtype after each torch op as the single-tensor path does. */
+ * rounded to the tensor dtype after each torch op as the single-tensor path does.
+ * Optional device gate (either pointer may be NULL): the step is skipped on the
+ * device when *finite == 0 or *halt != 0, so a training loop can launch it
+ * before it reads the step's finite flag on the host (train.py:649-672 decides
+ * on the host).  A gated call cannot be the first step (first_step != 0). */
 int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momentum_buf, int64_t n, int32_t dtype, double lr,
-                               double momentum, double weight_decay, int32_t first_step, void* stream);
+                               double momentum, double weight_decay, int32_t first_step, const int32_t* finite,
+                               const int32_t* halt, void* stream);
 
 /* out = in / denom (fp32) and *finite_flag = 0 if any result is inf/NaN (train.py:661-663);
  * the caller sets *finite_flag = 1 beforehand. */

@@ -723,6 +723,43 @@ def test_momentum_sgd_matches_torch(gpu_device, dtype):
             assert float((diff > 0).float().mean()) < 1e-3
 
 
+def test_momentum_sgd_device_gate(gpu_device):
+    _say("MomentumSGD gated on device flags: closed gates leave p and buf untouched, open = ungated step")
+    from usaf_amd.sparse_optim import MomentumSGD
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(78)
+    p0 = (torch.randn(64, 512, generator=g) * 0.05).to(dt).to(gpu_device)
+    grads = [torch.randn(64, 512, generator=g).to(dt).to(gpu_device) for _ in range(3)]
+    one = torch.ones(1, dtype=torch.int32, device=gpu_device)
+    zero = torch.zeros(1, dtype=torch.int32, device=gpu_device)
+    a = p0.clone().requires_grad_(True)
+    b = p0.clone().requires_grad_(True)
+    ours = MomentumSGD([a], lr=2e-4, momentum=0.9, weight_decay=0.005)
+    plain = MomentumSGD([b], lr=2e-4, momentum=0.9, weight_decay=0.005)
+    # first step of the buffer: the gate is read on the host; a closed one creates nothing
+    a.grad = grads[0].clone()
+    ours.step(finite=zero, halt=zero)
+    assert not ours._buf and torch.equal(a.detach(), p0)
+    ours.step(finite=one, halt=zero)
+    b.grad = grads[0].clone()
+    plain.step()
+    torch.cuda.synchronize()
+    assert torch.equal(a.detach(), b.detach()) and torch.equal(ours._buf[0], plain._buf[0])
+    for closed in ((zero, zero), (one, one), (zero, one)):
+        p_before, buf_before = a.detach().clone(), ours._buf[0].clone()
+        a.grad = grads[1].clone()
+        ours.step(finite=closed[0], halt=closed[1])
+        torch.cuda.synchronize()
+        assert torch.equal(a.detach(), p_before) and torch.equal(ours._buf[0], buf_before)
+    for gr in grads[1:]:
+        a.grad = gr.clone()
+        b.grad = gr.clone()
+        ours.step(finite=one, halt=zero)
+        plain.step()
+        torch.cuda.synchronize()
+        assert torch.equal(a.detach(), b.detach()) and torch.equal(ours._buf[0], plain._buf[0])
+
+
 @pytest.mark.parametrize("T,E,H,k,norm", [(4096, 128, 2048, 8, False), (333, 60, 768, 4, True), (5, 8, 256, 2, False),
                                           (77, 200, 512, 6, False)])
 def test_router_fwd_exact_logits(gpu_device, T, E, H, k, norm):

@@ -476,8 +476,13 @@ __global__ __launch_bounds__(256) void sparse_adam_kernel(float* __restrict__ p,
 template <int DT>
 __global__ __launch_bounds__(256) void sgd_momentum_kernel(void* __restrict__ p, const void* __restrict__ grad,
                                                            void* __restrict__ buf, int64_t n, float lr,
-                                                           float momentum, float wd, int first) {
+                                                           float momentum, float wd, int first,
+                                                           const int32_t* __restrict__ finite,
+                                                           const int32_t* __restrict__ halt) {
 #pragma clang fp contract(off)
+  // the step's gate, read on the device (no host read): skipped unless the
+  // finite flag is set and the halt flag is clear
+  if ((finite && *finite == 0) || (halt && *halt != 0)) return;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   // Each fp32 result is pinned (asm) before its conversion: otherwise the
   // compiler folds product-then-fp16 into v_fma_mix, which rounds once from the
@@ -724,8 +729,10 @@ extern "C" int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, 
 
 extern "C" int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momentum_buf, int64_t n, int32_t dtype,
                                           double lr, double momentum, double weight_decay, int32_t first_step,
-                                          void* stream) {
+                                          const int32_t* finite, const int32_t* halt, void* stream) {
   if (n < 0) return set_error(USAF_ERR_INVALID, "sgd_momentum_step: negative n");
+  if (first_step && (finite || halt))
+    return set_error(USAF_ERR_INVALID, "sgd_momentum_step: the first step (momentum buffer = d) cannot be gated");
   if (n == 0) return clear_error();
   if (!p || !grad || !momentum_buf) return set_error(USAF_ERR_INVALID, "sgd_momentum_step: null pointer");
   hipStream_t st = as_stream(stream);
@@ -733,13 +740,16 @@ extern "C" int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momen
   const int first = first_step ? 1 : 0;
   switch (dtype) {
     case USAF_F32:
-      sgd_momentum_kernel<USAF_F32><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first);
+      sgd_momentum_kernel<USAF_F32><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first,
+                                                                                  finite, halt);
       break;
     case USAF_F16:
-      sgd_momentum_kernel<USAF_F16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first);
+      sgd_momentum_kernel<USAF_F16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first,
+                                                                                  finite, halt);
       break;
     case USAF_BF16:
-      sgd_momentum_kernel<USAF_BF16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first);
+      sgd_momentum_kernel<USAF_BF16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first,
+                                                                                  finite, halt);
       break;
     default:
       return set_error(USAF_ERR_INVALID, "sgd_momentum_step: dtype must be fp32, fp16 or bf16");

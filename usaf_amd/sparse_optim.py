@@ -191,20 +191,35 @@ class MomentumSGD:
                 p.grad.zero_()
 
     @torch.no_grad()
-    def step(self) -> None:
+    def step(self, finite: torch.Tensor | None = None, halt: torch.Tensor | None = None) -> None:
+        """One step.  ``finite`` / ``halt``: optional int32 GPU flags read by the
+        kernel, which skips the update unless finite[0] != 0 and halt[0] == 0 --
+        the trainer's finite gate (train.py:649-672) decided on the device, so
+        the step can be launched before the host has read the flag.  A tensor's
+        first step (which creates its momentum buffer, as torch does) reads the
+        gate on the host instead."""
+        for t, what in ((finite, "finite"), (halt, "halt")):
+            if t is not None and (not t.is_cuda or t.dtype != torch.int32 or t.numel() < 1):
+                raise TypeError(f"MomentumSGD: {what} must be an int32 GPU tensor")
         for i, p in enumerate(self.params):
             g = p.grad
             if g is None:
                 continue
             if not p.is_cuda or not p.is_contiguous() or not g.is_contiguous() or g.dtype != p.dtype:
                 raise RuntimeError("MomentumSGD: parameters and gradients must be contiguous GPU tensors of one dtype")
-            buf = self._buf.get(i)
-            first = buf is None
-            if first:
-                buf = torch.empty_like(p)
-                self._buf[i] = buf
             if self.momentum == 0.0:
                 raise NotImplementedError("MomentumSGD: momentum 0 (plain SGD) is not on the fused path")
+            buf = self._buf.get(i)
+            first = buf is None
+            gate_f = gate_h = None
+            if first:
+                if (finite is not None and int(finite[0]) == 0) or (halt is not None and int(halt[0]) != 0):
+                    continue
+                buf = torch.empty_like(p)
+                self._buf[i] = buf
+            else:
+                gate_f = finite.data_ptr() if finite is not None else None
+                gate_h = halt.data_ptr() if halt is not None else None
             N.call("usaf_hip_sgd_momentum_step", p.data_ptr(), g.data_ptr(), buf.data_ptr(), p.numel(),
                    N.dtype_code(p.dtype), self.lr, self.momentum, self.weight_decay, 1 if first else 0,
-                   N.stream_ptr(p.device))
+                   gate_f, gate_h, N.stream_ptr(p.device))
