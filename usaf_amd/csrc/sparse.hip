@@ -390,19 +390,35 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
   // in registers while the row does not change, halving the loads per position.
   constexpr int RUN = 8;
   const int64_t gi = (int64_t)(blockIdx.x / dies) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  // A run's position data is fetched once: lane j of the group loads position
+  // base + j's row code, column and compact slot (and the old compact value),
+  // the group takes them from lane j by shuffles, and lane j stores position
+  // j's sum at the end -- a handful of memory instructions per run instead of
+  // five per position, which the address units were spending most of their time on.
   for (int64_t base = lo + gi * RUN; base < hi; base += n_grp * RUN) {
-    const int64_t end = base + RUN < hi ? base + RUN : hi;
+    const int nrun = (int)(base + RUN < hi ? RUN : hi - base);  // uniform across the group
+    uint32_t my_code = 0xFFFFFFFFu, my_i = 0;
+    int64_t my_pos = 0;
+    float my_old = 0.f, my_sum = 0.f;
+    bool my_ok = false;
+    if (gl < nrun) {
+      my_code = (uint32_t)rcode[base + gl];
+      my_i = (uint32_t)col_idx[base + gl];
+      my_ok = (my_code >> 21) < (uint32_t)E && (my_code & 0x1FFFFFu) < (uint32_t)R && my_i < (uint32_t)C;
+      if (my_ok) {
+        my_pos = pos_map ? pos_map[base + gl] : base + gl;
+        my_old = compact[my_pos];
+      }
+    }
     uint32_t cached = 0xFFFFFFFFu;
     int ld = 0;
     const uint16_t* rv = rowB;
     uint4 r0 = make_uint4(0, 0, 0, 0), r1 = make_uint4(0, 0, 0, 0);
-    for (int64_t p = base; p < end; ++p) {
-      const uint32_t code = (uint32_t)rcode[p];
-      const uint32_t i = (uint32_t)col_idx[p];
+    for (int j = 0; j < nrun; ++j) {
+      const uint32_t code = (uint32_t)__shfl((int)my_code, j, 16);
+      const uint32_t i = (uint32_t)__shfl((int)my_i, j, 16);
       const uint32_t e = code >> 21, o = code & 0x1FFFFFu;
-      if (e >= (uint32_t)E || o >= (uint32_t)R || i >= (uint32_t)C) continue;
-      const int64_t pos = pos_map ? pos_map[p] : p;
-      const float old = gl == 0 ? compact[pos] : 0.f;
+      if (e >= (uint32_t)E || o >= (uint32_t)R || i >= (uint32_t)C) continue;  // uniform across the group
       const int pe = s_pre[e];
       if (code != cached) {  // uniform across the group
         cached = code;
@@ -437,8 +453,9 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
       }
 #pragma unroll
       for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
-      if (gl == 0) compact[pos] = old + round_to<DT>(acc);
+      if (gl == j) my_sum = round_to<DT>(acc);
     }
+    if (my_ok) compact[my_pos] = my_old + my_sum;
   }
 }
 
