@@ -155,6 +155,7 @@ constexpr int BLK_MAX_E = 1024;
 // boundary, so the transposes' 128-byte row segments cover whole 32-byte
 // sectors and no write of theirs is a partial-sector read-modify-write.
 constexpr int BLK_PAD = 16;
+constexpr int GT_TILES = 4;  // 64-column tiles per block of the blocked gather-transpose
 __host__ __device__ inline int blk_ld(int se) { return (se + BLK_PAD - 1) & ~(BLK_PAD - 1); }
 __host__ __device__ inline int64_t blk_chunk_bound(int64_t S, int64_t E) { return (S + BLK_PAD * E) / 64 + E + 1; }
 
@@ -218,39 +219,47 @@ __global__ __launch_bounds__(256) void gather_transpose_blocked_kernel(const uin
                                                                        const int32_t* __restrict__ offsets,
                                                                        const int32_t* __restrict__ table, int E,
                                                                        int64_t C, uint16_t* __restrict__ out) {
-  __shared__ __align__(16) uint32_t tile32[TT_DWORDS];
+  // A block covers one 64-slot chunk and GT_TILES 64-column tiles: the chunk
+  // lookup and the row indices are read once, and all the tiles' loads are in
+  // flight before the first store.
+  __shared__ __align__(16) uint32_t tile32[GT_TILES][TT_DWORDS];
   const int64_t chunk = blockIdx.x;
   const int e = table[2 * (E + 1) + chunk];
   if (e < 0) return;  // block-uniform
   const int s0 = offsets[e], se = offsets[e + 1] - s0, ld = blk_ld(se);
   const int j0 = (int)(chunk - table[E + 1 + e]) * 64;  // first slot of the chunk within the expert
-  const int64_t c0 = (int64_t)blockIdx.y * 64;
+  const int64_t c0 = (int64_t)blockIdx.y * 64 * GT_TILES;
   {
     const int sp = threadIdx.x >> 3, cg = threadIdx.x & 7;
     const int ja = j0 + 2 * sp;
-    const int64_t c = c0 + 8 * cg;
-    uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-    if (c < C) {
-      if (ja < se) {
-        const int64_t row = rows ? (int64_t)rows[s0 + ja] : (int64_t)(s0 + ja);
-        a = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
-      }
-      if (ja + 1 < se) {
-        const int64_t row = rows ? (int64_t)rows[s0 + ja + 1] : (int64_t)(s0 + ja + 1);
-        b = *reinterpret_cast<const uint4*>(in + row * ld_in + c);
+    const int64_t ra = ja < se ? (rows ? (int64_t)rows[s0 + ja] : (int64_t)(s0 + ja)) : -1;
+    const int64_t rb = ja + 1 < se ? (rows ? (int64_t)rows[s0 + ja + 1] : (int64_t)(s0 + ja + 1)) : -1;
+    uint4 a[GT_TILES], b[GT_TILES];
+#pragma unroll
+    for (int t = 0; t < GT_TILES; ++t) {
+      const int64_t c = c0 + 64 * t + 8 * cg;
+      a[t] = make_uint4(0, 0, 0, 0);
+      b[t] = make_uint4(0, 0, 0, 0);
+      if (c < C) {
+        if (ra >= 0) a[t] = *reinterpret_cast<const uint4*>(in + ra * ld_in + c);
+        if (rb >= 0) b[t] = *reinterpret_cast<const uint4*>(in + rb * ld_in + c);
       }
     }
-    tt_write(tile32, sp, cg, a, b);
+#pragma unroll
+    for (int t = 0; t < GT_TILES; ++t) tt_write(tile32[t], sp, cg, a[t], b[t]);
   }
   __syncthreads();
   uint16_t* const blk = out + C * (int64_t)table[e];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int v = threadIdx.x + 256 * it;
-    const int cl = v >> 3, sg = v & 7;
-    const int64_t c = c0 + cl;
-    const int j = j0 + 8 * sg;
-    if (c < C && j < ld) *reinterpret_cast<uint4*>(blk + c * ld + j) = tt_read(tile32, cl, sg);
+  for (int t = 0; t < GT_TILES; ++t) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int v = threadIdx.x + 256 * it;
+      const int cl = v >> 3, sg = v & 7;
+      const int64_t c = c0 + 64 * t + cl;
+      const int j = j0 + 8 * sg;
+      if (c < C && j < ld) *reinterpret_cast<uint4*>(blk + c * ld + j) = tt_read(tile32[t], cl, sg);
+    }
   }
 }
 
@@ -652,7 +661,7 @@ extern "C" int usaf_hip_gather_transpose_blocked(const void* in, int64_t ld_in, 
   if (!in || !out || !offsets || !table) return set_error(USAF_ERR_INVALID, "gather_transpose_blocked: null pointer");
   if (C % 8 != 0 || ld_in % 8 != 0 || ((uintptr_t)in & 15) || ((uintptr_t)out & 15))
     return set_error(USAF_ERR_UNSUPPORTED, "gather_transpose_blocked: needs C, ld_in %% 8 == 0 and 16-byte aligned bases");
-  const int64_t gx = blk_chunk_bound(S, E), gy = (C + 63) / 64;
+  const int64_t gx = blk_chunk_bound(S, E), gy = (C + 64 * GT_TILES - 1) / (64 * GT_TILES);
   if (gx > 0x7fffffff || gy > 65535) return set_error(USAF_ERR_INVALID, "gather_transpose_blocked: too large");
   gather_transpose_blocked_kernel<<<dim3((unsigned)gx, (unsigned)gy), 256, 0, as_stream(stream)>>>(
       (const uint16_t*)in, ld_in, rows, offsets, table, (int)E, C, (uint16_t*)out);
