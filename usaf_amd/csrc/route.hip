@@ -581,8 +581,14 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
 #pragma clang fp contract(off)
   __shared__ float s_part[4][32 * 33];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t t0 = (int64_t)blockIdx.x * 32;
-  const int e0 = (int)blockIdx.y * 32;
+  // Blocks go round-robin over the 8 dies (block b on die b % 8).  The
+  // expert tiles of one token tile get blocks b, b + 8, b + 16, ... of one die,
+  // dispatched together, so that die's L2 serves the token rows to all of them.
+  const int n_et = (E + 31) / 32;
+  const int64_t r = (int64_t)blockIdx.x / 8;
+  const int64_t t0 = ((r / n_et) * 8 + (int64_t)(blockIdx.x % 8)) * 32;
+  const int e0 = (int)(r % n_et) * 32;
+  if (t0 >= T) return;  // block-uniform: the last token tiles of the padded grid
   // rows past T or E read row 0: their results are never stored, and the loads
   // stay unpredicated (a conditional load joins its branch with a wait)
   const int64_t ta = t0 + (lane & 31) < T ? t0 + (lane & 31) : 0;
@@ -817,9 +823,10 @@ extern "C" int usaf_hip_router_fwd(const void* x, const void* w, int64_t T, int6
   if (!x || !w || !logits || !weights) return set_error(USAF_ERR_INVALID, "router_fwd: null pointer");
   if (H % 256 != 0 || (((uintptr_t)x | (uintptr_t)w) & 15))
     return set_error(USAF_ERR_UNSUPPORTED, "router_fwd: needs H %% 256 == 0 and 16-byte aligned operands");
-  if ((T + 31) / 32 > 0x7fffffff) return set_error(USAF_ERR_INVALID, "router_fwd: too many tokens");
+  if (((T + 31) / 32 + 7) / 8 * 8 * ((E + 31) / 32) > 0x7fffffff)
+    return set_error(USAF_ERR_INVALID, "router_fwd: too many tokens");
   hipStream_t st = as_stream(stream);
-  const dim3 grid((unsigned)((T + 31) / 32), (unsigned)((E + 31) / 32));
+  const dim3 grid((unsigned)(((T + 31) / 32 + 7) / 8 * 8 * ((E + 31) / 32)));
   if (dtype == USAF_BF16)
     router_logits_kernel<USAF_BF16><<<grid, 256, 0, st>>>((const uint16_t*)x, (const uint16_t*)w, T, (int)E, H,
                                                           (uint16_t*)logits);
