@@ -574,16 +574,26 @@ struct TileWalk {
     mt = xcd + (int64_t)dies * (u / n_nt);
     nt = u % n_nt;
   }
-  // Snake order: pass p hands units [p * per_xcd, (p + 1) * per_xcd) to the
-  // die's blocks upward when p is even, downward when p is odd.  The unit list
-  // runs heavy tiles before light remainders, so the blocks left one tile short
-  // at the end of the heavy tiles are the first to take the light ones.
+  // Pass p hands units [p * per_xcd, (p + 1) * per_xcd) to the die's blocks,
+  // upward (block b takes position b), as a plain round-robin does.  When the
+  // heavy units do not fill whole passes, the passes after the one holding the
+  // last heavy unit alternate downward and upward: the unit list runs heavy
+  // tiles before light remainders, so the blocks left one heavy tile short
+  // take the light ones first, and a second round of light units starts again
+  // from them instead of from the blocks that ran the extra heavy tile.
+  int64_t pass_turn = INT64_MAX;  // first pass that runs downward (set by set_heavy)
+  __device__ void set_heavy(int64_t n_heavy_mt) {
+    const int64_t hd = n_heavy_mt > xcd ? (n_heavy_mt - xcd + dies - 1) / dies : 0;
+    const int64_t uh = hd * n_nt;
+    pass_turn = uh % per_xcd == 0 ? INT64_MAX : uh / per_xcd + 1;
+  }
+  __device__ bool down(int64_t p) const { return p >= pass_turn && ((p - pass_turn) & 1) == 0; }
   __device__ int64_t snake_unit(int64_t p) const {
-    return p * per_xcd + ((p & 1) ? per_xcd - 1 - local_b : local_b);
+    return p * per_xcd + (down(p) ? per_xcd - 1 - local_b : local_b);
   }
   __device__ int snake_count() const {
     const int64_t tot = end(), full = tot / per_xcd, rem = tot % per_xcd;
-    const int64_t pos = (full & 1) ? per_xcd - 1 - local_b : local_b;
+    const int64_t pos = down(full) ? per_xcd - 1 - local_b : local_b;
     return (int)(full + (pos < rem ? 1 : 0));
   }
 };
@@ -1172,7 +1182,8 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     lds_barrier();
   }
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
-  const TileWalk walk(s_h[E] + s_l[E], n_nt);
+  TileWalk walk(s_h[E] + s_l[E], n_nt);
+  walk.set_heavy(s_h[E]);
   const int n_grp = (int)(g.N / 128);  // BT: 128-column groups of n
   const int n_my = walk.snake_count();
   if (n_my == 0) return;  // block-uniform
