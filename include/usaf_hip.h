@@ -261,11 +261,13 @@ int usaf_hip_gather_transpose_blocked(const void* in, int64_t ld_in, const int32
  * usaf_hip_sddmm_masked on blocked operands (row_blk: R rows per expert block,
  * col_blk: C rows per expert block, both from usaf_hip_gather_transpose_blocked
  * with the same layout table).  Replaces the same reference steps (qwen3moe_dml.py:44-56,
- * moe_loader.py:564-578).
+ * moe_loader.py:564-578).  accumulate = 0 writes 0 + sum instead of compact + sum
+ * (the first add into a zeroed buffer, without the zeroing pass); every position
+ * of the list is written.
  */
 int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, const int32_t* table, int64_t E, int64_t R,
                            int64_t C, int64_t n_pos, const int32_t* row_code, const int32_t* col_idx,
-                           const int64_t* pos_map, int32_t dtype, float* compact, void* stream);
+                           const int64_t* pos_map, int32_t dtype, float* compact, int32_t accumulate, void* stream);
 
 /* Backward of the weighted combine (as usaf_hip_moe_combine_bwd) that also writes
  * dcur in the blocked slot-major layout of `table` (usaf_hip_blocked_layout of the

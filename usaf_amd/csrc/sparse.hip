@@ -156,6 +156,7 @@ constexpr int BLK_MAX_E = 1024;
 // sectors and no write of theirs is a partial-sector read-modify-write.
 constexpr int BLK_PAD = 16;
 constexpr int GT_TILES = 4;  // 64-column tiles per block of the blocked gather-transpose
+constexpr int CB_STEPS = 4;  // 64-feature steps per load batch of the blocked combine backward
 __host__ __device__ inline int blk_ld(int se) { return (se + BLK_PAD - 1) & ~(BLK_PAD - 1); }
 __host__ __device__ inline int64_t blk_chunk_bound(int64_t S, int64_t E) { return (S + BLK_PAD * E) / 64 + E + 1; }
 
@@ -278,7 +279,10 @@ __global__ __launch_bounds__(256) void combine_bwd_blocked_kernel(
     const float* __restrict__ slot_w, const int32_t* __restrict__ offsets, const int32_t* __restrict__ table, int E,
     int64_t H, int64_t S_cap, uint16_t* __restrict__ dcur, uint16_t* __restrict__ dcurB, float* __restrict__ part) {
 #pragma clang fp contract(off)
-  __shared__ __align__(16) uint32_t tile32[TT_DWORDS];
+  // the 512 features go in batches of CB_STEPS 64-feature steps: every load of
+  // a batch is issued before its first product, and one barrier pair serves
+  // the batch's transposed stores
+  __shared__ __align__(16) uint32_t tile32[CB_STEPS][TT_DWORDS];
   const int64_t chunk = blockIdx.x;
   const int e = table[2 * (E + 1) + chunk];
   if (e < 0) return;  // block-uniform
@@ -302,43 +306,62 @@ __global__ __launch_bounds__(256) void combine_bwd_blocked_kernel(
     wv[u] = ok[u] ? slot_w[s0 + j] : 0.f;
     acc[u] = 0.f;
   }
-  for (int64_t c0 = hbeg; c0 < hend; c0 += 64) {
-    const int64_t c = c0 + 8 * cg;
-    uint4 d[2];
+  for (int64_t cb0 = hbeg; cb0 < hend; cb0 += 64 * CB_STEPS) {
+    uint4 gq[CB_STEPS][2], yq[CB_STEPS][2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      d[u] = make_uint4(0, 0, 0, 0);
-      if (ok[u] && c < hend) {
-        const uint4 gq = *reinterpret_cast<const uint4*>(dout + trow[u] * H + c);
-        const uint4 yq = *reinterpret_cast<const uint4*>(y + srow[u] * H + c);
-        const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w}, yw[4] = {yq.x, yq.y, yq.z, yq.w};
-        uint32_t dw[4];
+    for (int st = 0; st < CB_STEPS; ++st) {
+      const int64_t c = cb0 + 64 * st + 8 * cg;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint16_t g2[2] = {(uint16_t)gw[q], (uint16_t)(gw[q] >> 16)};
-          const uint16_t y2[2] = {(uint16_t)yw[q], (uint16_t)(yw[q] >> 16)};
-          uint16_t d2[2];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float g = load_as_f32<DT>(g2, h);
-            store_from_f32<DT>(d2, h, g * wv[u]);
-            acc[u] += g * load_as_f32<DT>(y2, h);
-          }
-          dw[q] = d2[0] | ((uint32_t)d2[1] << 16);
+      for (int u = 0; u < 2; ++u) {
+        gq[st][u] = make_uint4(0, 0, 0, 0);
+        yq[st][u] = make_uint4(0, 0, 0, 0);
+        if (ok[u] && c < hend) {
+          gq[st][u] = *reinterpret_cast<const uint4*>(dout + trow[u] * H + c);
+          yq[st][u] = *reinterpret_cast<const uint4*>(y + srow[u] * H + c);
         }
-        d[u] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
-        *reinterpret_cast<uint4*>(dcur + srow[u] * H + c) = d[u];
       }
     }
-    tt_write(tile32, sp, cg, d[0], d[1]);
+#pragma unroll
+    for (int st = 0; st < CB_STEPS; ++st) {
+      const int64_t c = cb0 + 64 * st + 8 * cg;
+      uint4 d[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        d[u] = make_uint4(0, 0, 0, 0);
+        if (ok[u] && c < hend) {
+          const uint32_t gw[4] = {gq[st][u].x, gq[st][u].y, gq[st][u].z, gq[st][u].w};
+          const uint32_t yw[4] = {yq[st][u].x, yq[st][u].y, yq[st][u].z, yq[st][u].w};
+          uint32_t dw[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint16_t g2[2] = {(uint16_t)gw[q], (uint16_t)(gw[q] >> 16)};
+            const uint16_t y2[2] = {(uint16_t)yw[q], (uint16_t)(yw[q] >> 16)};
+            uint16_t d2[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float g = load_as_f32<DT>(g2, h);
+              store_from_f32<DT>(d2, h, g * wv[u]);
+              acc[u] += g * load_as_f32<DT>(y2, h);
+            }
+            dw[q] = d2[0] | ((uint32_t)d2[1] << 16);
+          }
+          d[u] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+          *reinterpret_cast<uint4*>(dcur + srow[u] * H + c) = d[u];
+        }
+      }
+      tt_write(tile32[st], sp, cg, d[0], d[1]);
+    }
     __syncthreads();
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int v = tid + 256 * it;
-      const int cl = v >> 3, sg = v & 7;
-      const int64_t cc = c0 + cl;
-      const int j = j0 + 8 * sg;
-      if (cc < hend && j < ld) *reinterpret_cast<uint4*>(blk + cc * ld + j) = tt_read(tile32, cl, sg);
+    for (int st = 0; st < CB_STEPS; ++st) {
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int v = tid + 256 * it;
+        const int cl = v >> 3, sg = v & 7;
+        const int64_t cc = cb0 + 64 * st + cl;
+        const int j = j0 + 8 * sg;
+        if (cc < hend && j < ld) *reinterpret_cast<uint4*>(blk + cc * ld + j) = tt_read(tile32[st], cl, sg);
+      }
     }
     __syncthreads();
   }
@@ -381,7 +404,7 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
                                                             const int32_t* __restrict__ rcode,
                                                             const int32_t* __restrict__ col_idx,
                                                             const int64_t* __restrict__ pos_map,
-                                                            float* __restrict__ compact) {
+                                                            float* __restrict__ compact, int accumulate) {
   __shared__ int32_t s_pre[BLK_MAX_E + 1];
   for (int e = threadIdx.x; e <= E; e += blockDim.x) s_pre[e] = table[e];
   __syncthreads();
@@ -414,10 +437,8 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
       my_code = (uint32_t)rcode[base + gl];
       my_i = (uint32_t)col_idx[base + gl];
       my_ok = (my_code >> 21) < (uint32_t)E && (my_code & 0x1FFFFFu) < (uint32_t)R && my_i < (uint32_t)C;
-      if (my_ok) {
-        my_pos = pos_map ? pos_map[base + gl] : base + gl;
-        my_old = compact[my_pos];
-      }
+      my_pos = pos_map ? pos_map[base + gl] : base + gl;
+      if (my_ok && accumulate) my_old = compact[my_pos];  // else 0 + sum: a zeroed buffer's first add
     }
     uint32_t cached = 0xFFFFFFFFu;
     int ld = 0;
@@ -464,7 +485,8 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
       for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
       if (gl == j) my_sum = round_to<DT>(acc);
     }
-    if (my_ok) compact[my_pos] = my_old + my_sum;
+    // positions with an invalid row code or column: left alone when accumulating, 0 otherwise
+    if (gl < nrun && (my_ok || !accumulate)) compact[my_pos] = my_old + my_sum;
   }
 }
 
@@ -711,7 +733,7 @@ extern "C" int usaf_hip_moe_combine_bwd_blocked(const void* dout, const void* y_
 extern "C" int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, const int32_t* table, int64_t E,
                                       int64_t R, int64_t C, int64_t n_pos, const int32_t* row_code,
                                       const int32_t* col_idx, const int64_t* pos_map, int32_t dtype, float* compact,
-                                      void* stream) {
+                                      int32_t accumulate, void* stream) {
   if (E <= 0 || R <= 0 || C <= 0 || n_pos < 0) return set_error(USAF_ERR_INVALID, "sddmm_blocked: bad sizes");
   if (E > BLK_MAX_E || R >= (1 << 21) || C > 0x7fffffff)
     return set_error(USAF_ERR_INVALID, "sddmm_blocked: needs E <= %d, R < 2^21, C < 2^31", BLK_MAX_E);
@@ -730,11 +752,13 @@ extern "C" int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, 
   if (dtype == USAF_BF16)
     sddmm_blocked_kernel<USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)row_blk, (const uint16_t*)col_blk,
                                                                       table, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
-                                                                      row_code, col_idx, pos_map, compact);
+                                                                      row_code, col_idx, pos_map, compact,
+                                                                      accumulate ? 1 : 0);
   else
     sddmm_blocked_kernel<USAF_F16><<<(unsigned)blocks, 256, 0, st>>>((const uint16_t*)row_blk, (const uint16_t*)col_blk,
                                                                      table, (int32_t)E, (int32_t)R, (int32_t)C, n_pos,
-                                                                     row_code, col_idx, pos_map, compact);
+                                                                     row_code, col_idx, pos_map, compact,
+                                                                     accumulate ? 1 : 0);
   return check_launch("sddmm_blocked");
 }
 

@@ -331,13 +331,14 @@ class SparseGradStore:
     def __init__(self, active_idx: Dict[str, torch.Tensor], shapes: Dict[str, Any], device=None) -> None:
         dev = torch.device(device) if device is not None else N.default_device()
         self.device = dev
-        self.compact: Dict[str, torch.Tensor] = {}
+        self._compact: Dict[str, torch.Tensor] = {}
+        self._zero_pending: set = set()
         self._csr: Dict[str, tuple] = {}
         self._maps: Dict[str, Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = {}
         for name, idx in active_idx.items():
             idx = idx.reshape(-1).to(device=dev, dtype=torch.long)
             shape = [int(s) for s in shapes[name]]
-            self.compact[name] = torch.zeros(idx.numel(), dtype=torch.float32, device=dev)
+            self._compact[name] = torch.zeros(idx.numel(), dtype=torch.float32, device=dev)
             if len(shape) < 2:
                 raise ValueError(f"{name}: expert tensors are [E, rows, ...], got shape {shape}")
             E, R = shape[0], shape[1]
@@ -362,9 +363,23 @@ class SparseGradStore:
             row_code = ((e_of << 21) | (rows - e_of * R)).to(torch.int32).contiguous()  # e << 21 | o
             self._csr[name] = (row_ptr, row_code, cols.contiguous(), None if identity else order.contiguous(), E, R, C)
 
+    @property
+    def compact(self) -> Dict[str, torch.Tensor]:
+        """name -> compact fp32 gradient (moe_loader.py:541-562)."""
+        for name in list(self._zero_pending):
+            self._materialize(name)
+        return self._compact
+
+    def _materialize(self, name: str) -> None:
+        if name in self._zero_pending:
+            self._zero_pending.discard(name)
+            self._compact[name].zero_()
+
     def zero_(self) -> None:
-        for v in self.compact.values():
-            v.zero_()
+        """Zero every compact gradient.  The zeroing is deferred: the first
+        sampled add into a tensor writes 0 + sum instead of accumulating, so a
+        step that fills the store from the fused backward launches no fill."""
+        self._zero_pending = set(self._compact)
 
     def add_sampled(self, full_name: str, rowT: torch.Tensor, colT: torch.Tensor, offsets: torch.Tensor,
                     dtype: torch.dtype) -> None:
@@ -382,9 +397,11 @@ class SparseGradStore:
                                  f"the weight rows {R} x cols {C}")
             if rowT.offsets.data_ptr() != offsets.data_ptr() or colT.offsets.data_ptr() != offsets.data_ptr():
                 raise ValueError(f"{full_name}: blocked operands were built with other expert offsets")
+            first = full_name in self._zero_pending
             N.call("usaf_hip_sddmm_blocked", rowT.data.data_ptr(), colT.data.data_ptr(), rowT.table.data_ptr(), E, R, C,
                    cols.numel(), row_code.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
-                   self.compact[full_name].data_ptr(), N.stream_ptr(self.device))
+                   self._compact[full_name].data_ptr(), 0 if first else 1, N.stream_ptr(self.device))
+            self._zero_pending.discard(full_name)
             return
         if rowT.shape[0] != R or colT.shape[0] != C or rowT.shape[1] != colT.shape[1]:
             raise ValueError(f"{full_name}: operands {tuple(rowT.shape)} / {tuple(colT.shape)} do not match "
@@ -393,9 +410,10 @@ class SparseGradStore:
         if rowT.stride(1) != 1 or colT.stride(1) != 1 or colT.stride(0) != ldT or ldT % 8:
             raise ValueError("slot-major operands need unit column stride and one row stride, a multiple of 8 "
                              "(use usaf_amd.moe.slot_major)")
+        self._materialize(full_name)
         N.call("usaf_hip_sddmm_masked", rowT.data_ptr(), colT.data_ptr(), ldT, offsets.data_ptr(), E, R, C,
                cols.numel(), row_code.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
-               self.compact[full_name].data_ptr(), N.stream_ptr(self.device))
+               self._compact[full_name].data_ptr(), N.stream_ptr(self.device))
 
     def add(self, full_name: str, ei: int, g: torch.Tensor) -> None:
         """Reference protocol (moe_loader.py:564-578): dense grad of expert ei."""
@@ -411,10 +429,11 @@ class SparseGradStore:
         local = (rows - ei * R) * C + cols[p0:p1].long()
         pos = pos_map[p0:p1] if pos_map is not None else torch.arange(p0, p1, device=row_ptr.device)
         vals = g.detach().to(self.device).reshape(-1).gather(0, local).float()
-        self.compact[full_name].index_add_(0, pos, vals)
+        self._materialize(full_name)
+        self._compact[full_name].index_add_(0, pos, vals)
 
     def n_captured(self) -> int:
-        return len(self.compact)
+        return len(self._compact)
 
 
 class TopKImportanceStore:
