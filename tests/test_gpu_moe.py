@@ -662,6 +662,41 @@ def test_sddmm_blocked_ragged_experts(gpu_device, dtype):
     assert torch.equal(got[e0], init.double()[e0])
 
 
+def test_store_deferred_zero(gpu_device):
+    _say("SparseGradStore.zero_ deferred to the first sampled add: same values as zero-then-accumulate")
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(13)
+    counts = [5, 0, 300, 64]
+    E, R, C = len(counts), 24, 32
+    offs = [0]
+    for c in counts:
+        offs.append(offs[-1] + c)
+    S = offs[-1]
+    numel = E * R * C
+    act = torch.randperm(numel, generator=g)[: numel // 4]
+    offsets = torch.tensor(offs, dtype=torch.int32, device=gpu_device)
+    tb = G.blocked_layout(offsets, S)
+    ops = []
+    for _ in range(2):
+        rb = G.slot_blocked(torch.randn(S, R, generator=g).to(dtype).to(gpu_device), offsets, S, table=tb)
+        cb = G.slot_blocked(torch.randn(S, C, generator=g).to(dtype).to(gpu_device), offsets, S, table=tb)
+        ops.append((rb, cb))
+    fresh = SparseGradStore({"L.w": act}, {"L.w": (E, R, C)}, device=gpu_device)  # zeros, accumulating adds
+    for rb, cb in ops:
+        fresh.add_sampled("L.w", rb, cb, offsets, dtype)
+    lazy = SparseGradStore({"L.w": act}, {"L.w": (E, R, C)}, device=gpu_device)
+    lazy.compact["L.w"].fill_(123.0)
+    lazy.zero_()
+    assert torch.equal(lazy.compact["L.w"], torch.zeros_like(lazy.compact["L.w"]))  # reading materializes
+    lazy.compact["L.w"].fill_(7.0)
+    lazy.zero_()
+    for rb, cb in ops:  # first add overwrites the stale 7.0 values, the second accumulates
+        lazy.add_sampled("L.w", rb, cb, offsets, dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(lazy.compact["L.w"], fresh.compact["L.w"])
+    assert bool((fresh.compact["L.w"] != 0).any())
+
+
 @pytest.mark.parametrize("T,E,H", [(4096, 128, 2048), (100, 16, 264), (1, 8, 8), (1000, 256, 136), (0, 8, 16)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_router_dw_vs_fp64(gpu_device, T, E, H, dtype):
