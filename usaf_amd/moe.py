@@ -289,8 +289,23 @@ def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Opt
 # the routed expert layer
 # ---------------------------------------------------------------------------
 
+# Optional per-launch timing of the fused GEMMs: None, or a dict that collects
+# entry-point name -> [(start, end) HIP events recorded on the launch stream].
+# bench.py sets it over its timed steps.
+launch_events: Optional[dict] = None
+
+
 def _gemm_call(name, *args):
+    ev = launch_events
+    if ev is None:
+        N.call(name, *args)
+        return
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
     N.call(name, *args)
+    b.record()
+    ev.setdefault(name, []).append((a, b))
 
 
 class RoutedExpertsFn(torch.autograd.Function):
