@@ -292,17 +292,24 @@ def bench_moe_step(dev, steps: int, warmup: int) -> dict:
         loop.step()
     loop.flush()
     loop.applied = loop.skipped = loop.recomputed = 0
-    G.launch_events = {}  # HIP events around each fused-GEMM launch of the timed steps
+    with _Timer() as t:
+        for _ in range(steps):
+            loop.step()
+        loop.flush()
+    ms = t.ms / steps
+    counts = (loop.applied, loop.skipped, loop.recomputed)
+    # the same steps again with a HIP event pair around each fused-GEMM launch
+    # (kept out of the run above: each event adds a few µs to the step)
+    G.launch_events = {}
     try:
-        with _Timer() as t:
+        with _Timer():
             for _ in range(steps):
                 loop.step()
             loop.flush()
     finally:
         events, G.launch_events = G.launch_events, None
-    ms = t.ms / steps
-    _log(f"moe step: {loop.applied} of {steps} timed steps applied, {loop.skipped} skipped (non-finite), "
-         f"{loop.recomputed} recomputed after overflowing the static slot capacity")
+    _log(f"moe step: {counts[0]} of {steps} timed steps applied, {counts[1]} skipped (non-finite), "
+         f"{counts[2]} recomputed after overflowing the static slot capacity")
     fl = moe_step_flops(L["T"], L["H"], L["I"], L["E"], L["k"], L["n_act"]["gate_up_proj"],
                         L["n_act"]["down_proj"])
     kern = moe_kernel_times(L, events)
@@ -311,9 +318,10 @@ def bench_moe_step(dev, steps: int, warmup: int) -> dict:
 
 
 def moe_kernel_times(L, events: dict) -> dict:
-    """Average duration of each fused GEMM over its launches inside the timed
-    steps (HIP events recorded around the launches on their stream) and its
-    algorithmic FLOPs, 2 * S * N * K with S the step's routed slot count."""
+    """Average duration of each fused GEMM over its launches inside the steps
+    (HIP events recorded around the launches on their stream; the event pair
+    also takes in the launch's dispatch) and its algorithmic FLOPs,
+    2 * S * N * K with S the step's routed slot count."""
     from usaf_amd import moe as G
     T, H, I, E = L["T"], L["H"], L["I"], L["E"]
     with torch.no_grad():
@@ -432,8 +440,8 @@ def _load_traffic() -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--probe-kernels", action="store_true",
                     help="launch each hot kernel once (counter-collection target) and exit")
@@ -459,7 +467,7 @@ def main() -> int:
     for name, kv in mo["kernels"].items():
         if isinstance(kv, dict):
             _log(f"  {name}: {kv['ms']:.3f} ms, {kv['tflops']:.1f} TFLOP/s (average of {kv['launches']} launches "
-                 f"inside the timed steps)")
+                 f"inside the steps)")
     _log("dequant: one Qwen3 MoE layer (603,979,776 elements) -> bf16")
     dq = bench_dequant(dev, args.steps, args.warmup)
     _log(f"dequant: {dq['ms_per_launch']:.3f} ms/launch, {dq['gbs']:.1f} GB/s")
