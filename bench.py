@@ -372,7 +372,7 @@ def bench_moe_kernels(L, reps: int) -> None:
     qdt = ew._ptrs_t("down")
     for _ in range(reps):
         N.call("usaf_hip_moe_gate_up_fwd", x.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(), S, E, I,
-               *qg, code, gu.data_ptr(), act.data_ptr(), st)
+               *qg, code, gu.data_ptr(), act.data_ptr(), None, None, st)
         N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *qd, code, y.data_ptr(), st)
         N.call("usaf_hip_moe_down_bwd_t", y.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I, *qdt, code,
                dgu.data_ptr(), st)

@@ -200,10 +200,16 @@ int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_
 
 /* Replaces qwen3moe_dml.py:58-60 per routed slot: gu[s] = x[token_idx[s]] @ W_gate_up[e]^T
  * ([S, 2I], dtype-rounded), act[s] = dtype(dtype(silu(gate)) * up) ([S, I]).
- * x [T, H] (token_idx values < T); W_gate_up [E, 2I, H]; needs H % 128 == 0, I % 64 == 0. */
+ * x [T, H] (token_idx values < T); W_gate_up [E, 2I, H]; needs H % 128 == 0, I % 64 == 0.
+ * act_blk (optional, 16-byte aligned): act also in the blocked slot-major layout
+ * of blk_table (usaf_hip_blocked_layout of the same offsets and S), as
+ * usaf_hip_gather_transpose_blocked(act, ...) would write it -- the column operand
+ * of the down projection's sampled gradient; the 4-bit kernel writes it from its
+ * epilogue. */
 int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T, int64_t H, const int32_t* token_idx, const int32_t* offsets, int64_t S,
                              int64_t E, int64_t I, const int8_t* wq, const uint32_t* wsz,
-                             const void* w16, int32_t dtype, void* gu, void* act, void* stream);
+                             const void* w16, int32_t dtype, void* gu, void* act, void* act_blk,
+                             const int32_t* blk_table, void* stream);
 
 /* Replaces qwen3moe_dml.py:61: y[s] = act[s] @ W_down[e]^T ([S, H]).  W_down [E, H, I];
  * needs I % 128 == 0, H % 128 == 0. */

@@ -195,11 +195,13 @@ def test_experts_edge_shapes(gpu_device, E, T, k):
     assert rel_err(w.grad.cpu()[routed], dw_r[routed]) <= 1e-2
 
 
-def test_experts_forward_intermediates(gpu_device):
-    # per-slot gate_up / SwiGLU / down outputs against the oracle's per-expert tensors
-    _say("experts fwd intermediates E=8 H=256 I=128 bf16")
+@pytest.mark.parametrize("T", [300, 1500])
+def test_experts_forward_intermediates(gpu_device, T):
+    # per-slot gate_up / SwiGLU / down outputs against the oracle's per-expert tensors;
+    # the blocked act^T written by the gate_up epilogue against the blocked transpose of act
+    _say(f"experts fwd intermediates E=8 H=256 I=128 T={T} bf16")
     dt = torch.bfloat16
-    L = make_layer(gpu_device, 8, 256, 128, 300, 2, dt, seed=2)
+    L = make_layer(gpu_device, 8, 256, 128, T, 2, dt, seed=2)
     _, slots = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"], return_slots=True)
     b = G.bucket_by_expert(L["w"].to(gpu_device))
     ew = L["ew"]
@@ -210,12 +212,20 @@ def test_experts_forward_intermediates(gpu_device):
     from usaf_amd import _native as N
     st = N.stream_ptr(gpu_device)
     q, sz, w16 = ew._ptrs("gate_up", dt)
+    tb = G.blocked_layout(b.offsets, S)
+    lib = N.load()
+    act_blk = torch.full((int(lib.usaf_hip_blocked_elems(S, ew.E, I)),), float("nan"), dtype=dt, device=gpu_device)
     N.call("usaf_hip_moe_gate_up_fwd", L["hs"].to(gpu_device).data_ptr(), L["hs"].shape[0], H, b.token_idx.data_ptr(),
-           b.offsets.data_ptr(), S, ew.E, I, q, sz, w16, N.BF16, gu.data_ptr(), act.data_ptr(), st)
+           b.offsets.data_ptr(), S, ew.E, I, q, sz, w16, N.BF16, gu.data_ptr(), act.data_ptr(), act_blk.data_ptr(),
+           tb.data_ptr(), st)
     q, sz, w16 = ew._ptrs("down", dt)
     N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, ew.E, H, q, sz, w16, N.BF16,
            y.data_ptr(), st)
+    want_blk = G.slot_blocked(act, b.offsets, S, table=tb)
     torch.cuda.synchronize()
+    n_used = int(want_blk.table[ew.E]) * I  # elements of the layout (the rest of the buffer is never written)
+    assert n_used > 0
+    assert torch.equal(act_blk[:n_used].view(torch.int16), want_blk.data[:n_used].view(torch.int16))
     offs = b.offsets.cpu().tolist()
     for e, sl in slots.items():
         s0, s1 = offs[e], offs[e + 1]

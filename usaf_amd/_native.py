@@ -43,7 +43,7 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_moe_combine": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p],
     "usaf_hip_moe_combine_bwd": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p],
     "usaf_hip_moe_gate_up_fwd": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
-                                 _c_i32, _c_p, _c_p, _c_p],
+                                 _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p],
     "usaf_hip_moe_down_fwd": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p],
     "usaf_hip_moe_down_bwd": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p,
                               _c_p],

@@ -79,6 +79,8 @@ struct GemmArgs {
   uint16_t* out;  int64_t ldo;   // STORE: C; SWIGLU_FWD: act; SWIGLU_BWD: dgu
   uint16_t* out2; int64_t ldo2;  // SWIGLU_FWD: gu
   const uint16_t* aux; int64_t ld_aux;  // SWIGLU_BWD: saved gu
+  uint16_t* out_t;                // SWIGLU_FWD (4-bit DMA kernel): act also in the blocked slot-major
+  const int32_t* blk_table;       //   layout of blk_table (usaf_hip_blocked_layout), or nullptr
 };
 
 // Workgroup barrier ordering LDS accesses only.  __syncthreads() also orders
@@ -1474,6 +1476,17 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     if constexpr (EPI == EPI_SWIGLU_FWD) {
       const int64_t n0 = (int64_t)t.nt * 128 + wave * 32;
       if (n0 >= g.inter) return;
+      // blocked act^T: the expert's block holds, per feature n, ld = round_up(se, 16)
+      // slots (zero past se); tblk points at feature n0's row of it
+      uint16_t* tblk = nullptr;
+      int jt = 0, se = 0, ld = 0;
+      if (g.out_t) {  // wave-uniform
+        const int s0 = s_off[t.e];
+        se = s_off[t.e + 1] - s0;
+        ld = (se + 15) & ~15;
+        jt = t.m_beg - s0;
+        tblk = g.out_t + g.inter * (int64_t)g.blk_table[t.e] + n0 * (int64_t)ld;
+      }
 #pragma unroll
       for (int i = 0; i < NRB; ++i) {
         if (32 * i >= t.valid) break;
@@ -1506,6 +1519,26 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
             *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + n0 + ch) = gv;
             *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + g.inter + n0 + ch) = uv;
             *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n0 + ch) = av;
+          }
+        }
+        if (tblk) {
+          // the staged act columns read down the slots: chunk c = lane + 64 p is
+          // feature c >> 2, slots 8 (c & 3) + [0, 8) of block i, one 16-byte store
+          // per chunk; slots at or past se (padding up to ld) are zero
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const int c = lane + 64 * p, f = c >> 2, sg = c & 3;
+            const int j = jt + 32 * i + 8 * sg;
+            if (j < ld) {
+              uint32_t w[4];
+#pragma unroll
+              for (int k2 = 0; k2 < 4; ++k2) {
+                const uint32_t lo = j + 2 * k2 < se ? sEp[(8 * sg + 2 * k2) * Q_EPW + 64 + f] : 0u;
+                const uint32_t hi = j + 2 * k2 + 1 < se ? sEp[(8 * sg + 2 * k2 + 1) * Q_EPW + 64 + f] : 0u;
+                w[k2] = lo | (hi << 16);
+              }
+              *reinterpret_cast<u32x4*>(tblk + f * (int64_t)ld + j) = u32x4{w[0], w[1], w[2], w[3]};
+            }
           }
         }
       }
@@ -1697,6 +1730,13 @@ int launch_q4t(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_tota
   return check_launch(what);
 }
 
+// 4-bit weights go to the LDS-DMA kernel when the activation rows are 16-byte
+// aligned and the row and code offsets within one operand fit 32-bit byte offsets
+bool q4_dma_ok(const GemmArgs& g, int64_t a_rows_total) {
+  return g.w16 == nullptr && ((uintptr_t)g.A & 15) == 0 && g.lda % 8 == 0 && g.K % 128 == 0 && g.E <= Q_MAX_E &&
+         a_rows_total * g.lda * 2 < ((int64_t)1 << 32) && (int64_t)g.E * g.w_rows * g.w_cols / 2 < ((int64_t)1 << 32);
+}
+
 template <int EPI>
 int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_total, hipStream_t st,
                    const char* what) {
@@ -1707,11 +1747,7 @@ int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_
   if (blocks > max_tiles) blocks = max_tiles;
   if (blocks < 1) blocks = 1;
   const bool dense = g.w16 != nullptr;
-  // 4-bit weights: the LDS-DMA kernel (activation rows must be 16-byte aligned)
-  // (row offsets and code offsets within one operand as 32-bit byte offsets)
-  const bool dma = !dense && ((uintptr_t)g.A & 15) == 0 && g.lda % 8 == 0 && g.K % 128 == 0 && g.E <= Q_MAX_E &&
-                   a_rows_total * g.lda * 2 < ((int64_t)1 << 32) &&
-                   (int64_t)g.E * g.w_rows * g.w_cols / 2 < ((int64_t)1 << 32);
+  const bool dma = q4_dma_ok(g, a_rows_total);
   int rc;
   if (dt == USAF_BF16)
     rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
@@ -1785,7 +1821,8 @@ using namespace usaf;
 // Forward gate_up + SwiGLU (qwen3moe_dml.py:58-60, per routed slot).
 extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T_rows, int64_t H, const int32_t* token_idx, const int32_t* offsets,
                                         int64_t S, int64_t E, int64_t I, const int8_t* wq, const uint32_t* wsz,
-                                        const void* w16, int32_t dtype, void* gu, void* act, void* stream) {
+                                        const void* w16, int32_t dtype, void* gu, void* act, void* act_blk,
+                                        const int32_t* blk_table, void* stream) {
   if (int rc = check_common("moe_gate_up_fwd", S, E, offsets, wq, wsz, w16)) return rc;
   if (H % 128 != 0 || H <= 0 || I % 32 != 0 || I <= 0)
     return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_fwd: needs H %% 128 == 0 and I %% 32 == 0 (H=%lld, I=%lld)",
@@ -1797,8 +1834,20 @@ extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T_rows, int64_t H
   g.wq = (const uint8_t*)wq; g.wsz = wsz; g.w16 = (const uint16_t*)w16; g.w_rows = 2 * I; g.w_cols = H;
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)act; g.ldo = I; g.out2 = (uint16_t*)gu; g.ldo2 = 2 * I;
+  if (act_blk && !blk_table) return set_error(USAF_ERR_INVALID, "moe_gate_up_fwd: act_blk needs blk_table");
+  if (act_blk && ((uintptr_t)act_blk & 15)) return set_error(USAF_ERR_INVALID, "moe_gate_up_fwd: act_blk must be 16-byte aligned");
+  // the 4-bit DMA kernel writes the blocked act^T from its epilogue; the other
+  // kernels leave it to the blocked transpose of act afterwards
+  const bool fused_t = act_blk && q4_dma_ok(g, T_rows);
+  if (fused_t) {
+    g.out_t = (uint16_t*)act_blk;
+    g.blk_table = blk_table;
+  }
   const int64_t max_tiles = (S / NK_BM + E) * ((I + 127) / 128);
-  return launch_gemm_nk<EPI_SWIGLU_FWD>(g, dtype, max_tiles, T_rows, as_stream(stream), "moe_gate_up_fwd");
+  if (int rc = launch_gemm_nk<EPI_SWIGLU_FWD>(g, dtype, max_tiles, T_rows, as_stream(stream), "moe_gate_up_fwd")) return rc;
+  if (act_blk && !fused_t)
+    return usaf_hip_gather_transpose_blocked(act, I, nullptr, offsets, blk_table, S, E, I, act_blk, stream);
+  return USAF_OK;
 }
 
 // Forward down projection (qwen3moe_dml.py:61): y[m] = act[m] @ W_down[e]^T.

@@ -245,12 +245,14 @@ def _sampled_blocked(capture, b: "Buckets") -> bool:
 
 
 def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Optional[torch.Tensor],
-             b: "Buckets", full_shape, dtype, dy_blocked: Optional["BlockedSlots"] = None) -> None:
+             b: "Buckets", full_shape, dtype, dy_blocked: Optional["BlockedSlots"] = None,
+             x_blocked: Optional["BlockedSlots"] = None) -> None:
     """Deliver the weight gradient of ``{prefix}.{which}`` (dW_e = dy_e^T @ x_e over
     expert e's slots; x_e = x[x_rows] when x_rows is given) to the capture store.
 
     SparseGradStore (``add_sampled``): only the active positions, by the
-    sampled-product kernel.  Other stores get dense per-expert gradients in
+    sampled-product kernel (dy_blocked / x_blocked: the operands already in
+    the blocked layout of b.blk_table, written by the kernels that produced them).  Other stores get dense per-expert gradients in
     the activation dtype, as F.linear's weight grad in the reference:
     ``store.add(name, ei, g)`` or, for a dict store, accumulation into
     per-tensor fp16 CPU buffers (usaf/qwen3moe_dml.py:34-47).
@@ -263,8 +265,9 @@ def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Opt
                 b.blk_table = blocked_layout(b.offsets, b.n_slots)
             if dy_blocked is None:
                 dy_blocked = slot_blocked(dy, b.offsets, b.n_slots, table=b.blk_table)
-            store.add_sampled(name, dy_blocked,
-                              slot_blocked(x, b.offsets, b.n_slots, rows=x_rows, table=b.blk_table), b.offsets, dtype)
+            if x_blocked is None:
+                x_blocked = slot_blocked(x, b.offsets, b.n_slots, rows=x_rows, table=b.blk_table)
+            store.add_sampled(name, dy_blocked, x_blocked, b.offsets, dtype)
         else:
             store.add_sampled(name, slot_major(dy), slot_major(x, rows=x_rows), b.offsets, dtype)
         return
@@ -336,10 +339,20 @@ class RoutedExpertsFn(torch.autograd.Function):
         gu = torch.empty(S, 2 * I, dtype=dt, device=dev)
         act = torch.empty(S, I, dtype=dt, device=dev)
         y = torch.empty(S, H, dtype=dt, device=dev)
+        act_blk = None
+        if S > 0 and _sampled_blocked(capture, b):
+            # the down projection's sampled gradient reads act blocked slot-major:
+            # written by the gate_up epilogue, with act
+            if b.blk_table is None:
+                b.blk_table = blocked_layout(b.offsets, S)
+            n_blk = max(1, int(N.load().usaf_hip_blocked_elems(S, E, I)))
+            act_blk = BlockedSlots(torch.empty(n_blk, dtype=dt, device=dev), I, b.offsets, b.blk_table)
         if S > 0:
             q, sz, w16 = ew._ptrs("gate_up", dt)
             _gemm_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
-                       S, E, I, q, sz, w16, code, gu.data_ptr(), act.data_ptr(), st)
+                       S, E, I, q, sz, w16, code, gu.data_ptr(), act.data_ptr(),
+                       None if act_blk is None else act_blk.data.data_ptr(),
+                       None if act_blk is None else b.blk_table.data_ptr(), st)
             q, sz, w16 = ew._ptrs("down", dt)
             _gemm_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
                        code, y.data_ptr(), st)
@@ -347,6 +360,7 @@ class RoutedExpertsFn(torch.autograd.Function):
         ctx.ew = ew
         ctx.capture = capture
         ctx.b = b
+        ctx.act_blk = act_blk
         ctx.wdt = (None if w_gate_up is None else w_gate_up.dtype, None if w_down is None else w_down.dtype)
         ctx.save_for_backward(hs, gu, act, y)
         return out
@@ -396,7 +410,8 @@ class RoutedExpertsFn(torch.autograd.Function):
             _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
                        q, sz, w16, code, dgu.data_ptr(), st)
         if capture is not None:
-            _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt, dy_blocked=dcur_blk)
+            _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt, dy_blocked=dcur_blk,
+                     x_blocked=ctx.act_blk)
         if want_dn:
             _dense_weight_grad(d_wdn, dcur, act, None, b)
         dx_slots = torch.empty(S, H, dtype=dt, device=dev)
