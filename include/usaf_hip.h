@@ -44,6 +44,16 @@ int usaf_hip_abi_version(void);
 const char* usaf_hip_last_error(void);
 
 /*
+ * One-time host set-up for the current device: caches its CU count, raises the
+ * dynamic-LDS limit of every GEMM kernel and queries the occupancy of the
+ * sampled-gradient kernels.  Every entry point does the parts it needs on first
+ * use (thread-safe); calling this once beforehand keeps those host-side HIP
+ * calls out of later work, e.g. out of a stream capture.  No counterpart in the
+ * reference (its Vulkan module initialises on import, usaf/vulkan/src/pybind_module.cpp:487-555).
+ */
+int usaf_hip_init(void);
+
+/*
  * 4-bit unpack + dequant.
  * Replaces usaf/quantization.py:88-132 `dequantize_4bit` (and the Vulkan
  * `dequant_pipe`, usaf/vulkan/src/pybind_module.cpp:175-200).

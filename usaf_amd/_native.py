@@ -32,6 +32,7 @@ _c_p = ctypes.c_void_p
 _c_d = ctypes.c_double
 
 _SIGNATURES: dict[str, list] = {
+    "usaf_hip_init": [],
     "usaf_hip_dequant_q4": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i32, _c_p],
     "usaf_hip_quantize_q4": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],
     "usaf_hip_pack_scale_zero": [_c_p, _c_p, _c_i64, _c_p, _c_p],
@@ -111,6 +112,7 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = restype
             fn.argtypes = argtypes
+        check(lib.usaf_hip_init(), "usaf_hip_init") if torch.cuda.is_available() else None
         _lib = lib
     return _lib
 

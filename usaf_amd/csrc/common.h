@@ -20,6 +20,11 @@ int set_error(int code, const char* fmt, ...);
 int clear_error();
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
+// One-time host set-up of the GEMM kernels (dynamic-LDS limits) and of the
+// sampled-gradient kernels (occupancy queries); safe to call from any thread,
+// run by usaf_hip_init() and otherwise on first use.
+void prepare_gemm_kernels();
+void prepare_sparse_kernels();
 
 // 16-bit float types used in device code.
 typedef _Float16 f16;

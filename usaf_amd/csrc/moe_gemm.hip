@@ -1685,28 +1685,41 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // drain the trailing DMAs before the wave ends
 }
 
+// The dynamic-LDS limit of each kernel instantiation is raised once per
+// process, before its first launch: each *_prepare() holds a function-local
+// static whose initializer C++11 runs exactly once even under concurrent first
+// calls (the reference's prefetch thread), and usaf_hip_init() runs them all
+// up front for callers that must not make such calls later (stream capture).
+// A runtime that does not need (or know) the attribute may refuse it; the
+// launch reports any real problem.
+bool raise_lds_limit(const void* kernel, size_t bytes) {
+  (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  (void)hipGetLastError();
+  return true;
+}
+
+template <int EPI, int BQ, int DT>
+void nk_prepare() {
+  static const bool done = raise_lds_limit(reinterpret_cast<const void*>(&moe_gemm_nk_kernel<EPI, BQ, DT>), kNkSmemBytes);
+  (void)done;
+}
+
 template <int EPI, int BQ, int DT>
 int launch_nk_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_nk_kernel<EPI, BQ, DT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kNkSmemBytes);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  nk_prepare<EPI, BQ, DT>();
   moe_gemm_nk_kernel<EPI, BQ, DT><<<blocks, NK_THREADS, kNkSmemBytes, st>>>(g);
   return USAF_OK;
 }
 
+template <int EPI, int DT, bool BT>
+void q4_prepare() {
+  static const bool done = raise_lds_limit(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT, BT>), kQSmemBytes);
+  (void)done;
+}
+
 template <int EPI, int DT, bool BT = false>
 int launch_q4_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT, BT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQSmemBytes);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  q4_prepare<EPI, DT, BT>();
   moe_gemm_q4_kernel<EPI, DT, BT><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
   return USAF_OK;
 }
@@ -1764,16 +1777,14 @@ int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_
 }
 
 template <int BMODE, int EPI, int BQ, int DT>
+void ws_prepare() {
+  static const bool done = raise_lds_limit(reinterpret_cast<const void*>(&moe_gemm_kernel<BMODE, EPI, BQ, DT>), kSmemBytes);
+  (void)done;
+}
+
+template <int BMODE, int EPI, int BQ, int DT>
 int launch_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
-  static bool attr_set = false;  // per instantiation; the attribute is a property of the function
-  if (!attr_set) {
-    // Raise the dynamic-LDS limit for this kernel.  A runtime that does not need
-    // (or know) the attribute may refuse it; the launch below reports any real problem.
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gemm_kernel<BMODE, EPI, BQ, DT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSmemBytes);
-    (void)hipGetLastError();
-    attr_set = true;
-  }
+  ws_prepare<BMODE, EPI, BQ, DT>();
   moe_gemm_kernel<BMODE, EPI, BQ, DT><<<blocks, kThreads, kSmemBytes, st>>>(g);
   return USAF_OK;
 }
@@ -1813,7 +1824,30 @@ int check_common(const char* what, int64_t S, int64_t E, const void* offsets, co
   return USAF_OK;
 }
 
+template <int DT>
+void prepare_dt() {
+  nk_prepare<EPI_SWIGLU_FWD, BQ_Q4, DT>();
+  nk_prepare<EPI_SWIGLU_FWD, BQ_DENSE16, DT>();
+  nk_prepare<EPI_STORE, BQ_Q4, DT>();
+  nk_prepare<EPI_STORE, BQ_DENSE16, DT>();
+  q4_prepare<EPI_SWIGLU_FWD, DT, false>();
+  q4_prepare<EPI_STORE, DT, false>();
+  q4_prepare<EPI_SWIGLU_BWD, DT, true>();
+  q4_prepare<EPI_STORE, DT, true>();
+  ws_prepare<BMODE_KN, EPI_SWIGLU_BWD, BQ_Q4, DT>();
+  ws_prepare<BMODE_KN, EPI_SWIGLU_BWD, BQ_DENSE16, DT>();
+  ws_prepare<BMODE_KN, EPI_STORE, BQ_Q4, DT>();
+  ws_prepare<BMODE_KN, EPI_STORE, BQ_DENSE16, DT>();
+}
+
 }  // namespace
+
+// Every kernel instantiation the GEMM entry points launch.
+void prepare_gemm_kernels() {
+  prepare_dt<USAF_F16>();
+  prepare_dt<USAF_BF16>();
+}
+
 }  // namespace usaf
 
 using namespace usaf;

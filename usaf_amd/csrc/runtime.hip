@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 namespace usaf {
 
 static thread_local char g_last_error[1024] = {0};
@@ -22,16 +24,18 @@ int clear_error() {
 }
 
 int device_cu_count() {
-  // Up to 64 devices per process; the count never changes for a device.
-  static int cached[64] = {0};
+  // Up to 64 devices per process; the count never changes for a device.  Each
+  // slot is written once with the same value by whichever thread gets there
+  // first, so relaxed atomics suffice.
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 }  // namespace usaf
@@ -39,3 +43,15 @@ int device_cu_count() {
 extern "C" int usaf_hip_abi_version(void) { return USAF_HIP_ABI_VERSION; }
 
 extern "C" const char* usaf_hip_last_error(void) { return usaf::g_last_error; }
+
+extern "C" int usaf_hip_init(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return usaf::set_error(USAF_ERR_RUNTIME, "init: no current HIP device");
+  }
+  (void)usaf::device_cu_count();
+  usaf::prepare_gemm_kernels();
+  usaf::prepare_sparse_kernels();
+  return usaf::clear_error();
+}

@@ -610,7 +610,24 @@ int resident_blocks_per_cu(const void* kernel) {
   }
   return n;
 }
+
+// Resident blocks per CU of the four sampled-gradient kernel instantiations,
+// queried once per process (a function-local static: C++11 runs its
+// initializer exactly once, also under concurrent first calls).
+struct SddmmOccupancy {
+  int masked_bf16, masked_f16, blocked_bf16, blocked_f16;
+};
+const SddmmOccupancy& sddmm_occupancy() {
+  static const SddmmOccupancy occ = {
+      resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_kernel<USAF_BF16>)),
+      resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_kernel<USAF_F16>)),
+      resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_blocked_kernel<USAF_BF16>)),
+      resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_blocked_kernel<USAF_F16>))};
+  return occ;
+}
 }  // namespace
+
+void usaf::prepare_sparse_kernels() { (void)sddmm_occupancy(); }
 
 extern "C" int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const int32_t* rows, int64_t S, int64_t C,
                                          void* out, int64_t ld_out, void* stream) {
@@ -645,10 +662,9 @@ extern "C" int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t
   if (((uintptr_t)rowT & 15) || ((uintptr_t)colT & 15))
     return set_error(USAF_ERR_INVALID, "sddmm_masked: rowT and colT must be 16-byte aligned");
   if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "sddmm_masked: dtype must be 16-bit");
-  static const int per_cu_b = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_kernel<USAF_BF16>));
-  static const int per_cu_h = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_kernel<USAF_F16>));
+  const SddmmOccupancy& occ = sddmm_occupancy();
   int64_t blocks = (n_pos + 15) / 16;
-  const int64_t cap = (int64_t)device_cu_count() * (dtype == USAF_BF16 ? per_cu_b : per_cu_h);
+  const int64_t cap = (int64_t)device_cu_count() * (dtype == USAF_BF16 ? occ.masked_bf16 : occ.masked_f16);
   if (blocks > cap) blocks = cap;
   hipStream_t st = as_stream(stream);
   if (dtype == USAF_BF16)
@@ -743,10 +759,9 @@ extern "C" int usaf_hip_sddmm_blocked(const void* row_blk, const void* col_blk, 
   if (((uintptr_t)row_blk & 15) || ((uintptr_t)col_blk & 15))
     return set_error(USAF_ERR_INVALID, "sddmm_blocked: operands must be 16-byte aligned");
   if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "sddmm_blocked: dtype must be 16-bit");
-  static const int per_cu_b = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_blocked_kernel<USAF_BF16>));
-  static const int per_cu_h = resident_blocks_per_cu(reinterpret_cast<const void*>(&sddmm_blocked_kernel<USAF_F16>));
+  const SddmmOccupancy& occ = sddmm_occupancy();
   int64_t blocks = (n_pos + 15) / 16;
-  const int64_t cap = (int64_t)device_cu_count() * (dtype == USAF_BF16 ? per_cu_b : per_cu_h);
+  const int64_t cap = (int64_t)device_cu_count() * (dtype == USAF_BF16 ? occ.blocked_bf16 : occ.blocked_f16);
   if (blocks > cap) blocks = cap;
   hipStream_t st = as_stream(stream);
   if (dtype == USAF_BF16)
