@@ -123,3 +123,94 @@ def combine_slots(y_slots: torch.Tensor, offsets, token_idx: torch.Tensor, weigh
         idx = token_idx[s0:s1].long()
         final = final.index_add(0, idx, y_slots[s0:s1].float() * weights[idx, e].float().unsqueeze(-1))
     return final.to(weights.dtype)
+
+
+def _rd(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Round an fp32 tensor to `dtype` and back: the output of one torch op in
+    that dtype (torch computes 16-bit ops in fp32 and rounds the result once)."""
+    return x.to(dtype).float()
+
+
+def experts_routed_manual(hs, weights, w_gate_up, w_down, dout, active=None):
+    """The forward and backward of experts_routed_autograd (the routed expert
+    loop of benchmarks/kaggle_t4_bench.py:253-282 and qwen3moe_dml.py:58-64,
+    differentiated as torch autograd does), written out op by op.
+
+    Every op computes in fp32 and rounds its output to the activation dtype
+    where the reference's dtype op does: F.linear outputs (forward, grad-input
+    and grad-weight), F.silu and the SwiGLU product, silu_backward, the mul
+    backwards, the expert output's cast of its gradient; the combine and its
+    backward stay in fp32 (qwen3moe_dml.py:62-64).  Gradients reaching the same
+    token from several experts are summed in fp32 and rounded once.  Instead of
+    the dense per-expert weight gradients, ``active`` {"gate_up_proj": flat
+    idx, "down_proj": flat idx} asks for their values at those positions only,
+    as SparseGradStore.add gathers them (usaf/moe_loader.py:564-578): fp32 of
+    the dtype-rounded dot product over the expert's routed tokens.
+
+    Returns (out, dhs, dweights, compact) with compact {name: fp32 [n]}.
+    Large shapes run in seconds on CPU threads, where the dtype autograd of the
+    same loop (experts_routed_autograd) takes minutes; tests pin one against
+    the other on small shapes."""
+    dt = hs.dtype
+    T, H = hs.shape
+    E, I2, _ = w_gate_up.shape
+    I = I2 // 2
+    hs32 = hs.float()
+    dout32 = dout.float()
+    final = torch.zeros(T, H, dtype=torch.float32)
+    dhs = torch.zeros(T, H, dtype=torch.float32)
+    dweights = torch.zeros(T, E, dtype=torch.float32)
+    per_expert = {}
+    if active is not None:
+        for name, rows, cols in (("gate_up_proj", I2, H), ("down_proj", H, I)):
+            idx = active[name].reshape(-1).long()
+            e_of = torch.div(idx, rows * cols, rounding_mode="floor")
+            per_expert[name] = (idx, e_of, rows, cols)
+    compact = {name: torch.zeros(v[0].numel(), dtype=torch.float32) for name, v in per_expert.items()}
+
+    def sampled(name, ei, dy, x):
+        if name not in per_expert:
+            return
+        idx, e_of, rows, cols = per_expert[name]
+        sel = (e_of == ei).nonzero(as_tuple=False).reshape(-1)
+        if sel.numel() == 0:
+            return
+        local = idx[sel] - ei * rows * cols
+        o = torch.div(local, cols, rounding_mode="floor")
+        i = local - o * cols
+        for c0 in range(0, sel.numel(), 65536):  # bounded temporaries
+            oc, ic = o[c0:c0 + 65536], i[c0:c0 + 65536]
+            dots = (dy[:, oc] * x[:, ic]).sum(0)
+            compact[name][sel[c0:c0 + 65536]] = _rd(dots, dt)
+
+    for ei in range(E):
+        w_col = weights[:, ei]
+        idx = torch.nonzero(w_col, as_tuple=False).reshape(-1)
+        if idx.numel() == 0:
+            continue
+        x = hs32.index_select(0, idx)
+        wg = w_gate_up[ei].float()
+        wd = w_down[ei].float()
+        w_e = w_col.index_select(0, idx).float().unsqueeze(-1)
+        # forward (qwen3moe_dml.py:58-62)
+        gu = _rd(x @ wg.t(), dt)
+        g, u = gu[:, :I], gu[:, I:]
+        sig = torch.sigmoid(g)
+        sg = _rd(g * sig, dt)
+        act = _rd(sg * u, dt)
+        y = _rd(act @ wd.t(), dt)
+        final.index_add_(0, idx, y * w_e)
+        # backward of final + y.float() * w (fp32), then of each dtype op
+        d_fin = dout32.index_select(0, idx)
+        dweights[idx, ei] = (d_fin * y).sum(-1)
+        dy = _rd(d_fin * w_e, dt)
+        dact = _rd(dy @ wd, dt)
+        sampled("down_proj", ei, dy, act)
+        dsg = _rd(dact * u, dt)
+        du = _rd(dact * sg, dt)
+        dg = _rd(dsg * (sig * (1.0 + g * (1.0 - sig))), dt)
+        dgu = torch.cat([dg, du], dim=1)
+        dx = _rd(dgu @ wg, dt)
+        sampled("gate_up_proj", ei, dgu, x)
+        dhs.index_add_(0, idx, dx)
+    return final.to(dt), dhs.to(dt), dweights.to(dt), compact

@@ -193,3 +193,36 @@ def test_combine_slots_brute_force():
             ref[t] += y[s].double() * float(w[t, e])
     assert torch.allclose(out.double(), ref, rtol=1e-6, atol=1e-6)
     assert torch.all(out[(w != 0).sum(1) == 0] == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_manual_backward_matches_autograd(dtype):
+    # experts_routed_manual (fp32 ops rounded at the reference's dtype op
+    # outputs, sampled weight gradient only) against the dtype autograd oracle;
+    # the two differ only in fp32 summation order and in where several
+    # experts' token gradients are added
+    g = torch.Generator().manual_seed(21)
+    E, H, I, T, k = 8, 256, 128, 300, 2
+    wg = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(dtype)
+    wd = (torch.randn(E, H, I, generator=g) * 0.02).to(dtype)
+    hs = torch.randn(T, H, generator=g).to(dtype)
+    w, _, _ = M.route(torch.randn(T, E, generator=g), k, False, dtype)
+    dout = torch.randn(T, H, generator=g).to(dtype)
+    nG, nD = wg.numel(), wd.numel()
+    active = {"gate_up_proj": torch.randperm(nG, generator=g)[: nG // 200],
+              "down_proj": torch.randperm(nD, generator=g)[: nD // 200]}
+    out_m, dhs_m, dw_m, comp = M.experts_routed_manual(hs, w, wg, wd, dout, active)
+    out_a = M.experts_routed(hs, w, wg, wd)
+    dhs_a, dw_a, dwg_a, dwd_a = M.experts_routed_autograd(hs, w, wg, wd, dout)
+    tol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+
+    def rel(a, b):
+        return float((a.float() - b.float()).abs().max() / b.float().abs().max())
+
+    assert rel(out_m, out_a) <= tol / 4
+    assert rel(dhs_m, dhs_a) <= tol / 4
+    routed = w != 0
+    assert torch.all(dw_m[~routed] == 0)
+    assert rel(dw_m[routed], dw_a[routed]) <= tol / 4
+    assert rel(comp["gate_up_proj"], M.gather_compact(dwg_a, active["gate_up_proj"])) <= tol / 4
+    assert rel(comp["down_proj"], M.gather_compact(dwd_a, active["down_proj"])) <= tol / 4
