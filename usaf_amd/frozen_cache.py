@@ -1,78 +1,200 @@
-"""Frozen-layer activation cache on disk (usaf/frozen_cache.py:14-74).
+"""Frozen-layer activation cache (drop-in for usaf/frozen_cache.py).
 
-hidden@DETACH_AT is computed once per sample and kept as an fp16 ``.npy``
-memory map with a JSON fingerprint; training then starts at layer
-DETACH_AT + 1.  ``get_hidden`` stages a sample through pinned host memory into
-the device (HBM) asynchronously.
+The hidden state after layer ``detach_at`` is computed once per training
+sample and kept on disk as an fp16 ``.npy`` array [N, seq, hidden] with a
+JSON sidecar (``<path>.json``: fingerprint, N, seq, hidden, detach_at); the
+fingerprint hashes the layer, the model source and every sample's input ids
+(usaf/frozen_cache.py:14-22), so a reference-built cache is reused here and
+the other way round.  Training then starts at layer detach_at + 1.
+
+Feeding the device, the MI355X way:
+
+* ``HBMHiddenStore`` uploads the whole cache into HBM once (a cache of a few
+  GB is small next to 288 GB) through a pair of pinned staging buffers, so
+  ``get_hidden`` becomes a slice of a resident tensor;
+* otherwise ``get_hidden`` reads one sample from the memory map into a pinned
+  host buffer and copies it asynchronously; two staging buffers alternate,
+  each reused only after the device has finished reading it (an event per
+  buffer), so the host can fill sample i + 1 while sample i is in flight.
 """
 from __future__ import annotations
 
 import hashlib
 import json
 import os
-from typing import Callable, Optional
+import threading
+from typing import Callable, Optional, Union
 
 import numpy as np
 import torch
 
+_SIDECAR = ".json"
+
+
+def _ids_as_int32(ids) -> np.ndarray:
+    arr = ids.detach().cpu().numpy() if isinstance(ids, torch.Tensor) else np.asarray(ids)
+    return np.ascontiguousarray(arr, dtype=np.int32)
+
 
 def dataset_fingerprint(samples, detach_at: int, src: str) -> str:
-    """frozen_cache.py:14-22: sha256 over (detach_at, src, int32 input ids), 16 hex digits."""
-    h = hashlib.sha256()
-    h.update(f"{detach_at}|{src}".encode())
-    for s in samples:
-        ids = s["input_ids"]
-        arr = ids.numpy() if hasattr(ids, "numpy") else np.asarray(ids)
-        h.update(np.asarray(arr, dtype=np.int32).tobytes())
-    return h.hexdigest()[:16]
+    """Cache key (format of usaf/frozen_cache.py:14-22): the first 16 hex digits
+    of sha256 over "<detach_at>|<src>" followed by every sample's input ids as
+    int32 bytes, in sample order."""
+    digest = hashlib.sha256(("%d|%s" % (detach_at, src)).encode())
+    for sample in samples:
+        digest.update(_ids_as_int32(sample["input_ids"]).tobytes())
+    return digest.hexdigest()[:16]
 
 
-def load_frozen_cache(samples, seq: int, hidden: int, detach_at: int, src: str, path: str) -> Optional[np.ndarray]:
-    """frozen_cache.py:25-39: read-only memmap when the fingerprint and shape match, else None."""
-    meta_path = path + ".json"
-    if not (os.path.exists(path) and os.path.exists(meta_path)):
-        return None
+def _read_sidecar(path: str) -> Optional[dict]:
     try:
-        with open(meta_path) as f:
+        with open(path + _SIDECAR) as f:
             meta = json.load(f)
     except (OSError, ValueError):
         return None
-    if (meta.get("fingerprint") != dataset_fingerprint(samples, detach_at, src) or meta.get("seq") != seq
-            or meta.get("hidden") != hidden or meta.get("N") != len(samples)):
+    return meta if isinstance(meta, dict) else None
+
+
+def _write_sidecar(path: str, meta: dict) -> None:
+    tmp = path + _SIDECAR + ".tmp"
+    with open(tmp, "w") as f:
+        json.dump(meta, f)
+    os.replace(tmp, path + _SIDECAR)  # readers never see a half-written sidecar
+
+
+def load_frozen_cache(samples, seq: int, hidden: int, detach_at: int, src: str, path: str) -> Optional[np.ndarray]:
+    """usaf/frozen_cache.py:25-39: the cache as a read-only memory map if its
+    sidecar matches (fingerprint, N, seq, hidden), else None."""
+    meta = _read_sidecar(path)
+    if meta is None or not os.path.exists(path):
+        return None
+    expected = {"fingerprint": dataset_fingerprint(samples, detach_at, src), "N": len(samples), "seq": seq,
+                "hidden": hidden}
+    if any(meta.get(key) != value for key, value in expected.items()):
         return None
     return np.lib.format.open_memmap(path, mode="r")
 
 
 def build_frozen_cache(samples, seq: int, hidden: int, detach_at: int, src: str,
                        compute_hidden: Callable[[dict], torch.Tensor], path: str, verbose: bool = True) -> np.ndarray:
-    """frozen_cache.py:42-67: build (or reuse) the [N, seq, hidden] fp16 cache."""
-    existing = load_frozen_cache(samples, seq, hidden, detach_at, src, path)
-    if existing is not None:
+    """usaf/frozen_cache.py:42-67: reuse a matching cache, else compute every
+    sample's hidden state (``compute_hidden(sample) -> [seq, hidden]``) into a
+    new fp16 memory map and write the sidecar last (a build that dies midway
+    leaves no sidecar, so it is never mistaken for a complete cache)."""
+    found = load_frozen_cache(samples, seq, hidden, detach_at, src, path)
+    if found is not None:
         if verbose:
-            print(f"  frozen cache: reusing {path} {existing.shape}")
-        return existing
-    os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
-    n = len(samples)
-    arr = np.lib.format.open_memmap(path, mode="w+", dtype=np.float16, shape=(n, seq, hidden))
-    for i, s in enumerate(samples):
-        with torch.no_grad():
-            h = compute_hidden(s)
-        arr[i] = h.reshape(seq, hidden).detach().to("cpu", torch.float16).numpy()
-        if verbose and (i % 25 == 0 or i == n - 1):
-            print(f"  frozen cache build {i + 1}/{n}")
-    arr.flush()
-    with open(path + ".json", "w") as f:
-        json.dump({"fingerprint": dataset_fingerprint(samples, detach_at, src), "N": n, "seq": seq,
-                   "hidden": hidden, "detach_at": detach_at}, f)
+            print(f"  frozen cache: reusing {path} {tuple(found.shape)}")
+        return found
+    parent = os.path.dirname(path)
+    if parent:
+        os.makedirs(parent, exist_ok=True)
+    if os.path.exists(path + _SIDECAR):
+        os.remove(path + _SIDECAR)
+    total = len(samples)
+    out = np.lib.format.open_memmap(path, mode="w+", dtype=np.float16, shape=(total, seq, hidden))
+    report_every = max(1, total // 10)
+    with torch.no_grad():
+        for row, sample in enumerate(samples):
+            h = compute_hidden(sample)
+            out[row] = h.detach().reshape(seq, hidden).to(device="cpu", dtype=torch.float16).numpy()
+            if verbose and ((row + 1) % report_every == 0 or row + 1 == total):
+                print(f"  frozen cache: {row + 1}/{total} samples")
+    out.flush()
+    _write_sidecar(path, {"fingerprint": dataset_fingerprint(samples, detach_at, src), "N": total, "seq": seq,
+                          "hidden": hidden, "detach_at": detach_at})
     if verbose:
-        print(f"  frozen cache: saved {path} {arr.shape} ({arr.nbytes / 1e9:.2f}GB)")
-    return arr
+        print(f"  frozen cache: wrote {path} {tuple(out.shape)} ({out.nbytes / 1e9:.2f} GB)")
+    return out
 
 
-def get_hidden(cache: np.ndarray, idx: int, device, dtype=torch.float16) -> torch.Tensor:
-    """frozen_cache.py:70-74: sample ``idx`` as [1, seq, hidden] on ``device``."""
-    host = torch.from_numpy(np.array(cache[idx], copy=True))
+class _PinnedRing:
+    """Two pinned host buffers for one sample shape, used alternately.  A buffer
+    is refilled only after the copy that last read it has completed."""
+
+    def __init__(self, shape, np_dtype) -> None:
+        self.shape = tuple(shape)
+        self.np_dtype = np.dtype(np_dtype)
+        t_dtype = torch.from_numpy(np.zeros(1, dtype=self.np_dtype)).dtype
+        self.bufs = [torch.empty(self.shape, dtype=t_dtype, pin_memory=True) for _ in range(2)]
+        self.done = [None, None]
+        self.turn = 0
+        self.lock = threading.Lock()
+
+    def stage(self, src: np.ndarray, device: torch.device, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Copy ``src`` through the next buffer into ``out`` (a new device tensor
+        if None) and return it; the copy is enqueued on the current stream of
+        ``device``."""
+        with self.lock:
+            i = self.turn
+            self.turn ^= 1
+            if self.done[i] is not None:
+                self.done[i].synchronize()
+            host = self.bufs[i]
+            host.numpy()[...] = src
+            if out is None:
+                dev = host.to(device, non_blocking=True)
+            else:
+                dev = out.copy_(host, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(device))
+            self.done[i] = ev
+        return dev
+
+
+_rings: dict = {}
+_rings_lock = threading.Lock()
+
+
+def _ring_for(shape, np_dtype, device: torch.device) -> _PinnedRing:
+    key = (tuple(shape), np.dtype(np_dtype).str, device.index)
+    with _rings_lock:
+        ring = _rings.get(key)
+        if ring is None:
+            ring = _rings[key] = _PinnedRing(shape, np_dtype)
+    return ring
+
+
+class HBMHiddenStore:
+    """The whole frozen cache resident in device memory ([N, seq, hidden], fp16
+    as on disk), uploaded in slabs through the pinned staging ring.  Pass it to
+    ``get_hidden`` in place of the memory map."""
+
+    def __init__(self, cache: np.ndarray, device, slab_bytes: int = 64 << 20) -> None:
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError("HBMHiddenStore keeps the cache in GPU memory; pass a cuda device")
+        n = int(cache.shape[0])
+        per = int(np.prod(cache.shape[1:])) * cache.dtype.itemsize
+        rows = max(1, min(n, slab_bytes // max(per, 1)))
+        self.data = torch.empty(tuple(cache.shape), dtype=torch.float16, device=dev)
+        for r0 in range(0, n, rows):
+            r1 = min(n, r0 + rows)
+            ring = _ring_for((r1 - r0,) + tuple(cache.shape[1:]), cache.dtype, dev)
+            ring.stage(cache[r0:r1], dev, out=self.data[r0:r1])
+        self.shape = tuple(cache.shape)
+
+    def __len__(self) -> int:
+        return self.shape[0]
+
+    def nbytes(self) -> int:
+        return self.data.numel() * self.data.element_size()
+
+
+def get_hidden(cache: Union[np.ndarray, HBMHiddenStore], idx: int, device, dtype=torch.float16) -> torch.Tensor:
+    """usaf/frozen_cache.py:70-74: sample ``idx`` as [1, seq, hidden] in ``dtype``
+    on ``device``.  From an HBMHiddenStore: a slice of the resident cache (a
+    copy only when ``dtype`` differs).  From a memory map onto a GPU: staged
+    through a pinned buffer and copied asynchronously on the current stream.
+    A CPU target gets an independent host copy."""
     dev = torch.device(device)
-    if dev.type == "cuda":
-        host = host.pin_memory()
-    return host.to(device=dev, dtype=dtype, non_blocking=dev.type == "cuda").unsqueeze(0)
+    if isinstance(cache, HBMHiddenStore):
+        row = cache.data[idx]
+        if row.device != dev:
+            row = row.to(dev)
+        return row.to(dtype).unsqueeze(0)
+    src = cache[idx]
+    if dev.type != "cuda":
+        return torch.from_numpy(np.array(src, copy=True)).to(dtype).unsqueeze(0)
+    staged = _ring_for(src.shape, src.dtype, dev).stage(src, dev)
+    return staged.to(dtype).unsqueeze(0)

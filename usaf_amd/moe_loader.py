@@ -14,6 +14,7 @@ Drop-in for usaf/moe_loader.py.  Differences of placement, not of interface:
 from __future__ import annotations
 
 import fnmatch
+import functools
 from collections import OrderedDict
 from typing import Any, Dict, List, Optional, Tuple, Union
 
@@ -22,6 +23,7 @@ import torch.nn as nn
 
 from . import _native as N
 from .moe import Q4Tensor
+from .olmoe_streaming import _record_grad, apply_captured_expert_grads  # noqa: F401  (moe_loader.py:778-802)
 from .quantization import dequantize_4bit
 
 
@@ -480,68 +482,48 @@ class TopKImportanceStore:
         return sum(len(d) for d in self._vals.values())
 
 
-def _move_module_tensors_to(module: nn.Module, target: torch.device) -> None:
-    for pname, p in list(module._parameters.items()):
-        if p is None or p.device == target:
-            continue
-        new = torch.nn.Parameter(p.detach().to(target), requires_grad=p.requires_grad)
-        if p.grad is not None:
-            new.grad = p.grad.to(target)
-        module._parameters[pname] = new
-    for bname, b in list(module._buffers.items()):
-        if b is None or b.device == target:
-            continue
-        module._buffers[bname] = b.to(target)
-
-
 def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], device: torch.device, *,
                               max_cached_experts: int = 2, group_size: int = 128,
                               expert_pattern: str = "*.mlp.experts", verbose: bool = True,
                               fused: bool = True) -> nn.Module:
-    """moe_loader.py:650-769.  Non-expert params go to the GPU; expert modules get
-    a pre-hook that attaches their HBM 4-bit tensors (``module._usaf_q4``, read
-    by the fused forward) -- or, with ``fused=False``, dequantized fp16
-    Parameters from the LRU as the reference does -- and a post-hook that
-    detaches them again."""
+    """moe_loader.py:650-769.  The expert modules lose their Parameters (their
+    weights live in the cache's HBM 4-bit store); everything else moves to the
+    GPU in place.  Each expert module gets a pre-hook that attaches its HBM 4-bit
+    tensors (``module._usaf_q4``, read by the fused forward) -- or, with
+    ``fused=False``, dequantized fp16 Parameters from the LRU as the reference
+    does, their gradients captured into ``model._expert_grads`` -- and a
+    post-hook that detaches them again."""
     cache = QuantizedExpertCache(quantized_dict, device=device, max_cached=max_cached_experts,
                                  group_size=group_size)
-    expert_names: List[str] = []
-    n_gpu = bytes_gpu = 0
-    for mname, mod in model.named_modules():
-        if fnmatch.fnmatch(mname, expert_pattern):
-            expert_names.append(mname)
+    expert_names = [name for name, _ in model.named_modules() if fnmatch.fnmatch(name, expert_pattern)]
+    experts = set(expert_names)
+    for name, mod in model.named_modules():
+        if name in experts:
             mod._parameters.clear()
-            continue
-        for p in mod._parameters.values():
-            if p is not None:
-                n_gpu += 1
-                bytes_gpu += p.numel() * p.element_size()
-        _move_module_tensors_to(mod, torch.device(device))
+    resident = [p for p in model.parameters()]
+    model.to(device)
     if verbose:
-        print(f"  GPU (resident): {n_gpu} tensors, {bytes_gpu / 1e9:.2f}GB")
+        nbytes = sum(p.numel() * p.element_size() for p in resident)
+        print(f"  GPU (resident): {len(resident)} tensors, {nbytes / 1e9:.2f}GB")
         print(f"  HBM (4-bit):    {len(quantized_dict)} entries, ~{cache.estimate_cpu_mb() / 1024:.2f}GiB")
     state: Dict[str, int] = {"resident": 0, "max": 0}
-    model._expert_grads = {}
-    grad_store = model._expert_grads
+    grads: Dict[str, torch.Tensor] = {}
+    model._expert_grads = grads
 
-    def make_pre_hook(mod_name: str):
+    def attach(mod_name: str):
         def pre_hook(module: nn.Module, _args) -> None:
             if fused:
                 module._usaf_q4 = cache.get_q4(mod_name)
             else:
                 for pname, param in cache.get_expert_weights(mod_name).items():
                     module._parameters[pname] = param
-                    full = f"{mod_name}.{pname}"
-
-                    def _cap(p, _full=full):
-                        if p.grad is not None:
-                            grad_store[_full] = p.grad.detach()
-                    param.register_post_accumulate_grad_hook(_cap)
+                    param.register_post_accumulate_grad_hook(
+                        functools.partial(_record_grad, grads, f"{mod_name}.{pname}"))
             state["resident"] += 1
             state["max"] = max(state["max"], state["resident"])
         return pre_hook
 
-    def post_hook(module: nn.Module, _args, output):
+    def detach(module: nn.Module, _args, output):
         module._parameters.clear()
         module._usaf_q4 = None
         state["resident"] -= 1
@@ -549,31 +531,15 @@ def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], 
 
     model._stream_state = state
     for name, mod in model.named_modules():
-        if name in expert_names:
-            mod.register_forward_pre_hook(make_pre_hook(name))
-            mod.register_forward_hook(post_hook)
+        if name in experts:
+            mod.register_forward_pre_hook(attach(name))
+            mod.register_forward_hook(detach)
     model._quantized_cache = cache
     return model
 
 
 def get_quantized_cache(model: nn.Module) -> Optional[QuantizedExpertCache]:
     return getattr(model, "_quantized_cache", None)
-
-
-def apply_captured_expert_grads(model: nn.Module, scale: float = 1.0) -> int:
-    """moe_loader.py:778-802: captured expert grads -> canonical Parameters."""
-    store: Dict[str, torch.Tensor] = getattr(model, "_expert_grads", {})
-    if not store:
-        return 0
-    params = dict(model.named_parameters())
-    applied = 0
-    for full, g in store.items():
-        p = params.get(full)
-        if p is not None:
-            p.grad = (g.detach().float() * scale).to(device=p.device, dtype=p.dtype)
-            applied += 1
-    store.clear()
-    return applied
 
 
 def load_and_stream(model: nn.Module, quantized_path: str, device: torch.device, **stream_kwargs: Any) -> nn.Module:
