@@ -383,6 +383,196 @@ def bench_moe_kernels(L, reps: int) -> None:
                dx.data_ptr(), st)
 
 
+MIXTRAL = dict(E=8, H=4096, I=14336, k=2, T=8192)
+
+
+def bench_mixtral(dev, steps: int, warmup: int) -> dict:
+    """one Mixtral-8x7B-shaped MoE layer (H 4096, I 14336, 8 experts,
+    top-2, 8192 bf16 tokens, 4-bit SwiGLU experts): router + fused 4-bit
+    forward + backward (grad-input through the transposed 4-bit copies, router
+    backward), no weight gradients.  Per-kernel averages come from HIP events
+    around the fused-GEMM launches in a second pass of the same steps."""
+    from usaf_amd import moe as G
+    E, H, I, k, T = (MIXTRAL[n] for n in ("E", "H", "I", "k", "T"))
+    gen = torch.Generator(device=dev).manual_seed(4321)
+    q = {}
+    for name, shp in (("gate_up", (E, 2 * I, H)), ("down", (E, H, I))):
+        w = (torch.randn(shp, device=dev, generator=gen) * 0.02).half()
+        q[name] = G.Q4Tensor.quantize(w)
+        del w
+    ew = G.ExpertWeights(q["gate_up"], q["down"])
+    q["gate_up"].transposed()
+    q["down"].transposed()
+    hs = torch.randn(T, H, device=dev, generator=gen).bfloat16().requires_grad_(True)
+    wr = (torch.randn(E, H, device=dev, generator=gen) / H ** 0.5).bfloat16().requires_grad_(True)
+    dy = torch.randn(T, H, device=dev, generator=gen).bfloat16()
+    ovf = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step():
+        hs.grad = None
+        wr.grad = None
+        out = G.moe_block(hs, wr, k, False, ew, overflow=ovf)
+        out.backward(dy)
+
+    for _ in range(warmup):
+        step()
+    with _Timer() as t:
+        for _ in range(steps):
+            step()
+    ms = t.ms / steps
+    G.launch_events = {}
+    try:
+        with _Timer():
+            for _ in range(steps):
+                step()
+    finally:
+        events, G.launch_events = G.launch_events, None
+    if int(ovf.item()):
+        raise RuntimeError("mixtral bench: routing overflowed the static slot capacity")
+    with torch.no_grad():
+        logits = torch.nn.functional.linear(hs, wr)
+        w, _ = G.route_topk(logits, k, False, torch.bfloat16, with_probs=False)
+        S = G.bucket_by_expert(w).n_slots
+    names = {"gate_up_fwd": "usaf_hip_moe_gate_up_fwd", "down_fwd": "usaf_hip_moe_down_fwd",
+             "down_bwd": "usaf_hip_moe_down_bwd_t", "gate_up_bwd": "usaf_hip_moe_gate_up_bwd_t"}
+    flops = {"gate_up_fwd": 2 * S * H * 2 * I, "down_fwd": 2 * S * I * H, "down_bwd": 2 * S * H * I,
+             "gate_up_bwd": 2 * S * 2 * I * H}
+    kern = {}
+    for key, entry in names.items():
+        ev = events.get(entry, [])
+        kms = sum(a.elapsed_time(b) for a, b in ev) / max(1, len(ev))
+        kern[key] = dict(ms=round(kms, 4), tflops=round(flops[key] / (kms * 1e-3) / 1e12, 1),
+                         frac=round(flops[key] / (kms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                         flop_per_launch=flops[key], launches=len(ev))
+    total = sum(flops.values()) + 2 * T * H * E * 3
+    dom = max(kern, key=lambda n: kern[n]["ms"])
+    return dict(workload="Mixtral-8x7B-shaped MoE layer fwd+bwd (configs[3]): 8192 tokens, hidden 4096, "
+                         "intermediate 14336, 8 experts, top-2, 4-bit SwiGLU experts, bf16; grad-input only",
+                ms_per_step=round(ms, 4), tokens_per_s=round(T / (ms * 1e-3), 1), slots=S,
+                algorithmic_gflop_per_step=round(total / 1e9, 1),
+                step_tflops=round(total / (ms * 1e-3) / 1e12, 1), kernels=kern,
+                roofline={"bound": "mfma", "kernel": dom, "achieved": kern[dom]["tflops"],
+                          "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": kern[dom]["frac"]})
+
+
+def cpu_baseline_mixtral(max_seconds: float = 15.0) -> dict:
+    """The reference's routed expert loop (oracle/moe.py, torch CPU bf16
+    autograd, all host cores) at the Mixtral shape on a bounded token sample."""
+    from oracle import moe as M
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(4321)
+    E, H, I, k, T = 8, 4096, 14336, 2, 64
+    wg = (torch.randn(E, 2 * I, H, generator=g) * 0.02).bfloat16()
+    wd = (torch.randn(E, H, I, generator=g) * 0.02).bfloat16()
+    hs = torch.randn(T, H, generator=g).bfloat16()
+    w, _, _ = M.route(torch.randn(T, E, generator=g), k, False, torch.bfloat16)
+    dout = torch.randn(T, H, generator=g).bfloat16()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        M.experts_routed_autograd(hs, w, wg, wd, dout)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt > max_seconds or reps >= 10:
+            break
+    return dict(value=round(reps * T / dt, 2), unit="tokens/s", cores=threads, kind="port",
+                sample=f"routed per-expert loop (torch CPU bf16 autograd: fwd + grad-input + dense expert weight "
+                       f"grads) at the Mixtral shape on {T} of the 8192 tokens, x{reps} reps in {dt:.1f} s")
+
+
+CFG4 = dict(L=48, E=128, H=2048, I=768, k=8, T=2048, cap_bytes=64 * 10 ** 9, zipf=1.1)
+
+
+def zipf_router_logits(T, E, rank_of, s, gen):
+    """Router logits whose top-k draws experts without replacement with
+    probability proportional to Zipf(s) popularity (Gumbel top-k); rank_of[e]
+    is expert e's popularity rank (1 = most popular)."""
+    u = torch.rand(T, E, device=rank_of.device, generator=gen).clamp_(1e-12, 1 - 1e-7)
+    return -s * torch.log(rank_of.float()) - torch.log(-torch.log(u))
+
+
+def bench_cache_stress(dev, microbatches: int = 6) -> dict:
+    """48 Qwen3-MoE-shaped layers of 4-bit experts resident in HBM
+    (15.4 GB), a per-expert LRU of dequantized bf16 copies in a slot arena capped
+    at 64 GB, Zipf(1.1) expert popularity per layer, 2048-token microbatches
+    through the 48 layers (routing, cache lookup and fill, arena GEMMs,
+    combine, residual add).  The first microbatch starts from an empty cache
+    (cold fill: every expert dequantized once); the later ones hit only.  The
+    same microbatches also run through the fused 4-bit GEMMs, which need no
+    copies at all."""
+    from usaf_amd import moe as G
+    from usaf_amd.expert_cache import ExpertSlotCache
+    c = CFG4
+    L, E, H, I, k, T = c["L"], c["E"], c["H"], c["I"], c["k"], c["T"]
+    gen = torch.Generator(device=dev).manual_seed(4848)
+    layers, ranks = {}, {}
+    for li in range(L):
+        qs = []
+        for shp in ((E, 2 * I, H), (E, H, I)):
+            w = (torch.randn(shp, device=dev, generator=gen) * 0.02).half()
+            qs.append(G.Q4Tensor.quantize(w))
+            del w
+        name = f"model.layers.{li}.mlp.experts"
+        layers[name] = G.ExpertWeights(*qs)
+        ranks[name] = torch.randperm(E, device=dev, generator=gen) + 1
+    q4_bytes = sum(ew.gate_up.nbytes() + ew.down.nbytes() for ew in layers.values())
+    cache = ExpertSlotCache(layers, dev, max_bytes=c["cap_bytes"], dtype=torch.bfloat16)
+    names = list(layers)
+    logits = [[zipf_router_logits(T, E, ranks[n], c["zipf"], gen) for n in names] for _ in range(microbatches)]
+    hs0 = torch.randn(T, H, device=dev, generator=gen).bfloat16()
+
+    def run(mb, fused):
+        x = hs0
+        for li, name in enumerate(names):
+            w, _ = G.route_topk(logits[mb][li], k, False, torch.bfloat16, with_probs=False)
+            if fused:
+                y = G.routed_experts(x, w, layers[name], slot_capacity=T * (k + 1),
+                                     overflow=torch.zeros(1, dtype=torch.int32, device=dev))
+            else:
+                y = cache.forward(name, x, w, k)
+            x = x + y
+        return x
+
+    cache.dequant_events = []
+    with _Timer() as t:
+        run(0, fused=False)
+    cold_ms = t.ms
+    fill_ms = sum(a.elapsed_time(b) for a, b, _ in cache.dequant_events)
+    filled = sum(n for _, _, n in cache.dequant_events)
+    fill_bytes = cache.dequant_bytes
+    cache.dequant_events = None
+    h0, m0 = cache.hits, cache.misses
+    with _Timer() as t:
+        for mb in range(1, microbatches):
+            run(mb, fused=False)
+    steady_ms = t.ms / (microbatches - 1)
+    steady_hits, steady_misses = cache.hits - h0, cache.misses - m0
+    run(0, fused=True)
+    with _Timer() as t:
+        for mb in range(1, microbatches):
+            run(mb, fused=True)
+    fused_ms = t.ms / (microbatches - 1)
+    fill_gbs = fill_bytes / (fill_ms * 1e-3) / 1e9 if fill_ms > 0 else None
+    flop_per_mb = 2 * T * k * (H * 2 * I + I * H) * L
+    return dict(
+        workload="48 stacked Qwen3-30B-A3B MoE layers (configs[4]): 4-bit experts resident in HBM, per-expert LRU "
+                 "of bf16 copies capped at 64 GB, Zipf(1.1) expert popularity, 2048-token microbatches, forward",
+        layers=L, q4_resident_gb=round(q4_bytes / 1e9, 2), arena_slots=cache.n_slots,
+        arena_gb=round(cache.nbytes() / 1e9, 2), microbatches=microbatches,
+        cold_fill={"ms_per_microbatch": round(cold_ms, 3), "tokens_per_s": round(T / (cold_ms * 1e-3), 1),
+                   "experts_filled": filled, "dequant_ms": round(fill_ms, 3),
+                   "dequant_roofline": {"bound": "hbm", "achieved": None if fill_gbs is None else round(fill_gbs, 1),
+                                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                        "frac": None if fill_gbs is None else round(fill_gbs / HBM_PEAK_GBS, 4),
+                                        "bytes": fill_bytes}},
+        steady={"ms_per_microbatch": round(steady_ms, 3), "tokens_per_s": round(T / (steady_ms * 1e-3), 1),
+                "hit_rate": round(steady_hits / max(1, steady_hits + steady_misses), 4),
+                "tflops": round(flop_per_mb / (steady_ms * 1e-3) / 1e12, 1)},
+        fused_q4_no_copies={"ms_per_microbatch": round(fused_ms, 3), "tokens_per_s": round(T / (fused_ms * 1e-3), 1),
+                            "tflops": round(flop_per_mb / (fused_ms * 1e-3) / 1e12, 1)},
+        hits=cache.hits, misses=cache.misses, evictions=cache.evictions)
+
+
 def cpu_baseline_moe(max_seconds: float = 20.0) -> dict:
     """The reference's routed expert layer fwd+bwd (oracle/moe.py, torch CPU
     autograd in bf16, all host cores) on a bounded sample of tokens."""
@@ -474,6 +664,18 @@ def main() -> int:
     _log("dequant: one Qwen3 MoE layer (603,979,776 elements) -> bf16")
     dq = bench_dequant(dev, args.steps, args.warmup)
     _log(f"dequant: {dq['ms_per_launch']:.3f} ms/launch, {dq['gbs']:.1f} GB/s")
+    _log("mixtral: configs[3] layer fwd+bwd, 8192 tokens")
+    mx = bench_mixtral(dev, max(5, args.steps // 5), max(2, args.warmup // 5))
+    _log(f"mixtral: {mx['ms_per_step']:.3f} ms/step, {mx['tokens_per_s']:.0f} tokens/s, "
+         f"{mx['step_tflops']:.1f} TFLOP/s algorithmic")
+    for name, kv in mx["kernels"].items():
+        _log(f"  {name}: {kv['ms']:.3f} ms, {kv['tflops']:.1f} TFLOP/s ({100 * kv['frac']:.1f} % of peak)")
+    _log("cache stress: configs[4], 48 layers, 64 GB per-expert LRU, Zipf(1.1), 2048-token microbatches")
+    cs = bench_cache_stress(dev)
+    _log(f"cache stress: cold fill {cs['cold_fill']['ms_per_microbatch']:.2f} ms/microbatch "
+         f"({cs['cold_fill']['experts_filled']} experts, dequant {cs['cold_fill']['dequant_roofline']['achieved']} GB/s), "
+         f"steady {cs['steady']['ms_per_microbatch']:.2f} ms ({cs['steady']['tokens_per_s']:.0f} tokens/s, hit rate "
+         f"{cs['steady']['hit_rate']}), fused 4-bit {cs['fused_q4_no_copies']['ms_per_microbatch']:.2f} ms")
     cpu = cpu_dq = None
     if not args.no_cpu_baseline:
         _log("cpu baseline: routed expert layer fwd+bwd sample")
@@ -481,6 +683,8 @@ def main() -> int:
         _log(f"cpu baseline: {cpu['value']} tokens/s on {cpu['cores']} threads")
         cpu_dq = cpu_baseline_dequant()
         _log(f"cpu baseline dequant: {cpu_dq['value']} GB/s")
+        mx["cpu_baseline"] = cpu_baseline_mixtral()
+        _log(f"cpu baseline mixtral: {mx['cpu_baseline']['value']} tokens/s")
 
     kern = {n: v for n, v in mo["kernels"].items() if isinstance(v, dict)}
     dom = max(kern, key=lambda n: kern[n]["ms"])
@@ -519,6 +723,8 @@ def main() -> int:
                                  "traffic": traffic.get("dequant")},
                     "cpu_baseline": cpu_dq},
         "cpu_baseline": cpu,
+        "mixtral": mx,
+        "cache_stress": cs,
     }
     print(json.dumps(line), flush=True)
     return 0

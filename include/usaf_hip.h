@@ -73,6 +73,34 @@ int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f16, const u
                         void* out, int32_t out_dtype, void* stream);
 
 /*
+ * Dequantized values at flat positions, without the whole tensor:
+ *   out[j] = fp32( fp16(fp16(q_i * scale) + zero) ),  i = idx[j]
+ * with q_i, scale, zero as usaf_hip_dequant_q4 takes them for element i; this
+ * is the reference's dequantize_4bit(...).reshape(-1)[idx].float(), the
+ * master values of newly active positions (train.py:456-465, :589-595).
+ * Positions outside [0, numel) give NaN and set *bad_flag = 1 (bad_flag may be NULL).
+ */
+int usaf_hip_dequant_q4_at(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
+                           int64_t n_groups, int64_t packed_cols, int64_t group_size, int64_t numel,
+                           const int64_t* idx, int64_t n, float* out, int32_t* bad_flag, void* stream);
+
+/*
+ * Batched dequant of whole slices into slots of an arena (the per-expert cache
+ * of dequantized copies, filled on demand as moe_loader.py:183-224 fills its
+ * LRU): job j writes the dequant (as usaf_hip_dequant_q4, out_dtype) of elements
+ * [src_slice[j] * slice_elems, +slice_elems) of the flat 4-bit tensor into
+ * elements [dst_slice[j] * slice_elems, +slice_elems) of `out`.  Group size 128
+ * (64 code bytes per group), slice_elems % 2048 == 0, codes 4-byte and out
+ * 16-byte aligned; src_slice / dst_slice int64 [n_jobs] on the device; `out`
+ * holds n_dst_slices slices.  Jobs naming a slice outside the tensor
+ * (n_groups * 128 / slice_elems slices) or the arena are skipped.
+ */
+int usaf_hip_dequant_q4_slices(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
+                               int64_t n_groups, int64_t slice_elems, int64_t n_jobs, const int64_t* src_slice,
+                               const int64_t* dst_slice, int64_t n_dst_slices, void* out, int32_t out_dtype,
+                               void* stream);
+
+/*
  * 4-bit group quantization.
  * Replaces usaf/quantization.py:21-85 `quantize_4bit`.
  *   x       fp32 / fp16 / bf16 [numel]  (flattened tensor)
@@ -227,6 +255,21 @@ int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* offsets, in
                           const int8_t* wq, const uint32_t* wsz, const void* w16, int32_t dtype, void* y,
                           void* stream);
 
+/* usaf_hip_moe_gate_up_fwd / usaf_hip_moe_down_fwd with dense weights held in a
+ * slot arena (dequantized expert copies of usaf_amd's per-expert cache, the
+ * on-demand fp16 copies of moe_loader.py:130-181): expert e's weight is block
+ * slot_of[e] of arena [n_slots, 2I, H] (gate_up) or [n_slots, H, I] (down), in
+ * the activation dtype.  slot_of int32 [E] on the device; entries outside
+ * [0, n_slots) are clamped (wrong weights, never an access outside the arena).
+ * Same shape requirements as the non-arena calls. */
+int usaf_hip_moe_gate_up_fwd_slots(const void* x, int64_t T, int64_t H, const int32_t* token_idx,
+                                   const int32_t* offsets, int64_t S, int64_t E, int64_t I, const void* arena,
+                                   const int32_t* slot_of, int64_t n_slots, int32_t dtype, void* gu, void* act,
+                                   void* stream);
+int usaf_hip_moe_down_fwd_slots(const void* act, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
+                                const void* arena, const int32_t* slot_of, int64_t n_slots, int32_t dtype, void* y,
+                                void* stream);
+
 /* Autograd of qwen3moe_dml.py:60-61: dact = dcur @ W_down[e] through the SwiGLU
  * (saved gu) -> dgu [S, 2I] (gate half, up half).  Needs I % 128 == 0, H % 64 == 0. */
 int usaf_hip_moe_down_bwd(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S, int64_t E,
@@ -320,6 +363,21 @@ int usaf_hip_gather_transpose(const void* in, int64_t ld_in, const int32_t* rows
 int usaf_hip_sddmm_masked(const void* rowT, const void* colT, int64_t ldT, const int32_t* offsets, int64_t E,
                           int64_t R, int64_t C, int64_t n_pos, const int32_t* row_code, const int32_t* col_idx,
                           const int64_t* pos_map, int32_t dtype, float* compact, void* stream);
+
+/*
+ * Positions of the k largest magnitudes |x[i]| among n values (fp32, fp16 or
+ * bf16; NaN ranks above +inf, as torch.topk ranks it): pos int64 [min(k, n)] in
+ * ascending position order, ties at the k-th largest magnitude taken from the
+ * lowest positions; vals fp32 [min(k, n)] = |x[pos]| (may be NULL).  The same
+ * set as torch.topk(x.abs(), k) whenever the k-th and (k+1)-th magnitudes
+ * differ.  Replaces the selections of usaf/moe_loader.py:584-631
+ * (TopKImportanceStore.add: per-expert top |grad| candidates; .select: global
+ * top-k over the candidates).  n < 2^31; workspace int32
+ * [usaf_hip_topk_abs_ws_ints(n)]; nothing is read back to the host.
+ */
+int64_t usaf_hip_topk_abs_ws_ints(int64_t n);
+int usaf_hip_topk_abs(const void* x, int32_t dtype, int64_t n, int64_t k, int64_t* pos, float* vals,
+                      int32_t* workspace, void* stream);
 
 /*
  * One SparseAdam step on compact fp32 vectors (usaf/sparse_optim.py:94-130,

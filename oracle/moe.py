@@ -214,3 +214,48 @@ def experts_routed_manual(hs, weights, w_gate_up, w_down, dout, active=None):
         sampled("gate_up_proj", ei, dgu, x)
         dhs.index_add_(0, idx, dx)
     return final.to(dt), dhs.to(dt), dweights.to(dt), compact
+
+
+def topk_store_candidates(g: torch.Tensor, ei: int, frac: float, cand_mult: float = 2.0):
+    """TopKImportanceStore.add (usaf/moe_loader.py:605-611): expert ei's top
+    |g| candidates as (fp32 magnitudes, global flat indices)."""
+    flat = g.detach().float().reshape(-1).abs()
+    k = max(1, int(flat.numel() * frac * cand_mult))
+    v, i = torch.topk(flat, min(k, flat.numel()))
+    return v, i.to(torch.long) + int(ei) * flat.numel()
+
+
+def topk_store_select(cands, numel: int, frac: float) -> torch.Tensor:
+    """TopKImportanceStore.select (usaf/moe_loader.py:613-627) for one tensor:
+    ``cands`` = [(vals, idx) per expert in insertion order]."""
+    vals = torch.cat([c[0] for c in cands])
+    idxs = torch.cat([c[1] for c in cands])
+    k = min(max(1, int(numel * frac)), vals.numel())
+    return idxs[torch.topk(vals, k).indices]
+
+
+def reselect_merge(old_idx: torch.Tensor, old_masters: torch.Tensor, new_idx, dequant_flat: torch.Tensor):
+    """The reselect merge of train.py:556-597 for one tensor, with Python sets
+    as there: (final flat indices, fp32 masters).  ``dequant_flat`` is the
+    tensor's fp16 dequantized weights, flattened (:589-595)."""
+    if new_idx is None or new_idx.numel() == 0:                         # :560-563
+        return old_idx.clone(), old_masters.clone()
+    old_set = set(old_idx.reshape(-1).tolist())                          # :559
+    nw_set = set(new_idx.reshape(-1).tolist())                           # :564
+    kept = sorted(old_set & nw_set)                                      # :565
+    candidates = sorted(nw_set - old_set)                                # :566
+    fill = max(0, len(old_set) - len(kept))                              # :568
+    grown = candidates[:fill]                                            # :569
+    final = torch.tensor(kept + grown, dtype=torch.long)                 # :570
+    old_flat = old_idx.reshape(-1).to(torch.long)
+    keep_mask = torch.isin(final, old_flat)                              # :575
+    new_vals = torch.zeros(final.numel(), dtype=torch.float32)
+    kept_pos = keep_mask.nonzero(as_tuple=False).reshape(-1)
+    if kept_pos.numel() > 0:                                             # :582-588
+        all_idx = torch.zeros(int(old_flat.max().item()) + 1, dtype=torch.long)
+        all_idx[old_flat] = torch.arange(old_flat.numel(), dtype=torch.long)
+        new_vals[kept_pos] = old_masters.float()[all_idx[final[kept_pos]]]
+    grow_pos = (~keep_mask).nonzero(as_tuple=False).reshape(-1)
+    if grow_pos.numel() > 0:                                             # :590-596
+        new_vals[grow_pos] = dequant_flat.reshape(-1)[final[grow_pos]].float()
+    return final, new_vals

@@ -1,0 +1,95 @@
+"""configs[4] at reduced size: stacked 4-bit MoE layers resident in HBM, a
+per-expert LRU of dequantized copies smaller than the working set, Zipf(1.1)
+expert popularity (usaf_amd/expert_cache.py; reference semantics
+usaf/moe_loader.py:130-181).
+
+Checks, after every layer forward of every microbatch:
+* the cached keys and their LRU order equal the reference policy's
+  (oracle/cache.py LRUModel) fed the same accesses;
+* sampled cached copies are bit-exact with the C oracle's dequant of that
+  expert's 4-bit slices;
+* the layer's output from the arena GEMMs is within the bf16 bar of the
+  oracle's routed forward on the same dequantized weights.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import moe as M
+from oracle.cache import LRUModel
+from usaf_amd import moe as G
+from usaf_amd.expert_cache import ExpertSlotCache
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _zipf_logits(T, E, perm, s, g):
+    """Router logits whose top-k draws experts without replacement with
+    probability proportional to Zipf(s) popularity (Gumbel top-k)."""
+    rank = torch.empty(E)
+    rank[perm] = torch.arange(1, E + 1, dtype=torch.float32)
+    logp = -s * torch.log(rank)
+    u = torch.rand(T, E, generator=g).clamp_(1e-12, 1 - 1e-7)
+    return logp + (-torch.log(-torch.log(u)))
+
+
+def test_slot_cache_lru_copies_and_forward(gpu_device):
+    L, E, H, I, T, k = 6, 16, 256, 128, 256, 4
+    dt = torch.bfloat16
+    _say(f"slot cache: {L} layers x {E} experts (H={H}, I={I}), 40 slots, Zipf(1.1), T={T} k={k}")
+    g = torch.Generator().manual_seed(99)
+    layers, deq, perms = {}, {}, {}
+    for li in range(L):
+        name = f"model.layers.{li}.mlp.experts"
+        qg = G.Q4Tensor.quantize((torch.randn(E, 2 * I, H, generator=g) * 0.02).half().to(gpu_device))
+        qd = G.Q4Tensor.quantize((torch.randn(E, H, I, generator=g) * 0.02).half().to(gpu_device))
+        layers[name] = G.ExpertWeights(qg, qd)
+        deq[name] = tuple(torch.from_numpy(oracle.dequant(q.q.cpu().numpy(), q.s.cpu().numpy(), q.z.cpu().numpy(),
+                                                          q.numel(), out_dtype="bf16").view(np.int16).copy())
+                          .view(torch.bfloat16).reshape(tuple(q.shape)) for q in (qg, qd))
+        perms[name] = torch.randperm(E, generator=g)
+    slot_bytes = (2 * I * H + H * I) * 2
+    cache = ExpertSlotCache(layers, gpu_device, max_bytes=40 * slot_bytes, dtype=dt)
+    assert cache.n_slots == 40
+    model = LRUModel(40)
+    hs0 = torch.randn(T, H, generator=g).to(dt)
+    # layers 1 and 3 come back two layers later (32 keys < 40 slots: hits), the
+    # rest only once per microbatch (a cyclic walk an LRU this small never hits)
+    walk = [0, 1, 2, 1, 3, 4, 3, 5]
+    for mb in range(3):
+        x = hs0.clone()
+        for li in walk:
+            name = f"model.layers.{li}.mlp.experts"
+            w, _, _ = M.route(_zipf_logits(T, E, perms[name], 1.1, g), k, False, dt)
+            out = cache.forward(name, x.to(gpu_device), w.to(gpu_device), k)
+            torch.cuda.synchronize()
+            assert not cache.overflowed()
+            for e in range(E):
+                model.access((name, e))
+            assert cache.cached_keys == model.keys(), f"LRU order differs after mb {mb} layer {li}"
+            ref = M.experts_routed(x, w, deq[name][0], deq[name][1])
+            rel = float((out.float().cpu() - ref.float()).abs().max() / ref.float().abs().max())
+            assert rel <= 1e-2, f"mb {mb} layer {li}: rel {rel:.3e}"
+            # sampled copies, bit for bit
+            keys = cache.cached_keys
+            for j in torch.randint(0, len(keys), (3,), generator=g).tolist():
+                lname, e = keys[j]
+                s = cache.slot_of(lname, e)
+                assert torch.equal(cache.gu_arena[s].cpu().view(torch.int16), deq[lname][0][e].view(torch.int16))
+                assert torch.equal(cache.dn_arena[s].cpu().view(torch.int16), deq[lname][1][e].view(torch.int16))
+            x = (x.float() + ref.float()).to(dt)
+    assert cache.evictions > 0 and cache.hits > 0
+    _say(f"  hits {cache.hits}, misses {cache.misses}, evictions {cache.evictions}")
+
+
+def test_slot_cache_refuses_arena_below_one_layer(gpu_device):
+    E, H, I = 16, 256, 128
+    q = G.Q4Tensor.quantize((torch.randn(E, 2 * I, H) * 0.02).half().to(gpu_device))
+    d = G.Q4Tensor.quantize((torch.randn(E, H, I) * 0.02).half().to(gpu_device))
+    with pytest.raises(ValueError):
+        ExpertSlotCache({"l0": G.ExpertWeights(q, d)}, gpu_device, max_bytes=(2 * I * H + H * I) * 2 * (E - 1))

@@ -226,3 +226,54 @@ def test_manual_backward_matches_autograd(dtype):
     assert rel(dw_m[routed], dw_a[routed]) <= tol / 4
     assert rel(comp["gate_up_proj"], M.gather_compact(dwg_a, active["gate_up_proj"])) <= tol / 4
     assert rel(comp["down_proj"], M.gather_compact(dwd_a, active["down_proj"])) <= tol / 4
+
+
+def test_topk_store_oracle_against_full_sort():
+    # distinct magnitudes: the reference's topk selection equals a full sort's head
+    g = torch.Generator().manual_seed(5)
+    E, R, C, frac, cand = 3, 40, 50, 0.01, 2.0
+    grads = [((torch.randperm(R * C, generator=g).float() + 1) * (torch.randint(0, 2, (R * C,), generator=g) * 2 - 1))
+             .reshape(R, C) for _ in range(E)]
+    cands = []
+    for ei, gr in enumerate(grads):
+        v, i = M.topk_store_candidates(gr, ei, frac, cand)
+        k = max(1, int(R * C * frac * cand))
+        flat = gr.reshape(-1).abs()
+        order = torch.argsort(flat, descending=True)[:k]
+        assert set(i.tolist()) == set((order + ei * R * C).tolist())
+        assert torch.equal(v, flat[order])
+        cands.append((v, i))
+    sel = M.topk_store_select(cands, E * R * C, frac)
+    allv = torch.cat([c[0] for c in cands])
+    alli = torch.cat([c[1] for c in cands])
+    k = max(1, int(E * R * C * frac))
+    assert set(sel.tolist()) == set(alli[torch.argsort(allv, descending=True)[:k]].tolist())
+
+
+def test_reselect_merge_oracle_hand_example():
+    # old {5, 2, 9, 7}, new {9, 3, 1, 5, 8}: kept [5, 9]; newcomers [1, 3, 8];
+    # fill 4 - 2 = 2 -> grown [1, 3]; kept masters carried, grown from the weights
+    old = torch.tensor([5, 2, 9, 7])
+    masters = torch.tensor([0.5, 0.2, 0.9, 0.7])
+    new = torch.tensor([9, 3, 1, 5, 8])
+    deq = (torch.arange(12) * 10).half()
+    final, vals = M.reselect_merge(old, masters, new, deq)
+    assert final.tolist() == [5, 9, 1, 3]
+    assert vals.tolist() == [0.5, pytest.approx(0.9), 10.0, 30.0]
+    # an empty selection keeps the old set and masters
+    f2, v2 = M.reselect_merge(old, masters, torch.tensor([], dtype=torch.long), deq)
+    assert torch.equal(f2, old) and torch.equal(v2, masters)
+    # fewer newcomers than free slots: the set shrinks
+    f3, _ = M.reselect_merge(old, masters, torch.tensor([9, 11]), deq)
+    assert f3.tolist() == [9, 11]
+
+
+def test_lru_model_hand_sequence():
+    from oracle.cache import LRUModel
+    m = LRUModel(3)
+    trace = [m.access(k) for k in "abcabdaeb"]
+    # a b c miss; a b hit (order c a b); d misses and evicts c; a hits (b d a);
+    # e misses and evicts b (d a e); b misses and evicts d (a e b)
+    assert [h for h, _ in trace] == [False, False, False, True, True, False, True, False, False]
+    assert [ev for _, ev in trace] == [[], [], [], [], [], ["c"], [], ["b"], ["d"]]
+    assert m.keys() == ["a", "e", "b"]

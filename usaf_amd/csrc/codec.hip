@@ -76,23 +76,51 @@ __device__ __forceinline__ uint16_t dequant_one_f16(uint32_t q, uint16_t s_bits,
 // tile: one 32-bit code word in, one 128-bit store out, so every load and
 // store instruction of the wave touches one contiguous 256 B / 1 KiB span.
 // UNR tiles are loaded before any is converted to keep more bytes in flight.
-template <int OUT_DT, int UNR>
+// SLICES: the tiles come from a job list instead of one linear range.  Tile t
+// belongs to job j = t / tps (tps tiles per slice); it reads tile t % tps of
+// source slice src[j] and writes the same tile of destination slice dst[j]
+// (slices of tps * 2048 elements).  Jobs naming a slice outside
+// [0, n_src) / [0, n_dst) are skipped.
+template <int OUT_DT, int UNR, bool SLICES>
 __global__ __launch_bounds__(256) void dequant_g128_kernel(const uint32_t* __restrict__ packed,
                                                            const uint16_t* __restrict__ scale,
                                                            const uint16_t* __restrict__ zero,
-                                                           u32x4* __restrict__ out, int64_t n_tiles) {
+                                                           u32x4* __restrict__ out, int64_t n_tiles,
+                                                           const int64_t* __restrict__ src,
+                                                           const int64_t* __restrict__ dst, int64_t tps,
+                                                           int64_t n_src, int64_t n_dst) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  // first code word of a tile in the source and first output vector in the destination (-1: skip)
+  auto tile_src = [&](int64_t t) -> int64_t {
+    if constexpr (SLICES) {
+      const int64_t j = t / tps, s0 = src[j], d0 = dst[j];
+      if (s0 < 0 || s0 >= n_src || d0 < 0 || d0 >= n_dst) return -1;
+      return (s0 * tps + (t - j * tps)) * 256;
+    } else {
+      return t * 256;
+    }
+  };
+  auto tile_dst = [&](int64_t t) -> int64_t {
+    if constexpr (SLICES) {
+      const int64_t j = t / tps;
+      return (dst[j] * tps + (t - j * tps)) * 256;
+    } else {
+      return t * 256;
+    }
+  };
   for (int64_t t0 = wave * UNR; t0 < n_tiles; t0 += n_waves * UNR) {
     uint32_t w[UNR][4];
     uint16_t sb[UNR][4], zb[UNR][4];
+    int64_t us[UNR];
 #pragma unroll
     for (int r = 0; r < UNR; ++r) {
-      if (t0 + r < n_tiles) {
+      us[r] = t0 + r < n_tiles ? tile_src(t0 + r) : -1;
+      if (us[r] >= 0) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const int64_t u = (t0 + r) * 256 + lane + 64 * k;
+          const int64_t u = us[r] + lane + 64 * k;
           w[r][k] = __builtin_nontemporal_load(packed + u);
           sb[r][k] = scale[u >> 4];
           zb[r][k] = zero[u >> 4];
@@ -101,10 +129,11 @@ __global__ __launch_bounds__(256) void dequant_g128_kernel(const uint32_t* __res
     }
 #pragma unroll
     for (int r = 0; r < UNR; ++r) {
-      if (t0 + r < n_tiles) {
+      if (us[r] >= 0) {
+        const int64_t ud = tile_dst(t0 + r);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const int64_t u = (t0 + r) * 256 + lane + 64 * k;
+          const int64_t u = ud + lane + 64 * k;
           const f16 s = __builtin_bit_cast(f16, sb[r][k]);
           const f16 z = __builtin_bit_cast(f16, zb[r][k]);
           const f16x2 s2 = {s, s};
@@ -155,6 +184,32 @@ __global__ __launch_bounds__(256) void dequant_generic_kernel(const uint8_t* __r
     const uint16_t h = dequant_one_f16(q, scale[g], zero[g]);
     if constexpr (OUT_DT == USAF_F16) out[i] = h;
     else out[i] = f16bits_to_bf16bits(h);
+  }
+}
+
+// Dequantized values at a list of flat positions, fp32 of the fp16 result:
+// the reference's dequantize_4bit(...).reshape(-1)[idx].float() without the
+// full tensor (masters of new active positions, train.py:456-465, 589-595).
+// Element i takes nibble i of the flat code bytes and group i / eff_gs, as the
+// generic kernel; positions outside [0, numel) give NaN and set *bad.
+__global__ __launch_bounds__(256) void dequant_at_kernel(const uint8_t* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scale,
+                                                         const uint16_t* __restrict__ zero,
+                                                         const int64_t* __restrict__ idx, int64_t n, int64_t numel,
+                                                         int64_t eff_gs, float* __restrict__ out,
+                                                         int32_t* __restrict__ bad) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += stride) {
+    const int64_t i = idx[j];
+    if (i < 0 || i >= numel) {
+      out[j] = __builtin_nanf("");
+      if (bad) bad[0] = 1;
+      continue;
+    }
+    const uint32_t byte = packed[i >> 1];
+    const uint32_t q = (i & 1) ? (byte >> 4) : (byte & 0xFu);
+    const int64_t g = i / eff_gs;
+    out[j] = f16_bits_to_f32(dequant_one_f16(q, scale[g], zero[g]));
   }
 }
 
@@ -332,11 +387,11 @@ extern "C" int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f
       int64_t blocks = (n_tiles + 4 * UNR - 1) / (4 * UNR);  // 4 waves per block, UNR tiles per wave
       if (blocks > 65536) blocks = 65536;
       if (out_dtype == USAF_F16)
-        dequant_g128_kernel<USAF_F16, UNR><<<(unsigned)blocks, 256, 0, st>>>(
-            (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles);
+        dequant_g128_kernel<USAF_F16, UNR, false><<<(unsigned)blocks, 256, 0, st>>>(
+            (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles, nullptr, nullptr, 1, 0, 0);
       else
-        dequant_g128_kernel<USAF_BF16, UNR><<<(unsigned)blocks, 256, 0, st>>>(
-            (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles);
+        dequant_g128_kernel<USAF_BF16, UNR, false><<<(unsigned)blocks, 256, 0, st>>>(
+            (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles, nullptr, nullptr, 1, 0, 0);
       int rc = check_launch("dequant_q4");
       if (rc) return rc;
     }
@@ -353,6 +408,55 @@ extern "C" int usaf_hip_dequant_q4(const int8_t* packed, const uint16_t* scale_f
     return check_launch("dequant_q4");
   }
   return clear_error();
+}
+
+extern "C" int usaf_hip_dequant_q4_at(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
+                                      int64_t n_groups, int64_t packed_cols, int64_t group_size, int64_t numel,
+                                      const int64_t* idx, int64_t n, float* out, int32_t* bad_flag, void* stream) {
+  if (numel < 0 || n_groups < 0 || packed_cols < 0 || group_size <= 0 || n < 0)
+    return set_error(USAF_ERR_INVALID, "dequant_q4_at: negative size or non-positive group_size");
+  if (n == 0) return clear_error();
+  if (!packed || !scale_f16 || !zero_f16 || !idx || !out) return set_error(USAF_ERR_INVALID, "dequant_q4_at: null pointer");
+  const int64_t eff_gs = group_size < numel ? group_size : numel;
+  if (numel > 0 && (n_groups * eff_gs > 2 * n_groups * packed_cols || n_groups * eff_gs < numel))
+    return set_error(USAF_ERR_INVALID, "dequant_q4_at: %lld groups of %lld elements do not fit %lld elements",
+                     (long long)n_groups, (long long)eff_gs, (long long)numel);
+  dequant_at_kernel<<<launch_blocks(n, 256, 8), 256, 0, as_stream(stream)>>>(
+      (const uint8_t*)packed, scale_f16, zero_f16, idx, n, numel, eff_gs > 0 ? eff_gs : 1, out, bad_flag);
+  return check_launch("dequant_q4_at");
+}
+
+extern "C" int usaf_hip_dequant_q4_slices(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
+                                          int64_t n_groups, int64_t slice_elems, int64_t n_jobs,
+                                          const int64_t* src_slice, const int64_t* dst_slice, int64_t n_dst_slices,
+                                          void* out, int32_t out_dtype, void* stream) {
+  if (n_groups < 0 || slice_elems <= 0 || n_jobs < 0 || n_dst_slices < 0)
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices: bad sizes");
+  if (out_dtype != USAF_F16 && out_dtype != USAF_BF16)
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices: out_dtype must be fp16 or bf16");
+  if (slice_elems % 2048 != 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "dequant_q4_slices: slice_elems must be a multiple of 2048");
+  if (n_jobs == 0) return clear_error();
+  if (!packed || !scale_f16 || !zero_f16 || !src_slice || !dst_slice || !out)
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices: null pointer");
+  if ((((uintptr_t)packed) & 3) || (((uintptr_t)out) & 15))
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices: codes must be 4-byte and out 16-byte aligned");
+  const int64_t tps = slice_elems / 2048;
+  const int64_t n_src = n_groups * 128 / slice_elems;
+  const int64_t n_tiles = n_jobs * tps;
+  constexpr int UNR = 2;
+  int64_t blocks = (n_tiles + 4 * UNR - 1) / (4 * UNR);
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = as_stream(stream);
+  if (out_dtype == USAF_F16)
+    dequant_g128_kernel<USAF_F16, UNR, true><<<(unsigned)blocks, 256, 0, st>>>(
+        (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles, src_slice, dst_slice, tps, n_src,
+        n_dst_slices);
+  else
+    dequant_g128_kernel<USAF_BF16, UNR, true><<<(unsigned)blocks, 256, 0, st>>>(
+        (const uint32_t*)packed, scale_f16, zero_f16, (u32x4*)out, n_tiles, src_slice, dst_slice, tps, n_src,
+        n_dst_slices);
+  return check_launch("dequant_q4_slices");
 }
 
 extern "C" int usaf_hip_quantize_q4(const void* x, int32_t x_dtype, int64_t numel, int64_t group_size,

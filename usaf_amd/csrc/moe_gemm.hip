@@ -71,6 +71,8 @@ struct GemmArgs {
   const uint8_t* wq;       // packed codes of the whole [E, w_rows, w_cols] weight
   const uint32_t* wsz;     // per 128-element group: fp16 scale bits | fp16 zero bits << 16
   const uint16_t* w16;     // dense 16-bit weight [E, w_rows, w_cols] (BQ == BQ_DENSE16)
+  const int32_t* w_slot;   // dense weights in an arena: expert e's [w_rows, w_cols] block is
+  int64_t n_slots;         //   block w_slot[e] (clamped to [0, n_slots)) of w16; nullptr: block e
   int64_t w_rows, w_cols;  // per-expert weight matrix
   int64_t N, K;            // output columns, contraction length
   int64_t inter;           // I (SwiGLU epilogues)
@@ -91,6 +93,15 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Block of the dense weight operand that holds expert e: e itself, or its
+// arena slot (clamped, so a stale table can give wrong weights but never an
+// access outside the arena).
+__device__ __forceinline__ int64_t weight_block(const GemmArgs& g, int e) {
+  if (g.w_slot == nullptr) return e;
+  const int64_t s = g.w_slot[e];
+  return s < 0 ? 0 : (s >= g.n_slots ? g.n_slots - 1 : s);
 }
 
 // ---- 4-bit -> 16-bit conversion (bit-identical to dequantize_4bit) ----------
@@ -207,7 +218,7 @@ template <int BMODE, int EPI, int BQ, int DT>
 __device__ __forceinline__ void produce_tile(const GemmArgs& g, uint16_t* sA0, uint16_t* sB0, const int ptid,
                                              const int e, const int64_t m_beg, const int valid, const int64_t n0,
                                              const int nk) {
-  const int64_t w_base = (int64_t)e * g.w_rows * g.w_cols;  // element offset of expert e
+  const int64_t w_base = weight_block(g, e) * g.w_rows * g.w_cols;  // element offset of expert e's weight
   // A: chunks c = ptid + 256*i (i < A_CHUNKS) of 16 B: row c>>3, 8-element k block c&7.
   // Rows past the expert's last slot re-read its first row into LDS rows that
   // are never used: loads and stores stay unconditional, which keeps the
@@ -800,7 +811,9 @@ __device__ __forceinline__ void nk_tile(const GemmArgs& g, uint16_t* sA0, uint16
   // element offset of (weight row, k = 32 * half) in the [E, w_rows, K] weight
   int64_t woff[2];
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) woff[cb] = ((int64_t)e * g.w_rows + (wave_on ? wrow[cb] : 0)) * K + 32 * half;
+  for (int cb = 0; cb < 2; ++cb)
+    woff[cb] = ((BQ == BQ_DENSE16 ? weight_block(g, e) : (int64_t)e) * g.w_rows + (wave_on ? wrow[cb] : 0)) * K +
+               32 * half;
 
   // A: chunk c = tid + 256 i is row (tid >> 3) + 32 i (row block i), k block tid & 7
   int32_t a_off[NRB];
@@ -1901,6 +1914,47 @@ extern "C" int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* 
   g.out = (uint16_t*)y; g.ldo = H;
   const int64_t max_tiles = (S / NK_BM + E) * ((H + NK_BN - 1) / NK_BN);
   return launch_gemm_nk<EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_fwd");
+}
+
+// Forward gate_up + SwiGLU with dense weights held in a slot arena (usaf_amd's
+// per-expert cache of dequantized copies): expert e's [2I, H] weight is block
+// slot_of[e] of arena [n_slots, 2I, H].
+extern "C" int usaf_hip_moe_gate_up_fwd_slots(const void* x, int64_t T_rows, int64_t H, const int32_t* token_idx,
+                                              const int32_t* offsets, int64_t S, int64_t E, int64_t I,
+                                              const void* arena, const int32_t* slot_of, int64_t n_slots,
+                                              int32_t dtype, void* gu, void* act, void* stream) {
+  if (int rc = check_common("moe_gate_up_fwd_slots", S, E, offsets, nullptr, nullptr, arena)) return rc;
+  if (!slot_of || n_slots <= 0) return set_error(USAF_ERR_INVALID, "moe_gate_up_fwd_slots: needs slot_of and n_slots > 0");
+  if (H % 128 != 0 || H <= 0 || I % 32 != 0 || I <= 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_fwd_slots: needs H %% 128 == 0 and I %% 32 == 0");
+  if (S == 0) return clear_error();
+  if (!x || !token_idx || !gu || !act) return set_error(USAF_ERR_INVALID, "moe_gate_up_fwd_slots: null pointer");
+  GemmArgs g{};
+  g.A = (const uint16_t*)x; g.lda = H; g.a_rows = token_idx;
+  g.w16 = (const uint16_t*)arena; g.w_slot = slot_of; g.n_slots = n_slots; g.w_rows = 2 * I; g.w_cols = H;
+  g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
+  g.out = (uint16_t*)act; g.ldo = I; g.out2 = (uint16_t*)gu; g.ldo2 = 2 * I;
+  const int64_t max_tiles = (S / NK_BM + E) * ((I + 127) / 128);
+  return launch_gemm_nk<EPI_SWIGLU_FWD>(g, dtype, max_tiles, T_rows, as_stream(stream), "moe_gate_up_fwd_slots");
+}
+
+// Forward down projection with dense weights in a slot arena [n_slots, H, I].
+extern "C" int usaf_hip_moe_down_fwd_slots(const void* act, int64_t I, const int32_t* offsets, int64_t S, int64_t E,
+                                           int64_t H, const void* arena, const int32_t* slot_of, int64_t n_slots,
+                                           int32_t dtype, void* y, void* stream) {
+  if (int rc = check_common("moe_down_fwd_slots", S, E, offsets, nullptr, nullptr, arena)) return rc;
+  if (!slot_of || n_slots <= 0) return set_error(USAF_ERR_INVALID, "moe_down_fwd_slots: needs slot_of and n_slots > 0");
+  if (I % 128 != 0 || I <= 0 || H % 64 != 0 || H <= 0)
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_down_fwd_slots: needs I %% 128 == 0 and H %% 64 == 0");
+  if (S == 0) return clear_error();
+  if (!act || !y) return set_error(USAF_ERR_INVALID, "moe_down_fwd_slots: null pointer");
+  GemmArgs g{};
+  g.A = (const uint16_t*)act; g.lda = I; g.a_rows = nullptr;
+  g.w16 = (const uint16_t*)arena; g.w_slot = slot_of; g.n_slots = n_slots; g.w_rows = H; g.w_cols = I;
+  g.N = H; g.K = I; g.inter = I; g.offsets = offsets; g.E = (int)E;
+  g.out = (uint16_t*)y; g.ldo = H;
+  const int64_t max_tiles = (S / NK_BM + E) * ((H + NK_BN - 1) / NK_BN);
+  return launch_gemm_nk<EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_fwd_slots");
 }
 
 // Backward through the down projection and SwiGLU: dgu[m] from dcur[m] @ W_down[e].

@@ -1,0 +1,179 @@
+"""Per-expert LRU of dequantized copies in one HBM slot arena.
+
+The reference's ``QuantizedExpertCache`` keeps whole expert modules (one MoE
+layer's fused gate_up/down tensors, 1.2 GB in fp16) in an LRU and dequantizes
+a module on the CPU when it is missing (usaf/moe_loader.py:130-181).  On an
+MI355X every layer's 4-bit weights stay resident in HBM (15.4 GB for the 48
+layers of Qwen3-30B-A3B) and the copies are per expert:
+
+* one arena of ``n_slots`` slots is allocated once (``max_bytes`` of HBM, at
+  most one slot per expert of the model); a slot holds one expert's
+  dequantized gate_up [2I, H] and down [H, I] slices in the activation dtype;
+* ``touch(layer, experts)`` applies the reference's LRU policy to the keys
+  (layer, expert) in the given order -- a hit moves the key to the most
+  recent end, a miss takes a free slot or evicts the least recently used key
+  -- and fills every missed slot with one batched dequant launch per tensor
+  (usaf_hip_dequant_q4_slices), reading the 4-bit slices from HBM;
+* the layer's slot table (int32 [E] on the device) then feeds the arena
+  GEMMs (usaf_hip_moe_gate_up_fwd_slots / _down_fwd_slots), so no expert is
+  ever copied into a contiguous [E, ...] tensor.
+
+A layer's experts must fit the arena together (n_slots >= E), so a touch never
+evicts a key it inserted itself.  Slot tables of layers that lost experts to
+eviction are refreshed by their next touch, which every forward starts with.
+"""
+from __future__ import annotations
+
+from collections import OrderedDict
+from typing import Dict, Iterable, List, Optional, Tuple
+
+import torch
+
+from . import _native as N
+from .moe import ExpertWeights, Q4Tensor, bucket_by_expert, combine
+
+
+class ExpertSlotCache:
+    def __init__(self, layers: Dict[str, ExpertWeights], device, max_bytes: int,
+                 dtype: torch.dtype = torch.bfloat16) -> None:
+        if not layers:
+            raise ValueError("ExpertSlotCache needs at least one layer")
+        self.device = torch.device(device)
+        self.dtype = dtype
+        first = next(iter(layers.values()))
+        self.E, self.H, self.I = first.E, first.H, first.I
+        for name, ew in layers.items():
+            if not ew.is_q4 or (ew.E, ew.H, ew.I) != (self.E, self.H, self.I):
+                raise ValueError(f"{name}: every layer must hold 4-bit experts of one shape")
+            for q in (ew.gate_up, ew.down):
+                if not q.fused_ok():
+                    raise ValueError(f"{name}: the slot cache needs group size 128 along whole rows")
+        self.layers = dict(layers)
+        self.gu_elems = 2 * self.I * self.H
+        self.dn_elems = self.H * self.I
+        if self.gu_elems % 2048 or self.dn_elems % 2048:
+            raise ValueError("expert slices must be multiples of 2048 elements")
+        elem = torch.empty(0, dtype=dtype).element_size()
+        self.slot_bytes = (self.gu_elems + self.dn_elems) * elem
+        self.n_slots = int(min(len(layers) * self.E, max_bytes // self.slot_bytes))
+        if self.n_slots < self.E:
+            raise ValueError(f"max_bytes={max_bytes} holds {self.n_slots} expert slots; one layer needs {self.E}")
+        self.gu_arena = torch.empty(self.n_slots, 2 * self.I, self.H, dtype=dtype, device=self.device)
+        self.dn_arena = torch.empty(self.n_slots, self.H, self.I, dtype=dtype, device=self.device)
+        self._lru: "OrderedDict[Tuple[str, int], int]" = OrderedDict()
+        self._free: List[int] = list(range(self.n_slots - 1, -1, -1))
+        self._host_tables: Dict[str, List[int]] = {n: [0] * self.E for n in layers}
+        self._tables: Dict[str, torch.Tensor] = {n: torch.zeros(self.E, dtype=torch.int32, device=self.device)
+                                                  for n in layers}
+        self.hits = self.misses = self.evictions = 0
+        self.dequant_bytes = 0
+        self.dequant_events: Optional[list] = None  # set to a list to time the fill launches
+
+    # ---- bookkeeping ------------------------------------------------------------
+
+    @property
+    def cached_keys(self) -> List[Tuple[str, int]]:
+        """(layer, expert) keys, least recently used first."""
+        return list(self._lru.keys())
+
+    def slot_of(self, layer: str, expert: int) -> Optional[int]:
+        return self._lru.get((layer, int(expert)))
+
+    def nbytes(self) -> int:
+        return self.n_slots * self.slot_bytes
+
+    def touch(self, layer: str, experts: Optional[Iterable[int]] = None) -> torch.Tensor:
+        """Mark ``experts`` (default: all of the layer's) used, in order; dequantize
+        the misses; return the layer's slot table (int32 [E], device)."""
+        if layer not in self.layers:
+            raise KeyError(layer)
+        order = range(self.E) if experts is None else [int(e) for e in experts]
+        missed: List[Tuple[int, int]] = []
+        for e in order:
+            key = (layer, e)
+            slot = self._lru.get(key)
+            if slot is not None:
+                self._lru.move_to_end(key)
+                self.hits += 1
+                continue
+            self.misses += 1
+            if self._free:
+                slot = self._free.pop()
+            else:
+                _, slot = self._lru.popitem(last=False)
+                self.evictions += 1
+            self._lru[key] = slot
+            missed.append((e, slot))
+        if missed:
+            self._fill(layer, missed)
+            table = self._host_tables[layer]
+            for e, slot in missed:
+                table[e] = slot
+            staged = torch.tensor(table, dtype=torch.int32).pin_memory()
+            self._tables[layer].copy_(staged, non_blocking=True)
+        return self._tables[layer]
+
+    def _fill(self, layer: str, missed: List[Tuple[int, int]]) -> None:
+        ew = self.layers[layer]
+        jobs = torch.tensor([[e for e, _ in missed], [s for _, s in missed]], dtype=torch.int64).pin_memory()
+        jobs = jobs.to(self.device, non_blocking=True)
+        st = N.stream_ptr(self.device)
+        ev = self.dequant_events
+        if ev is not None:
+            a = torch.cuda.Event(enable_timing=True)
+            a.record()
+        for q, arena, elems in ((ew.gate_up, self.gu_arena, self.gu_elems), (ew.down, self.dn_arena, self.dn_elems)):
+            N.call("usaf_hip_dequant_q4_slices", q.q.data_ptr(), q.s.data_ptr(), q.z.data_ptr(), q.q.shape[0], elems,
+                   len(missed), jobs[0].data_ptr(), jobs[1].data_ptr(), self.n_slots, arena.data_ptr(),
+                   N.dtype_code(self.dtype), st)
+        if ev is not None:
+            b = torch.cuda.Event(enable_timing=True)
+            b.record()
+            ev.append((a, b, len(missed)))
+        # algorithmic bytes: codes + scale/zero in, dequantized copies out
+        n = len(missed) * (self.gu_elems + self.dn_elems)
+        self.dequant_bytes += int(n * (0.5 + 4.0 / 128 + torch.empty(0, dtype=self.dtype).element_size()))
+        # keep the job tensor alive until the launches have read it
+        self._last_jobs = jobs
+
+    # ---- forward --------------------------------------------------------------------
+
+    def forward(self, layer: str, hs: torch.Tensor, weights: torch.Tensor, top_k: int) -> torch.Tensor:
+        """The routed experts of ``layer`` (qwen3moe_dml.py:24-64, forward only) on
+        the cached copies: hs [T, H] and routing weights [T, E] in the cache dtype."""
+        if hs.dtype != self.dtype or weights.dtype != self.dtype:
+            raise TypeError("activations and routing weights must be in the cache dtype")
+        T = hs.shape[0]
+        table = self.touch(layer)
+        overflow = torch.zeros(1, dtype=torch.int32, device=self.device)
+        b = bucket_by_expert(weights, T * min(top_k + 1, self.E), overflow)
+        S = b.n_slots
+        st = N.stream_ptr(self.device)
+        code = N.dtype_code(self.dtype)
+        gu = torch.empty(S, 2 * self.I, dtype=self.dtype, device=self.device)
+        act = torch.empty(S, self.I, dtype=self.dtype, device=self.device)
+        y = torch.empty(S, self.H, dtype=self.dtype, device=self.device)
+        N.call("usaf_hip_moe_gate_up_fwd_slots", hs.data_ptr(), T, self.H, b.token_idx.data_ptr(),
+               b.offsets.data_ptr(), S, self.E, self.I, self.gu_arena.data_ptr(), table.data_ptr(), self.n_slots,
+               code, gu.data_ptr(), act.data_ptr(), st)
+        N.call("usaf_hip_moe_down_fwd_slots", act.data_ptr(), self.I, b.offsets.data_ptr(), S, self.E, self.H,
+               self.dn_arena.data_ptr(), table.data_ptr(), self.n_slots, code, y.data_ptr(), st)
+        out = combine(y, weights, b.pair_slot, self.dtype)
+        self._overflow = overflow
+        return out
+
+    def overflowed(self) -> bool:
+        """Whether the last forward's routing exceeded its static slot capacity
+        (T * (top_k + 1) pairs; then its output is incomplete)."""
+        ov = getattr(self, "_overflow", None)
+        return bool(ov is not None and int(ov.item()))
+
+
+def q4_expert_slice(q: Q4Tensor, expert: int, dtype: torch.dtype) -> torch.Tensor:
+    """Expert ``expert``'s dequantized slice of a 4-bit [E, rows, cols] tensor
+    (for checks): the codec's dequant of that expert's groups."""
+    E, rows, cols = (int(d) for d in q.shape)
+    per = rows * cols // q.group_size
+    sub = Q4Tensor(q.q[expert * per:(expert + 1) * per], q.s[expert * per:(expert + 1) * per],
+                   q.z[expert * per:(expert + 1) * per], torch.Size([rows, cols]), q.group_size)
+    return sub.dequantize(dtype)

@@ -22,6 +22,7 @@ import torch
 import torch.nn as nn
 
 from . import _native as N
+from .importance import TopKImportanceStore  # noqa: F401  (moe_loader.py:584-631, GPU selection)
 from .moe import Q4Tensor
 from .olmoe_streaming import _record_grad, apply_captured_expert_grads  # noqa: F401  (moe_loader.py:778-802)
 from .quantization import dequantize_4bit
@@ -436,50 +437,6 @@ class SparseGradStore:
 
     def n_captured(self) -> int:
         return len(self._compact)
-
-
-class TopKImportanceStore:
-    """moe_loader.py:584-631: per-expert top |grad| candidates, global top-k in
-    ``select`` (torch ops on the GPU over dense per-expert gradients)."""
-
-    def __init__(self, shapes: Dict[str, Any], frac: float, cand_mult: float = 2.0) -> None:
-        self._shapes = shapes
-        self._frac = frac
-        self._cand = cand_mult
-        self._vals: Dict[str, Dict[int, torch.Tensor]] = {n: {} for n in shapes}
-        self._idx: Dict[str, Dict[int, torch.Tensor]] = {n: {} for n in shapes}
-
-    def zero_(self) -> None:
-        for n in self._vals:
-            self._vals[n].clear()
-            self._idx[n].clear()
-
-    def add(self, full_name: str, ei: int, g: torch.Tensor) -> None:
-        if full_name not in self._vals:
-            return
-        flat = g.detach().float().reshape(-1).abs()
-        k = max(1, int(flat.numel() * self._frac * self._cand))
-        v, i = torch.topk(flat, min(k, flat.numel()))
-        self._vals[full_name][int(ei)] = v
-        self._idx[full_name][int(ei)] = i.to(torch.long) + int(ei) * flat.numel()
-
-    def select(self, frac: float | None = None) -> Dict[str, torch.Tensor]:
-        frac = self._frac if frac is None else frac
-        out: Dict[str, torch.Tensor] = {}
-        for name, shape in self._shapes.items():
-            if not self._vals[name]:
-                continue
-            vals = torch.cat(list(self._vals[name].values()))
-            idxs = torch.cat(list(self._idx[name].values()))
-            numel = 1
-            for s in shape:
-                numel *= int(s)
-            k = min(max(1, int(numel * frac)), vals.numel())
-            out[name] = idxs[torch.topk(vals, k).indices]
-        return out
-
-    def n_captured(self) -> int:
-        return sum(len(d) for d in self._vals.values())
 
 
 def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], device: torch.device, *,
