@@ -202,6 +202,22 @@ int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dtype, int64_
                               int32_t* pair_slot, int64_t capacity, int32_t* overflow, void* stream);
 
 /*
+ * usaf_hip_bucket_by_expert without a workspace argument and without any
+ * allocation: its kernels use a file-scope device array of
+ * usaf_hip_bucket_noalloc_max_ints() int32 (4 MiB, one per GPU, held until the
+ * process ends), so ceil(T / 16) * E must not exceed 2^20 (larger calls return
+ * USAF_ERR_UNSUPPORTED).  Same arguments (minus workspace), outputs and errors.
+ * Calls that overlap on one GPU share the array and race; the array keeps the
+ * last call's contents.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).
+ */
+int64_t usaf_hip_bucket_noalloc_max_ints(void);
+int usaf_hip_bucket_by_expert_noalloc(const void* weights, int32_t weights_dtype, int64_t T, int64_t E,
+                                      int32_t* counts, int32_t* offsets, int32_t* token_idx, float* slot_w,
+                                      int32_t* pair_slot, int64_t capacity, int32_t* overflow, void* stream);
+
+/*
  * Expert-ordered combine.  Replaces usaf/qwen3moe_dml.py:62-64:
  *   out[t] = dtype( sum_{e ascending, routed} fp32(y[slot(t,e)]) * fp32(w[t,e]) )
  * accumulated in fp32 with each product rounded before the add, as the

@@ -48,6 +48,8 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_route_topk_bwd": [_c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p],
     "usaf_hip_bucket_by_expert": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p,
                                   _c_p],
+    "usaf_hip_bucket_by_expert_noalloc": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p,
+                                          _c_p],
     "usaf_hip_moe_combine": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p],
     "usaf_hip_moe_combine_bwd": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p],
     "usaf_hip_moe_gate_up_fwd": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
@@ -79,6 +81,7 @@ _SIGNATURES: dict[str, list] = {
 # entry points that return a value instead of a status
 _VALUE_FUNCS: dict[str, tuple] = {
     "usaf_hip_bucket_workspace_ints": (_c_i64, [_c_i64, _c_i64]),
+    "usaf_hip_bucket_noalloc_max_ints": (_c_i64, []),
     "usaf_hip_blocked_elems": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "usaf_hip_blocked_table_elems": (_c_i64, [_c_i64, _c_i64]),
     "usaf_hip_combine_bwd_blocked_ws_floats": (_c_i64, [_c_i64, _c_i64]),

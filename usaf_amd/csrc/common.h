@@ -25,6 +25,9 @@ int device_cu_count();
 // run by usaf_hip_init() and otherwise on first use.
 void prepare_gemm_kernels();
 void prepare_sparse_kernels();
+// Resolves the current device's address of the no-alloc bucketing scratch
+// array (usaf_hip_bucket_by_expert_noalloc); returns a status code.
+int prepare_noalloc_scratch();
 
 // 16-bit float types used in device code.
 typedef _Float16 f16;

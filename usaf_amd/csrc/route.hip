@@ -7,6 +7,9 @@
 //  moe_combine       usaf/qwen3moe_dml.py:62-64 (fp32 accumulation in expert order)
 #include "common.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace usaf {
 namespace {
 
@@ -730,6 +733,77 @@ extern "C" int usaf_hip_bucket_by_expert(const void* weights, int32_t weights_dt
     if (int rc = check_launch("bucket_by_expert/fill")) return rc;
   }
   return clear_error();
+}
+
+// ---- bucketing without an allocation ---------------------------------------------
+// The workspace of usaf_hip_bucket_by_expert (per chunk of 16 tokens and expert:
+// the pair count, then that chunk's first slot) lives in this file-scope device
+// array instead of caller memory, for callers that cannot allocate device
+// memory.  Each GPU the library runs on holds its own copy until the process
+// ends.  The count pass writes every entry the scan and fill passes read, so
+// nothing has to start at zero, and the array keeps the last call's contents.
+// Calls that overlap on one GPU (other streams, other threads) share the array
+// and race.
+constexpr int64_t kBucketScratchInts = int64_t(1) << 20;  // 4 MiB: ceil(T / 16) * E <= 2^20
+static __device__ __align__(256) int32_t scratch[kBucketScratchInts];
+
+namespace {
+// Device address of `scratch` per device, resolved once per device with that
+// device current.  In host code the array's name only stands in for the symbol:
+// kernels, copies and fills get this address.
+std::mutex g_scratch_mu;
+std::atomic<int32_t*> g_scratch_ptr[64];
+
+int bucket_scratch(int32_t** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(USAF_ERR_RUNTIME, "bucket_by_expert_noalloc: no current HIP device");
+  }
+  if (dev < 0 || dev >= 64) return set_error(USAF_ERR_UNSUPPORTED, "bucket_by_expert_noalloc: device %d >= 64", dev);
+  int32_t* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || addr == nullptr) {
+        (void)hipGetLastError();
+        return set_error(USAF_ERR_RUNTIME, "bucket_by_expert_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                         hipGetErrorString(e));
+      }
+      p = static_cast<int32_t*>(addr);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return USAF_OK;
+}
+}  // namespace
+
+int usaf::prepare_noalloc_scratch() {
+  int32_t* p = nullptr;
+  return bucket_scratch(&p);
+}
+
+extern "C" int64_t usaf_hip_bucket_noalloc_max_ints(void) { return kBucketScratchInts; }
+
+extern "C" int usaf_hip_bucket_by_expert_noalloc(const void* weights, int32_t weights_dtype, int64_t T, int64_t E,
+                                                 int32_t* counts, int32_t* offsets, int32_t* token_idx,
+                                                 float* slot_w, int32_t* pair_slot, int64_t capacity,
+                                                 int32_t* overflow, void* stream) {
+  if (T < 0 || E <= 0 || E > 1024) return set_error(USAF_ERR_INVALID, "bucket_by_expert_noalloc: need 0 < E <= 1024");
+  const int64_t need = usaf_hip_bucket_workspace_ints(T, E);
+  if (need > kBucketScratchInts)
+    return set_error(USAF_ERR_UNSUPPORTED,
+                     "bucket_by_expert_noalloc: T=%lld, E=%lld need %lld workspace ints; the static scratch holds "
+                     "%lld (ceil(T/16) * E <= 2^20): use usaf_hip_bucket_by_expert with a workspace",
+                     (long long)T, (long long)E, (long long)need, (long long)kBucketScratchInts);
+  int32_t* ws = nullptr;
+  if (int rc = bucket_scratch(&ws)) return rc;
+  return usaf_hip_bucket_by_expert(weights, weights_dtype, T, E, ws, counts, offsets, token_idx, slot_w, pair_slot,
+                                   capacity, overflow, stream);
 }
 
 extern "C" int usaf_hip_moe_combine(const void* y_slots, const void* weights, const int32_t* pair_slot, int64_t T,

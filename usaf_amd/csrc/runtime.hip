@@ -53,5 +53,6 @@ extern "C" int usaf_hip_init(void) {
   (void)usaf::device_cu_count();
   usaf::prepare_gemm_kernels();
   usaf::prepare_sparse_kernels();
+  if (int rc = usaf::prepare_noalloc_scratch()) return rc;
   return usaf::clear_error();
 }
