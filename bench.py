@@ -370,17 +370,20 @@ def bench_moe_kernels(L, reps: int) -> None:
     qd = ew._ptrs("down", dt)
     qgt = ew._ptrs_t("gate_up")  # the grad-input GEMMs run on the transposed copies, as in the step
     qdt = ew._ptrs_t("down")
+    # the step's trained-value overlays (None when the experts carry none)
+    ovl_gu, ovl_dn = ew._ovl("gate_up_fwd", dt), ew._ovl("down_fwd", dt)
+    ovl_gut, ovl_dnt = ew._ovl("gate_up_bwd", dt), ew._ovl("down_bwd", dt)
     # the step's gate_up launch also writes act in the blocked layout of the sampled gradient
     tb = G.blocked_layout(b.offsets, S)
     act_blk = torch.empty(max(1, int(N.load().usaf_hip_blocked_elems(S, E, I))), dtype=dt, device=dev)
     for _ in range(reps):
         N.call("usaf_hip_moe_gate_up_fwd", x.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(), S, E, I,
-               *qg, code, gu.data_ptr(), act.data_ptr(), act_blk.data_ptr(), tb.data_ptr(), st)
-        N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *qd, code, y.data_ptr(), st)
+               *qg, code, gu.data_ptr(), act.data_ptr(), act_blk.data_ptr(), tb.data_ptr(), *ovl_gu, st)
+        N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *qd, code, y.data_ptr(), *ovl_dn, st)
         N.call("usaf_hip_moe_down_bwd_t", y.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I, *qdt, code,
-               dgu.data_ptr(), st)
+               dgu.data_ptr(), *ovl_dnt, st)
         N.call("usaf_hip_moe_gate_up_bwd_t", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *qgt, code,
-               dx.data_ptr(), st)
+               dx.data_ptr(), *ovl_gut, st)
 
 
 MIXTRAL = dict(E=8, H=4096, I=14336, k=2, T=8192)

@@ -263,13 +263,13 @@ int usaf_hip_moe_combine_bwd(const void* dout, const void* y_slots, const int32_
 int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T, int64_t H, const int32_t* token_idx, const int32_t* offsets, int64_t S,
                              int64_t E, int64_t I, const int8_t* wq, const uint32_t* wsz,
                              const void* w16, int32_t dtype, void* gu, void* act, void* act_blk,
-                             const int32_t* blk_table, void* stream);
+                             const int32_t* blk_table, const uint32_t* overlay, int64_t overlay_words, void* stream);
 
 /* Replaces qwen3moe_dml.py:61: y[s] = act[s] @ W_down[e]^T ([S, H]).  W_down [E, H, I];
  * needs I % 128 == 0, H % 128 == 0. */
 int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
                           const int8_t* wq, const uint32_t* wsz, const void* w16, int32_t dtype, void* y,
-                          void* stream);
+                          const uint32_t* overlay, int64_t overlay_words, void* stream);
 
 /* usaf_hip_moe_gate_up_fwd / usaf_hip_moe_down_fwd with dense weights held in a
  * slot arena (dequantized expert copies of usaf_amd's per-expert cache, the
@@ -303,12 +303,42 @@ int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_t* offsets,
  * of W_down [E, H, I] -> [E, I, H], of W_gate_up [E, 2I, H] -> [E, H, 2I]); same
  * results up to fp32 summation order.  Replace the same autograd steps
  * (qwen3moe_dml.py:58-61).  down_bwd_t needs I % 128 == 0 and H % 128 == 0;
- * gate_up_bwd_t needs H % 128 == 0 and I % 64 == 0; both E <= 512. */
+ * gate_up_bwd_t needs H % 128 == 0 and I % 64 == 0; both E <= 256. */
 int usaf_hip_moe_down_bwd_t(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S, int64_t E,
                             int64_t I, const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype, void* dgu,
-                            void* stream);
+                            const uint32_t* overlay, int64_t overlay_words, void* stream);
 int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E, int64_t H,
-                               const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype, void* dx_slots, void* stream);
+                               const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype, void* dx_slots,
+                               const uint32_t* overlay, int64_t overlay_words, void* stream);
+
+/*
+ * Overlays on the 4-bit GEMMs: trained values (the optimizer's fp32 masters)
+ * that replace the dequantized weight at a fixed set of flat positions, so that
+ * the forward and grad-input GEMMs above see the weights the reference builds
+ * by scattering the masters into its fp16 expert weights every step
+ * (moe_loader.py:218-221 _dequant_cpu, :425-443 sync_resident, train.py:666).
+ * `overlay` (NULL: none) of usaf_hip_moe_gate_up_fwd, usaf_hip_moe_down_fwd,
+ * usaf_hip_moe_down_bwd_t and usaf_hip_moe_gate_up_bwd_t is that GEMM's entry
+ * table of `overlay_words` uint32 words (at least the count below, else
+ * USAF_ERR_INVALID): for each (expert e, n-tile nt, wave w in 0..3) unit u = (e * n_nt + nt)
+ * * 4 + w and each k-step ks (64 contraction elements; n_nt = ceil(I / 128) for
+ * gate_up_fwd, else ceil(N / 256)), 128 uint32 words at ((u * K / 64 + ks) * 128):
+ * word 2 r + cb is entry r (< 64) of the wave's 32-row column block cb,
+ * {byte offset of the weight in the wave's 4 KiB fragment image | value << 16},
+ * offset >= 4096 for an unused word.  The Python layer (usaf_amd/moe.py
+ * Q4Overlay) builds the tables once per set of positions.  A GEMM with an overlay
+ * runs the 4-bit LDS-DMA kernel only (NotImplemented otherwise).
+ *
+ * usaf_hip_overlay_refresh writes new values into one or two such tables:
+ * word words_a[i] of table_a (words_b[i] of table_b) takes the 16-bit `dtype`
+ * (fp16 or bf16) value of fp16(p[i]) -- the reference's fp16 weight after the
+ * scatter -- in its high half.  Words outside [0, n_words) set *bad_flag
+ * (optional) and are skipped.  Replaces the per-step master scatter of
+ * moe_loader.py:425-443 (sync_resident) for weights the fused GEMMs read.
+ */
+int usaf_hip_overlay_refresh(const float* p, int64_t n, const int32_t* words_a, uint32_t* table_a, int64_t n_words_a,
+                             const int32_t* words_b, uint32_t* table_b, int64_t n_words_b, int32_t dtype,
+                             int32_t* bad_flag, void* stream);
 
 /* ---- sparse gradient path and optimizer ----------------------------------- */
 

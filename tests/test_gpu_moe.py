@@ -217,10 +217,10 @@ def test_experts_forward_intermediates(gpu_device, T):
     act_blk = torch.full((int(lib.usaf_hip_blocked_elems(S, ew.E, I)),), float("nan"), dtype=dt, device=gpu_device)
     N.call("usaf_hip_moe_gate_up_fwd", L["hs"].to(gpu_device).data_ptr(), L["hs"].shape[0], H, b.token_idx.data_ptr(),
            b.offsets.data_ptr(), S, ew.E, I, q, sz, w16, N.BF16, gu.data_ptr(), act.data_ptr(), act_blk.data_ptr(),
-           tb.data_ptr(), st)
+           tb.data_ptr(), None, 0, st)
     q, sz, w16 = ew._ptrs("down", dt)
     N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, ew.E, H, q, sz, w16, N.BF16,
-           y.data_ptr(), st)
+           y.data_ptr(), None, 0, st)
     want_blk = G.slot_blocked(act, b.offsets, S, table=tb)
     torch.cuda.synchronize()
     n_used = int(want_blk.table[ew.E]) * I  # elements of the layout (the rest of the buffer is never written)
@@ -524,14 +524,14 @@ def test_backward_transposed_vs_direct(gpu_device, E, H, I, T, k):
     tq = ew._ptrs_t("down")
     assert tq is not None
     N.call("usaf_hip_moe_down_bwd_t", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I, *tq,
-           code, dgu_b.data_ptr(), st)
+           code, dgu_b.data_ptr(), None, 0, st)
     dx_a, dx_b = torch.empty(S, H, dtype=dt, device=dev), torch.empty(S, H, dtype=dt, device=dev)
     N.call("usaf_hip_moe_gate_up_bwd", dgu_a.data_ptr(), I, b.offsets.data_ptr(), S, E, H,
            *ew._ptrs("gate_up", dt), code, dx_a.data_ptr(), st)
     tq = ew._ptrs_t("gate_up")
     assert tq is not None
     N.call("usaf_hip_moe_gate_up_bwd_t", dgu_a.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *tq, code,
-           dx_b.data_ptr(), st)
+           dx_b.data_ptr(), None, 0, st)
     torch.cuda.synchronize()
     assert rel_err(dgu_b, dgu_a) <= 1e-2
     assert rel_err(dx_b, dx_a) <= 1e-2

@@ -127,7 +127,7 @@ def test_cfg0_fp16_gemm_leg(gpu_device):
     y = torch.empty(512, 768, dtype=torch.float16, device=dev)
     Xd = X.to(dev)
     N.call("usaf_hip_moe_down_fwd", Xd.data_ptr(), 2048, offsets.data_ptr(), 512, 1, 768, q.q.data_ptr(),
-           q.scale_zero().data_ptr(), None, N.F16, y.data_ptr(), N.stream_ptr(dev))
+           q.scale_zero().data_ptr(), None, N.F16, y.data_ptr(), None, 0, N.stream_ptr(dev))
     torch.cuda.synchronize()
     ref = (X.float() @ deq[0].float().t()).half()  # F.linear in fp16: fp32 products, one rounding
     rep = {}

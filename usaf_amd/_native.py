@@ -53,14 +53,17 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_moe_combine": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p],
     "usaf_hip_moe_combine_bwd": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p],
     "usaf_hip_moe_gate_up_fwd": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
-                                 _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p],
-    "usaf_hip_moe_down_fwd": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p],
+                                 _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p],
+    "usaf_hip_moe_down_fwd": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_i64,
+                              _c_p],
     "usaf_hip_moe_down_bwd": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p,
                               _c_p],
     "usaf_hip_moe_gate_up_bwd": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p,
                                  _c_p],
-    "usaf_hip_moe_down_bwd_t": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_p],
-    "usaf_hip_moe_gate_up_bwd_t": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_p],
+    "usaf_hip_moe_down_bwd_t": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_p,
+                                _c_i64, _c_p],
+    "usaf_hip_moe_gate_up_bwd_t": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_i64,
+                                   _c_p],
     "usaf_hip_gather_transpose": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
     "usaf_hip_blocked_layout": [_c_p, _c_i64, _c_i64, _c_p, _c_p],
     "usaf_hip_gather_transpose_blocked": [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p],
@@ -77,6 +80,7 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_sparse_adam_step": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_d, _c_d, _c_d, _c_d, _c_i64, _c_p],
     "usaf_hip_scale_check": [_c_p, _c_p, _c_i64, _c_f32, _c_p, _c_p],
     "usaf_hip_overlay_scatter": [_c_p, _c_i32, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p],
+    "usaf_hip_overlay_refresh": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i32, _c_p, _c_p],
 }
 # entry points that return a value instead of a status
 _VALUE_FUNCS: dict[str, tuple] = {

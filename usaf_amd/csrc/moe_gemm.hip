@@ -83,6 +83,8 @@ struct GemmArgs {
   const uint16_t* aux; int64_t ld_aux;  // SWIGLU_BWD: saved gu
   uint16_t* out_t;                // SWIGLU_FWD (4-bit DMA kernel): act also in the blocked slot-major
   const int32_t* blk_table;       //   layout of blk_table (usaf_hip_blocked_layout), or nullptr
+  const uint32_t* ovl;            // 4-bit DMA kernel: overlay entries (usaf_hip_overlay_* layout), or nullptr
+  int64_t ovl_words;              //   and their count (checked against what the GEMM reads)
 };
 
 // Workgroup barrier ordering LDS accesses only.  __syncthreads() also orders
@@ -1137,24 +1139,34 @@ __global__ __launch_bounds__(NK_THREADS) void moe_gemm_nk_kernel(const GemmArgs 
 // steps and epilogue.
 // =====================================================================================
 constexpr int Q_BM = 256, Q_BN = 256, Q_THREADS = 256;
-constexpr int Q_MAX_E = 512;
+constexpr int Q_MAX_E = 256;
 constexpr int Q_A_BYTES = Q_BM * BK * 2;                 // activation rows of one k-step
 constexpr int Q_C_BYTES = Q_BN * BK / 2;                 // codes of one k-step
 constexpr int Q_Z_BYTES = Q_BN * 4;                      // scale|zero pairs of one k-step
 constexpr int Q_STAGE = Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES;
 constexpr int Q_A_LOADS = Q_A_BYTES / (16 * Q_THREADS);  // 8 x 16 B per thread
 constexpr int Q_DMAS = 3 + Q_A_LOADS;                    // DMA instructions per thread per k-step
-// Dynamic LDS (the DMA targets): 3 stages | s_h, s_l, s_off tables | token rows [2][Q_BM].
+constexpr int Q_OVL_DMAS = 2;                            // + overlay entries of one k-step (2 x 256 B per wave)
+// Overlay (trained values over the 4-bit weights): per wave and k-step one
+// group of 128 entries (64 per 32-row column block), each a 32-bit word
+// {byte offset into the wave's 4 KiB fragment image | value << 16}; an offset
+// >= 4096 marks an unused entry.  Two groups per wave are in LDS at a time.
+constexpr int Q_OVL_GROUP = 128 * 4;                     // bytes of one wave's entries per k-step
+constexpr int Q_IMG_BYTES = 64 * 4 * 16;                 // one column block of a wave's weight fragments
+// Dynamic LDS (the DMA targets): 3 stages | s_h, s_l, s_off tables | token rows
+// [2][Q_BM] | overlay entries [4 waves][2][Q_OVL_GROUP].
 // The epilogue tiles are a separate static array: the compiler then knows that
 // their stores cannot collide with DMA writes still in flight and does not
 // drain the DMAs before them.
 constexpr int Q_TAB_OFF = 3 * Q_STAGE;
 constexpr int Q_TOK_OFF = Q_TAB_OFF + 3 * (Q_MAX_E + 1) * 4;
-constexpr size_t kQSmemBytes = (size_t)Q_TOK_OFF + 2 * Q_BM * 4;
+constexpr int Q_OVL_OFF = Q_TOK_OFF + 2 * Q_BM * 4;
+constexpr size_t kQSmemBytes = (size_t)Q_OVL_OFF + 4 * 2 * Q_OVL_GROUP;
 constexpr int Q_EPW = 104;                      // staging row stride, 16-bit elements (96 columns + pad)
 constexpr int Q_EP_ELEMS = 32 * Q_EPW;          // one wave's 32 x 96 staging tile
 static_assert(kQSmemBytes + 4 * Q_EP_ELEMS * 2 <= 160 * 1024, "LDS budget");
 static_assert(4 * Q_EP_ELEMS * 2 >= Q_THREADS * 4, "the prefix scratch lives in the epilogue tiles");
+static_assert(Q_EP_ELEMS * 2 >= Q_IMG_BYTES, "the fragment image of the overlay lives in the wave's epilogue tile");
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -1178,7 +1190,15 @@ struct QTile {
 // BT: the weight is a transposed copy (usaf_hip_q4_transpose): codes along k as
 // usual, but every k has its own scale/zero, read as {s(k) | s(k+1) << 16,
 // z(k) | z(k+1) << 16} pairs from wsz (one 128-column group of n per 256 B per k-step).
-template <int EPI, int DT, bool BT>
+// OVL: trained values replace some of the dequantized weights (the reference's
+// overlay scatter into the fp16 weights, usaf/moe_loader.py:218-221, 425-443).
+// The entries of a k-step ride the activation stream (two more DMAs per step,
+// into the wave's own LDS slots).  After a wave has dequantized a k-step into
+// its fragment registers, it writes each 32-row column block of them to an
+// image in its epilogue tile, stores the entries' values over it (one 16-bit
+// LDS store per lane) and reads the fragments back: every weight the MFMAs see
+// is then the trained value where an entry names it.
+template <int EPI, int DT, bool BT, bool OVL>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
   __shared__ __attribute__((aligned(16))) uint16_t q_ep[4 * Q_EP_ELEMS];
@@ -1249,6 +1269,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   int a_ord = 0, a_kt = 0;
   bool a_enter = false;                       // entered a new tile at the last advance: refresh a_off
   uint32_t a_off[Q_A_LOADS];                  // byte offsets of this thread's chunks at k-step 0
+  uint32_t o_off = 0;                         // OVL: byte offset of this lane's entry word at k-step 0 of the tile
   const int a_lc = (tid & 7) ^ q_swz(tid >> 3);  // logical chunk of this thread's DMA slot
   const uint32_t lda_b = (uint32_t)g.lda * 2;
   auto c_setup = [&](const QTile& t) {
@@ -1276,6 +1297,12 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     }
   };
   auto a_refresh = [&](int ord) {
+    if constexpr (OVL) {
+      // entries of tile unit ((e * n_nt + nt) * 4 + wave): nk groups of Q_OVL_GROUP bytes
+      const QTile t = decode(ord);
+      const uint32_t unit = (uint32_t)(((int64_t)t.e * n_nt + t.nt) * 4 + wave);
+      o_off = unit * (uint32_t)nk * Q_OVL_GROUP + (uint32_t)lane * 4;
+    }
     if (g.a_rows) {
       const int32_t* src = s_tok + (ord & 1) * Q_BM;
 #pragma unroll
@@ -1290,12 +1317,19 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     }
   };
   // one DMA instruction of a k-step: d = 0, 1 the code chunks, 2 the scale|zero
-  // word (into stage sc_stage), d >= 3 activation chunk d - 3 (into stage sa_stage)
-  auto dma_one = [&](int d, int sc_stage, int sa_stage) {
+  // word (into stage sc_stage), 3 <= d < Q_DMAS activation chunk d - 3 (into
+  // stage sa_stage), OVL: d = Q_DMAS, Q_DMAS + 1 the two halves of the wave's
+  // overlay entries of the activation stream's k-step (into entry slot o_slot)
+  auto dma_one = [&](int d, int sc_stage, int sa_stage, int o_slot) {
     sc_stage = uni(sc_stage);
     sa_stage = uni(sa_stage);
     const int c_kt_u = uni(c_kt), a_kt_u = uni(a_kt);
-    if (d < 2) {
+    if (OVL && d >= Q_DMAS) {
+      const int h = d - Q_DMAS;
+      uint8_t* so = qsm + Q_OVL_OFF + (wave * 2 + uni(o_slot)) * Q_OVL_GROUP + h * 256;
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.ovl) + a_kt_u * Q_OVL_GROUP + h * 256;
+      dma4(base + o_off, so);
+    } else if (d < 2) {
       uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
       const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wq) + c_kt_u * 32;
       dma16(base + (d ? c_off1 : c_off0), sc + (d * 256 + wave * 64) * 16);
@@ -1397,6 +1431,39 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     }
   };
 
+  // the wave's epilogue tile (also the overlay's fragment image during the k-steps)
+  uint16_t* const sEp = q_ep + wave * Q_EP_ELEMS;
+  const uint32_t sEp_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sEp;
+
+  // OVL: the trained values of entry slot `slot` over weight fragment set BSX.
+  // Per column block: the 16 fragment registers go to the image as 4 x 1 KiB
+  // (lane l's 16 bytes of sub-step j at (64 j + l) * 16), one 16-bit store per
+  // lane puts entry l of the block over it, and the fragments are read back.
+  // The stores are explicit ds_write instructions (a compiler-visible LDS store
+  // would make it drain the DMAs in flight first); the LDS operations of one
+  // wave complete in order, so each read sees the stores before it.
+  auto ovl_patch = [&](auto bsx_c, int slot) {
+    constexpr int BSX = decltype(bsx_c)::value;
+    const uint8_t* ent = qsm + Q_OVL_OFF + (wave * 2 + uni(slot)) * Q_OVL_GROUP;
+    const uint32_t e0 = *reinterpret_cast<const uint32_t*>(ent + lane * 8);
+    const uint32_t e1 = *reinterpret_cast<const uint32_t*>(ent + lane * 8 + 4);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(sEp_lds + (uint32_t)lane * 16), "v"(wf[BSX][cb][j]),
+                     "i"(j * 1024)
+                     : "memory");
+      const uint32_t en = cb ? e1 : e0;
+      const uint32_t off = en & 0xFFFFu;
+      if (off < (uint32_t)Q_IMG_BYTES)
+        asm volatile("ds_write_b16 %0, %1" ::"v"(sEp_lds + off), "v"(en >> 16) : "memory");
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wf[BSX][cb][j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(sEp) + (64 * j + lane) * 16);
+    }
+  };
+
   // ---- one k-step: MFMAs of k-step gs (activations in stage s0, weights in
   //      slot BS) with the dequant of k-step gs + 1 (codes in stage s1) into
   //      slot BS ^ 1; the k-step's DMAs (codes of gs + 3 into stage s0,
@@ -1408,7 +1475,8 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     constexpr int R = NF / 2;       // regions of two fragments (four MFMAs)
     constexpr int PF = 4;           // fragment prefetch distance
     constexpr int PPR = (32 + R - 2) / (R - 1);  // weight pairs dequantized per region (regions 1..R-1)
-    constexpr int DPR = (Q_DMAS + R - 1) / R;    // DMAs issued per region
+    constexpr int QD = Q_DMAS + (OVL ? Q_OVL_DMAS : 0);  // DMA instructions of the step
+    constexpr int DPR = (QD + R - 1) / R;        // DMAs issued per region
     pre_step();
     u32x4 cq[2], kz[8];
     uint32_t csz[2];
@@ -1434,7 +1502,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       }
 #pragma unroll
       for (int dd = 0; dd < DPR; ++dd)
-        if (r * DPR + dd < Q_DMAS) dma_one(r * DPR + dd, s0, s2);
+        if (r * DPR + dd < QD) dma_one(r * DPR + dd, s0, s2, BS);
       if (r >= 1) {
 #pragma unroll
         for (int pp = 0; pp < PPR; ++pp) {
@@ -1461,24 +1529,29 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       __builtin_amdgcn_sched_barrier(0);
     }
     advance();
-    // this step's 11 DMAs may stay in flight; everything older (the stages the
-    // next step reads, the token rows) has landed in this wave, and after the
-    // barrier in all waves.  sched_barrier keeps the step's register work on
-    // its side of the barrier.
+    // this step's 11 DMAs (13 with OVL) may stay in flight; everything older
+    // (the stages the next step reads, the token rows, the entries of k-step
+    // gs + 1) has landed in this wave, and after the barrier in all waves.
+    // sched_barrier keeps the step's register work on its side of the barrier.
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(11)\n\ts_barrier" ::: "memory");
+    if constexpr (OVL) {
+      asm volatile("s_waitcnt vmcnt(13)" ::: "memory");
+      ovl_patch(std::integral_constant<int, BS ^ 1>{}, BS ^ 1);  // k-step gs + 1: entries in slot (gs + 1) & 1
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(11)\n\ts_barrier" ::: "memory");
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
   // ---- epilogue: per 32-slot block, the wave's dtype results go through its
   //      own LDS tile ([32 slots][96 columns]: gate, up, act or the 64 output
   //      columns) and out as 16-byte row stores, 4-8 lanes per row segment ----
-  uint16_t* const sEp = q_ep + wave * Q_EP_ELEMS;
   // lane's accumulator values r = 4q..4q+3 of weight block cb -> columns 32cb + 8q + 4half + [0,4) of slot l32.
   // Written with an explicit ds_write_b64: the compiler would otherwise drain
   // every DMA in flight (the next tile's first k-steps) before an LDS store.
   // The wave's own LDS operations complete in order, so the reads below see it.
-  const uint32_t sEp_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sEp;
   auto stage4 = [&](int col, uint32_t lo, uint32_t hi) {
     const uint32_t addr = sEp_lds + (uint32_t)(l32 * Q_EPW + col) * 2;
     const uint64_t v = (uint64_t)lo | ((uint64_t)hi << 32);
@@ -1646,7 +1719,8 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     a_refresh(0);
   }
-  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0);  // codes 0
+  constexpr int QD = Q_DMAS + (OVL ? Q_OVL_DMAS : 0);
+  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0, 0);  // codes 0
   if (nk == 2 && n_my > 1) {                       // the code stream enters tile 1 after codes 1
     c_next = decode(1);
     tok_fill(c_next, 1);
@@ -1660,13 +1734,14 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       c_kt = nk - 1;
     }
   }
-  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 1, 0);  // codes 1, activations 0
+  for (int d = 0; d < QD; ++d) dma_one(d, 1, 0, 0);  // codes 1, activations (and entries) 0
   advance();
   pre_step();
-  for (int d = 0; d < Q_DMAS; ++d) dma_one(d, 2, 1);  // codes 2, activations 1
+  for (int d = 0; d < QD; ++d) dma_one(d, 2, 1, 1);  // codes 2, activations (and entries) 1
   advance();
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   dequant_all(I0{}, 0);
+  if constexpr (OVL) ovl_patch(I0{}, 0);   // k-step 0: entries in slot 0
   asm volatile("s_barrier" ::: "memory");  // stage 0's codes are refilled by k-step 0
 
   // ---- tiles ----
@@ -1724,16 +1799,40 @@ int launch_nk_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   return USAF_OK;
 }
 
-template <int EPI, int DT, bool BT>
+template <int EPI, int DT, bool BT, bool OVL>
 void q4_prepare() {
-  static const bool done = raise_lds_limit(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT, BT>), kQSmemBytes);
+  static const bool done =
+      raise_lds_limit(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT, BT, OVL>), kQSmemBytes);
   (void)done;
 }
 
 template <int EPI, int DT, bool BT = false>
 int launch_q4_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
-  q4_prepare<EPI, DT, BT>();
-  moe_gemm_q4_kernel<EPI, DT, BT><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
+  if (g.ovl) {
+    q4_prepare<EPI, DT, BT, true>();
+    moe_gemm_q4_kernel<EPI, DT, BT, true><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
+  } else {
+    q4_prepare<EPI, DT, BT, false>();
+    moe_gemm_q4_kernel<EPI, DT, BT, false><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
+  }
+  return USAF_OK;
+}
+
+// Entry words of an overlay for this GEMM: 4 waves x (K / 64) k-steps x 128 per
+// (expert, n-tile); the kernel addresses them with 32-bit byte offsets.
+int64_t ovl_words(const GemmArgs& g, int epi) {
+  const int64_t n_nt = epi == EPI_SWIGLU_FWD ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
+  return (int64_t)g.E * n_nt * 4 * (g.K / BK) * 128;
+}
+
+int check_ovl(const GemmArgs& g, int epi, const char* what) {
+  if (!g.ovl) return USAF_OK;
+  if ((uintptr_t)g.ovl & 3) return set_error(USAF_ERR_INVALID, "%s: overlay entries must be 4-byte aligned", what);
+  const int64_t need = ovl_words(g, epi);
+  if (g.ovl_words < need)
+    return set_error(USAF_ERR_INVALID, "%s: overlay table of %lld words, this GEMM reads %lld", what,
+                     (long long)g.ovl_words, (long long)need);
+  if (need * 4 >= ((int64_t)1 << 32)) return set_error(USAF_ERR_UNSUPPORTED, "%s: overlay table beyond 4 GiB", what);
   return USAF_OK;
 }
 
@@ -1745,6 +1844,7 @@ int launch_q4t(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_tota
     return set_error(USAF_ERR_INVALID, "%s: activations must be 16-byte aligned rows", what);
   if (a_rows_total * g.lda * 2 >= ((int64_t)1 << 32) || (int64_t)g.E * g.w_rows * g.w_cols / 2 >= ((int64_t)1 << 32))
     return set_error(USAF_ERR_UNSUPPORTED, "%s: operands beyond 4 GiB", what);
+  if (int rc = check_ovl(g, EPI, what)) return rc;
   int64_t blocks = (int64_t)device_cu_count();
   if (blocks > max_tiles) blocks = max_tiles;
   if (blocks < 1) blocks = 1;
@@ -1774,6 +1874,11 @@ int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_
   if (blocks < 1) blocks = 1;
   const bool dense = g.w16 != nullptr;
   const bool dma = q4_dma_ok(g, a_rows_total);
+  if (g.ovl && !dma)
+    return set_error(USAF_ERR_UNSUPPORTED,
+                     "%s: an overlay needs the 4-bit LDS-DMA kernel (4-bit weights, 16-byte aligned activation rows, "
+                     "K %% 128 == 0, E <= %d, operands below 4 GiB)", what, Q_MAX_E);
+  if (int rc = check_ovl(g, EPI, what)) return rc;
   int rc;
   if (dt == USAF_BF16)
     rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
@@ -1843,10 +1948,14 @@ void prepare_dt() {
   nk_prepare<EPI_SWIGLU_FWD, BQ_DENSE16, DT>();
   nk_prepare<EPI_STORE, BQ_Q4, DT>();
   nk_prepare<EPI_STORE, BQ_DENSE16, DT>();
-  q4_prepare<EPI_SWIGLU_FWD, DT, false>();
-  q4_prepare<EPI_STORE, DT, false>();
-  q4_prepare<EPI_SWIGLU_BWD, DT, true>();
-  q4_prepare<EPI_STORE, DT, true>();
+  q4_prepare<EPI_SWIGLU_FWD, DT, false, false>();
+  q4_prepare<EPI_STORE, DT, false, false>();
+  q4_prepare<EPI_SWIGLU_BWD, DT, true, false>();
+  q4_prepare<EPI_STORE, DT, true, false>();
+  q4_prepare<EPI_SWIGLU_FWD, DT, false, true>();
+  q4_prepare<EPI_STORE, DT, false, true>();
+  q4_prepare<EPI_SWIGLU_BWD, DT, true, true>();
+  q4_prepare<EPI_STORE, DT, true, true>();
   ws_prepare<BMODE_KN, EPI_SWIGLU_BWD, BQ_Q4, DT>();
   ws_prepare<BMODE_KN, EPI_SWIGLU_BWD, BQ_DENSE16, DT>();
   ws_prepare<BMODE_KN, EPI_STORE, BQ_Q4, DT>();
@@ -1869,7 +1978,8 @@ using namespace usaf;
 extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T_rows, int64_t H, const int32_t* token_idx, const int32_t* offsets,
                                         int64_t S, int64_t E, int64_t I, const int8_t* wq, const uint32_t* wsz,
                                         const void* w16, int32_t dtype, void* gu, void* act, void* act_blk,
-                                        const int32_t* blk_table, void* stream) {
+                                        const int32_t* blk_table, const uint32_t* overlay, int64_t overlay_words,
+                                        void* stream) {
   if (int rc = check_common("moe_gate_up_fwd", S, E, offsets, wq, wsz, w16)) return rc;
   if (H % 128 != 0 || H <= 0 || I % 32 != 0 || I <= 0)
     return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_fwd: needs H %% 128 == 0 and I %% 32 == 0 (H=%lld, I=%lld)",
@@ -1881,6 +1991,8 @@ extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T_rows, int64_t H
   g.wq = (const uint8_t*)wq; g.wsz = wsz; g.w16 = (const uint16_t*)w16; g.w_rows = 2 * I; g.w_cols = H;
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)act; g.ldo = I; g.out2 = (uint16_t*)gu; g.ldo2 = 2 * I;
+  g.ovl = overlay;
+  g.ovl_words = overlay_words;
   if (act_blk && !blk_table) return set_error(USAF_ERR_INVALID, "moe_gate_up_fwd: act_blk needs blk_table");
   if (act_blk && ((uintptr_t)act_blk & 15)) return set_error(USAF_ERR_INVALID, "moe_gate_up_fwd: act_blk must be 16-byte aligned");
   // the 4-bit DMA kernel writes the blocked act^T from its epilogue; the other
@@ -1900,7 +2012,8 @@ extern "C" int usaf_hip_moe_gate_up_fwd(const void* x, int64_t T_rows, int64_t H
 // Forward down projection (qwen3moe_dml.py:61): y[m] = act[m] @ W_down[e]^T.
 extern "C" int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* offsets, int64_t S, int64_t E,
                                      int64_t H, const int8_t* wq, const uint32_t* wsz,
-                                     const void* w16, int32_t dtype, void* y, void* stream) {
+                                     const void* w16, int32_t dtype, void* y, const uint32_t* overlay,
+                                     int64_t overlay_words, void* stream) {
   if (int rc = check_common("moe_down_fwd", S, E, offsets, wq, wsz, w16)) return rc;
   if (I % 128 != 0 || I <= 0 || H % 64 != 0 || H <= 0)
     return set_error(USAF_ERR_UNSUPPORTED, "moe_down_fwd: needs I %% 128 == 0 and H %% 64 == 0 (I=%lld, H=%lld)",
@@ -1912,6 +2025,8 @@ extern "C" int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* 
   g.wq = (const uint8_t*)wq; g.wsz = wsz; g.w16 = (const uint16_t*)w16; g.w_rows = H; g.w_cols = I;
   g.N = H; g.K = I; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)y; g.ldo = H;
+  g.ovl = overlay;
+  g.ovl_words = overlay_words;
   const int64_t max_tiles = (S / NK_BM + E) * ((H + NK_BN - 1) / NK_BN);
   return launch_gemm_nk<EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_fwd");
 }
@@ -1998,7 +2113,7 @@ extern "C" int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_
 // dgu from dcur @ W_down[e] on the transposed copy W_down^T [E, I, H].
 extern "C" int usaf_hip_moe_down_bwd_t(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S,
                                        int64_t E, int64_t I, const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype,
-                                       void* dgu, void* stream) {
+                                       void* dgu, const uint32_t* overlay, int64_t overlay_words, void* stream) {
   if (int rc = check_common("moe_down_bwd_t", S, E, offsets, wq_t, wsz_t, nullptr)) return rc;
   if (I % 128 != 0 || I <= 0 || H % 128 != 0 || H <= 0)
     return set_error(USAF_ERR_UNSUPPORTED, "moe_down_bwd_t: needs I %% 128 == 0 and H %% 128 == 0 (I=%lld, H=%lld)",
@@ -2010,6 +2125,8 @@ extern "C" int usaf_hip_moe_down_bwd_t(const void* dcur, int64_t H, const void* 
   g.wq = (const uint8_t*)wq_t; g.wsz = wsz_t; g.w16 = nullptr; g.w_rows = I; g.w_cols = H;
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)dgu; g.ldo = 2 * I; g.aux = (const uint16_t*)gu; g.ld_aux = 2 * I;
+  g.ovl = overlay;
+  g.ovl_words = overlay_words;
   const int64_t max_tiles = (S / Q_BM + E) * ((I + Q_BN - 1) / Q_BN);
   return launch_q4t<EPI_SWIGLU_BWD>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_bwd_t");
 }
@@ -2017,7 +2134,8 @@ extern "C" int usaf_hip_moe_down_bwd_t(const void* dcur, int64_t H, const void* 
 // dx_slots from dgu @ W_gate_up[e] on the transposed copy W_gate_up^T [E, H, 2I].
 extern "C" int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offsets, int64_t S, int64_t E,
                                           int64_t H, const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype,
-                                          void* dx_slots, void* stream) {
+                                          void* dx_slots, const uint32_t* overlay, int64_t overlay_words,
+                                          void* stream) {
   if (int rc = check_common("moe_gate_up_bwd_t", S, E, offsets, wq_t, wsz_t, nullptr)) return rc;
   if (H % 128 != 0 || H <= 0 || I % 64 != 0 || I <= 0)
     return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_bwd_t: needs H %% 128 == 0 and I %% 64 == 0 (H=%lld, I=%lld)",
@@ -2029,6 +2147,8 @@ extern "C" int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int3
   g.wq = (const uint8_t*)wq_t; g.wsz = wsz_t; g.w16 = nullptr; g.w_rows = H; g.w_cols = 2 * I;
   g.N = H; g.K = 2 * I; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)dx_slots; g.ldo = H;
+  g.ovl = overlay;
+  g.ovl_words = overlay_words;
   const int64_t max_tiles = (S / Q_BM + E) * ((H + Q_BN - 1) / Q_BN);
   return launch_q4t<EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_gate_up_bwd_t");
 }

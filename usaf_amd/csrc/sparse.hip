@@ -585,6 +585,34 @@ __global__ __launch_bounds__(256) void overlay_scatter_kernel(uint16_t* __restri
   }
 }
 
+// Trained values into the overlay entries of the fused 4-bit GEMMs: entry word
+// wa[i] of table ta (and wb[i] of tb) takes DT(fp16(p[i])) in its high half --
+// the reference's fp16 weight after the overlay scatter (moe_loader.py:218-221),
+// then the activation dtype, as the GEMMs convert every dequantized weight.
+// Words outside a table set *bad and are skipped.
+template <int DT>
+__global__ __launch_bounds__(256) void overlay_refresh_kernel(const float* __restrict__ p, int64_t n,
+                                                              const int32_t* __restrict__ wa, uint16_t* __restrict__ ta,
+                                                              int64_t na, const int32_t* __restrict__ wb,
+                                                              uint16_t* __restrict__ tb, int64_t nb,
+                                                              int32_t* __restrict__ bad) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint16_t h = f32_to_f16_bits(p[i]);
+    const uint16_t v = DT == USAF_F16 ? h : f32_to_bf16_bits(f16_bits_to_f32(h));
+    if (ta) {
+      const int64_t w = wa[i];
+      if (w >= 0 && w < na) ta[2 * w + 1] = v;
+      else if (bad) bad[0] = 1;
+    }
+    if (tb) {
+      const int64_t w = wb[i];
+      if (w >= 0 && w < nb) tb[2 * w + 1] = v;
+      else if (bad) bad[0] = 1;
+    }
+  }
+}
+
 int grid_for(int64_t n, int per_cu = 8) {
   int64_t b = (n + 255) / 256;
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
@@ -829,6 +857,25 @@ extern "C" int usaf_hip_scale_check(const float* in, float* out, int64_t n, floa
   if (!in || !out || !finite_flag) return set_error(USAF_ERR_INVALID, "scale_check: null pointer");
   scale_check_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(in, out, n, denom, finite_flag);
   return check_launch("scale_check");
+}
+
+extern "C" int usaf_hip_overlay_refresh(const float* p, int64_t n, const int32_t* words_a, uint32_t* table_a,
+                                        int64_t n_words_a, const int32_t* words_b, uint32_t* table_b,
+                                        int64_t n_words_b, int32_t dtype, int32_t* bad_flag, void* stream) {
+  if (n < 0 || n_words_a < 0 || n_words_b < 0) return set_error(USAF_ERR_INVALID, "overlay_refresh: negative size");
+  if (n == 0) return clear_error();
+  if (!p || (table_a && !words_a) || (table_b && !words_b))
+    return set_error(USAF_ERR_INVALID, "overlay_refresh: null pointer");
+  hipStream_t st = as_stream(stream);
+  if (dtype == USAF_F16)
+    overlay_refresh_kernel<USAF_F16><<<grid_for(n), 256, 0, st>>>(p, n, words_a, (uint16_t*)table_a, n_words_a,
+                                                                   words_b, (uint16_t*)table_b, n_words_b, bad_flag);
+  else if (dtype == USAF_BF16)
+    overlay_refresh_kernel<USAF_BF16><<<grid_for(n), 256, 0, st>>>(p, n, words_a, (uint16_t*)table_a, n_words_a,
+                                                                    words_b, (uint16_t*)table_b, n_words_b, bad_flag);
+  else
+    return set_error(USAF_ERR_INVALID, "overlay_refresh: dtype must be fp16 or bf16");
+  return check_launch("overlay_refresh");
 }
 
 extern "C" int usaf_hip_overlay_scatter(void* base, int32_t dtype, int64_t numel, const int64_t* idx,

@@ -110,7 +110,131 @@ class Q4Tensor:
 
 
 # grad-input GEMMs on the transposed copies: shapes and expert counts they serve
-_T_MAX_E = 512
+_T_MAX_E = 256
+
+
+# ---------------------------------------------------------------------------
+# overlays: trained values over the 4-bit weights
+# ---------------------------------------------------------------------------
+
+# the four fused 4-bit GEMMs and how each reads its weight W [E, R, C]:
+#   gate_up_fwd  W = gate_up, output column n = row r (gate rows r < I pair with up rows I + r), k = column
+#   down_fwd     W = down,    n = r, k = c
+#   down_bwd     W = down^T (transposed copy), n = c, k = r
+#   gate_up_bwd  W = gate_up^T,                n = c, k = r
+_OVL_KINDS = {"gate_up": ("gate_up_fwd", "gate_up_bwd"), "down": ("down_fwd", "down_bwd")}
+_OVL_CAP = 64  # entries per (wave, k-step, 32-row column block): one 16-bit LDS store per lane
+
+
+def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
+    """Where each flat position ``idx`` of an expert tensor ``shape`` = [E, R, C]
+    sits in the fused GEMM ``kind``'s weight fragments, as the entry tables of
+    usaf_hip_moe_*(overlay=...) name it.  Returns (word int32 [n], byte offset
+    int32 [n], table words).
+
+    The GEMM's tile unit u = (e * n_nt + nt) * 4 + w is wave w of n-tile nt of
+    expert e; the wave holds 64 weight rows as two 32-row column blocks cb, and
+    per k-step of 64 contraction elements lane l32 + 32 h holds k = 32 h + 8 j +
+    [0, 8) of row 32 cb + l32 as fragment registers j = 0..3.  The fragment
+    image a lane writes puts register j at byte (64 j + lane) * 16, so the weight
+    at k-step offset kk = 32 h + 8 j + 2 q + b (b: low or high half of dword q)
+    sits at byte (64 j + l32 + 32 h) * 16 + 4 q + 2 b.  Entries of one
+    (u, k-step, cb) are ranked in position order; rank r goes to word
+    ((u * nk + ks) * 128) + 2 r + cb.  More than 64 positions in one 32 x 64 block
+    of a wave (3 % local density) raise ValueError."""
+    E, R, C = (int(d) for d in shape)
+    idx = idx.reshape(-1).to(torch.int64)
+    e = torch.div(idx, R * C, rounding_mode="floor")
+    rc = idx - e * (R * C)
+    r = torch.div(rc, C, rounding_mode="floor")
+    c = rc - r * C
+    if kind == "gate_up_fwd":
+        n, k, K = r, c, C
+        cb = (n >= inter).to(torch.int64)
+        g = n - cb * inter
+        n_nt = (inter + 127) // 128
+        nt = torch.div(g, 128, rounding_mode="floor")
+        w = torch.div(g % 128, 32, rounding_mode="floor")
+        l32 = g % 32
+    else:
+        if kind == "down_fwd":
+            n, k, N, K = r, c, R, C
+        elif kind in ("down_bwd", "gate_up_bwd"):
+            n, k, N, K = c, r, C, R
+        else:
+            raise ValueError(f"unknown overlay kind {kind!r}")
+        n_nt = (N + 255) // 256
+        nt = torch.div(n, 256, rounding_mode="floor")
+        w = torch.div(n % 256, 64, rounding_mode="floor")
+        cb = torch.div(n % 64, 32, rounding_mode="floor")
+        l32 = n % 32
+    if K % 128:
+        raise ValueError(f"overlay: contraction length {K} is not a multiple of 128")
+    nk = K // 64
+    ks = torch.div(k, 64, rounding_mode="floor")
+    kk = k % 64
+    lane = l32 + 32 * torch.div(kk, 32, rounding_mode="floor")
+    j = torch.div(kk % 32, 8, rounding_mode="floor")
+    off = (64 * j + lane) * 16 + 4 * torch.div(kk % 8, 2, rounding_mode="floor") + 2 * (kk % 2)
+    group = ((e * n_nt + nt) * 4 + w) * nk + ks
+    key = group * 2 + cb
+    order = torch.argsort(key, stable=True)
+    sk = key[order]
+    first = torch.searchsorted(sk, sk)  # start of each key's run
+    rank_sorted = torch.arange(sk.numel(), device=sk.device) - first
+    rank = torch.empty_like(rank_sorted)
+    rank[order] = rank_sorted
+    if rank.numel() and int(rank.max()) >= _OVL_CAP:
+        raise ValueError(f"overlay ({kind}): more than {_OVL_CAP} trained positions in one 32 x 64 weight block; "
+                         f"use dense expert weights with overlay_scatter for such masks")
+    word = group * 128 + 2 * rank + cb
+    n_words = E * n_nt * 4 * nk * 128
+    return word.to(torch.int32), off.to(torch.int32), n_words
+
+
+class Q4Overlay:
+    """Trained values at a fixed set of flat positions of one 4-bit expert
+    tensor, held as the entry tables the fused GEMMs read: the reference's
+    overlay scatter of the optimizer masters into its fp16 expert weights
+    (usaf/moe_loader.py:218-221, 425-443 sync_resident; train.py:666) without
+    materialising the weights.  ``role`` is "gate_up" or "down"; the tables
+    (forward and grad-input GEMM) are built for one activation dtype.
+    ``refresh(values)`` writes new fp32 values (aligned with ``idx``, e.g. the
+    SparseAdam masters) into both tables."""
+
+    def __init__(self, role: str, idx: torch.Tensor, shape, inter: int, dtype: torch.dtype,
+                 values: torch.Tensor):
+        if role not in _OVL_KINDS:
+            raise ValueError(f"overlay role must be 'gate_up' or 'down', got {role!r}")
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError("overlay dtype must be fp16 or bf16 (the activation dtype)")
+        dev = values.device
+        self.role, self.dtype, self.shape = role, dtype, torch.Size(shape)
+        self.n = int(idx.numel())
+        self.tables = {}
+        for kind in _OVL_KINDS[role]:
+            word, off, n_words = overlay_entries(kind, idx.to(dev), shape, inter)
+            table = torch.full((n_words,), 0xFFFF, dtype=torch.int32, device=dev)
+            table[word.long()] = off
+            self.tables[kind] = (table, word, n_words)
+        self.bad = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.refresh(values)
+
+    def table(self, kind: str, dtype: torch.dtype):
+        """(pointer, words) of GEMM ``kind``'s entry table."""
+        if dtype != self.dtype:
+            raise TypeError(f"overlay built for {self.dtype} activations, used with {dtype}")
+        t = self.tables[kind][0]
+        return t.data_ptr(), t.numel()
+
+    def refresh(self, values: torch.Tensor) -> None:
+        """New values (fp32 [n], on the tables' device) into both tables."""
+        v = values.detach().reshape(-1)
+        if v.dtype != torch.float32 or not v.is_contiguous() or v.numel() != self.n:
+            raise ValueError(f"overlay refresh needs {self.n} contiguous fp32 values")
+        (ta, wa, na), (tb, wb, nb) = (self.tables[k] for k in _OVL_KINDS[self.role])
+        N.call("usaf_hip_overlay_refresh", v.data_ptr(), self.n, wa.data_ptr(), ta.data_ptr(), na, wb.data_ptr(),
+               tb.data_ptr(), nb, N.dtype_code(self.dtype), self.bad.data_ptr(), N.stream_ptr(v.device))
 
 
 class ExpertWeights:
@@ -126,10 +250,34 @@ class ExpertWeights:
         if len(gs) != 3 or len(ds) != 3 or gs[0] != ds[0] or gs[2] != ds[1] or gs[1] != 2 * ds[2]:
             raise ValueError(f"expert shapes do not form gate_up [E,2I,H] / down [E,H,I]: {tuple(gs)}, {tuple(ds)}")
         self.E, self.H, self.I = int(gs[0]), int(gs[2]), int(ds[2])
+        self.overlays: dict = {}  # "gate_up" / "down" -> Q4Overlay
 
     @property
     def is_q4(self) -> bool:
         return isinstance(self.gate_up, Q4Tensor)
+
+    def set_overlay(self, which: str, idx: torch.Tensor, values: torch.Tensor, dtype: torch.dtype) -> "Q4Overlay":
+        """Trained values ``values`` (fp32) at flat positions ``idx`` of the 4-bit
+        tensor ``which`` ("gate_up" / "down"), seen by every fused GEMM from now on
+        (Q4Overlay; refresh its values after each optimizer step)."""
+        w = self.gate_up if which == "gate_up" else self.down
+        if not isinstance(w, Q4Tensor) or not w.fused_ok():
+            raise NotImplementedError("overlays apply to 4-bit weights on the fused GEMMs; scatter dense weights "
+                                      "with overlay_scatter instead")
+        ov = Q4Overlay(which, idx, w.shape, self.I, dtype, values)
+        self.overlays[which] = ov
+        return ov
+
+    def clear_overlay(self, which: Optional[str] = None) -> None:
+        if which is None:
+            self.overlays.clear()
+        else:
+            self.overlays.pop(which, None)
+
+    def _ovl(self, kind: str, dtype: torch.dtype):
+        """(entry table pointer, words) of GEMM ``kind`` (overlay_entries), or (None, 0)."""
+        ov = self.overlays.get("gate_up" if kind.startswith("gate_up") else "down")
+        return (None, 0) if ov is None else ov.table(kind, dtype)
 
     def _ptrs_t(self, which):
         """(codes, scale/zero) pointers of the transposed 4-bit copy for the
@@ -352,10 +500,10 @@ class RoutedExpertsFn(torch.autograd.Function):
             _gemm_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
                        S, E, I, q, sz, w16, code, gu.data_ptr(), act.data_ptr(),
                        None if act_blk is None else act_blk.data.data_ptr(),
-                       None if act_blk is None else b.blk_table.data_ptr(), st)
+                       None if act_blk is None else b.blk_table.data_ptr(), *ew._ovl("gate_up_fwd", dt), st)
             q, sz, w16 = ew._ptrs("down", dt)
             _gemm_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
-                       code, y.data_ptr(), st)
+                       code, y.data_ptr(), *ew._ovl("down_fwd", dt), st)
         out = combine(y, weights, b.pair_slot, dt)
         ctx.ew = ew
         ctx.capture = capture
@@ -404,8 +552,9 @@ class RoutedExpertsFn(torch.autograd.Function):
         tq = ew._ptrs_t("down")
         if tq is not None:
             _gemm_call("usaf_hip_moe_down_bwd_t", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
-                       *tq, code, dgu.data_ptr(), st)
+                       *tq, code, dgu.data_ptr(), *ew._ovl("down_bwd", dt), st)
         else:
+            _no_overlay(ew, "down")
             q, sz, w16 = ew._ptrs("down", dt)
             _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
                        q, sz, w16, code, dgu.data_ptr(), st)
@@ -418,8 +567,9 @@ class RoutedExpertsFn(torch.autograd.Function):
         tq = ew._ptrs_t("gate_up")
         if tq is not None:
             _gemm_call("usaf_hip_moe_gate_up_bwd_t", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *tq,
-                       code, dx_slots.data_ptr(), st)
+                       code, dx_slots.data_ptr(), *ew._ovl("gate_up_bwd", dt), st)
         else:
+            _no_overlay(ew, "gate_up")
             q, sz, w16 = ew._ptrs("gate_up", dt)
             _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
                        code, dx_slots.data_ptr(), st)
@@ -429,6 +579,12 @@ class RoutedExpertsFn(torch.autograd.Function):
             _dense_weight_grad(d_wgu, dgu, hs, b.token_idx, b)
         dhs = combine(dx_slots, None, b.pair_slot, dt)
         return dhs, dweights, None, None, d_wgu, d_wdn, None
+
+
+def _no_overlay(ew: ExpertWeights, which: str) -> None:
+    if which in ew.overlays:
+        raise NotImplementedError(f"the grad-input GEMM of {which} with an overlay needs the transposed 4-bit copy "
+                                  f"(E <= {_T_MAX_E}, rows % 64 == 0 and the GEMM's N, K multiples of 128)")
 
 
 def _dense_weight_grad(out: torch.Tensor, dy: torch.Tensor, x: torch.Tensor, x_rows: Optional[torch.Tensor],
