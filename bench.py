@@ -155,6 +155,12 @@ def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfl
                                            requires_grad=False)
     store = SparseGradStore(active, shapes, device=dev)
     opt = SparseAdam(masters, active_idx=active, lr=2e-4, weight_decay=0.005, compact_params=True)
+    # the masters are what the next forward multiplies: the reference scatters them into
+    # its fp16 expert weights after every optimizer step (train.py:666 sync_resident);
+    # here the fused 4-bit GEMMs read them through overlay tables refreshed after each step
+    overlays = {full: experts.set_overlay(full.rsplit(".", 1)[1].replace("_proj", ""), active[full],
+                                          masters[full].data, dtype)
+                for full in active}
     hs = torch.randn(T, H, device=dev, generator=gen).to(dtype).requires_grad_(True)
     router_w = (torch.randn(E, H, device=dev, generator=gen) / H ** 0.5).to(dtype).requires_grad_(True)
     # torch.optim.SGD(momentum=0.9) semantics (train.py:493-498) as one fused kernel
@@ -162,7 +168,14 @@ def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfl
     dy = torch.randn(T, H, device=dev, generator=gen).to(dtype)
     n_act = {n.rsplit(".", 1)[1]: int(i.numel()) for n, i in active.items()}
     return dict(experts=experts, store=store, opt=opt, hs=hs, router_w=router_w, sgd=sgd, dy=dy, k=k,
-                prefix=prefix, T=T, H=H, I=I, E=E, n_act=n_act, active=active)
+                prefix=prefix, T=T, H=H, I=I, E=E, n_act=n_act, active=active, masters=masters, overlays=overlays)
+
+
+def sync_overlays(L) -> None:
+    """The masters into the overlay tables the next GEMMs read (the reference's
+    per-step sync_resident, usaf/moe_loader.py:425-443, train.py:666)."""
+    for name, ov in L["overlays"].items():
+        ov.refresh(L["masters"][name].data)
 
 
 def _fwd_bwd_check(L, finite, overflow, slot: int = 0) -> dict:
@@ -210,6 +223,7 @@ def moe_train_step_sync(L) -> bool:
     if finite:
         L["sgd"].step()
         L["opt"].step(compact_grads=cg)
+        sync_overlays(L)
     return bool(finite)
 
 
@@ -218,12 +232,12 @@ class LaggedSteps:
     step n's finite flag, so the GPU never idles on that read.
 
     Each step launches forward + backward + finite check into its own flag slot
-    (two slots, alternating), the router's SGD step gated on the device by that
-    flag and by a sticky halt flag (capacity-mode bucketing sets it on overflow),
-    and an async copy of both flags to pinned host memory.  After launching step
-    n + 1 the host reads step n's flags and, if the step was finite, launches its
-    SparseAdam update: on the same stream, behind step n + 1's work, which reads
-    neither the masters nor the moments it updates.
+    (two slots, alternating), then the router's SGD step and SparseAdam, both
+    gated on the device by that flag and by a sticky halt flag (capacity-mode
+    bucketing sets it on overflow), the refresh of the overlay tables from the
+    masters (the next forward reads them), and an async copy of both flags to
+    pinned host memory.  After launching step n + 1 the host reads step n's
+    flags to count it.
     An overflow halts every gated update from that step on; the host recomputes
     the step with exact bucketing, applies it and relaunches the step after it.
     The updates applied, and their order, are those of moe_train_step_sync."""
@@ -247,6 +261,8 @@ class LaggedSteps:
         self.host[i].copy_(f, non_blocking=True)
         self.events[i].record()
         self.L["sgd"].step(finite=f[:1], halt=self.halt)
+        self.L["opt"].step(compact_grads=self.cg[i], finite=f[:1], halt=self.halt)
+        sync_overlays(self.L)
 
     def _resolve(self, j: int, relaunch=None) -> None:
         self.events[j].synchronize()
@@ -261,10 +277,11 @@ class LaggedSteps:
             finite = f.tolist()[0]
             if finite:
                 self.L["sgd"].step()
+                self.L["opt"].step(compact_grads=self.cg[j])
+                sync_overlays(self.L)
             if relaunch is not None:
-                self._launch(relaunch)  # the step after j, on the updated router weight
+                self._launch(relaunch)  # the step after j, on the updated weights
         if finite:
-            self.L["opt"].step(compact_grads=self.cg[j])
             self.applied += 1
         else:
             self.skipped += 1

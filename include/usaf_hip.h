@@ -303,7 +303,7 @@ int usaf_hip_moe_gate_up_bwd(const void* dgu, int64_t I, const int32_t* offsets,
  * of W_down [E, H, I] -> [E, I, H], of W_gate_up [E, 2I, H] -> [E, H, 2I]); same
  * results up to fp32 summation order.  Replace the same autograd steps
  * (qwen3moe_dml.py:58-61).  down_bwd_t needs I % 128 == 0 and H % 128 == 0;
- * gate_up_bwd_t needs H % 128 == 0 and I % 64 == 0; both E <= 256. */
+ * gate_up_bwd_t needs H % 128 == 0 and I % 64 == 0; both E <= 255. */
 int usaf_hip_moe_down_bwd_t(const void* dcur, int64_t H, const void* gu, const int32_t* offsets, int64_t S, int64_t E,
                             int64_t I, const int8_t* wq_t, const uint32_t* wsz_t, int32_t dtype, void* dgu,
                             const uint32_t* overlay, int64_t overlay_words, void* stream);
@@ -323,22 +323,28 @@ int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offset
  * USAF_ERR_INVALID): for each (expert e, n-tile nt, wave w in 0..3) unit u = (e * n_nt + nt)
  * * 4 + w and each k-step ks (64 contraction elements; n_nt = ceil(I / 128) for
  * gate_up_fwd, else ceil(N / 256)), 128 uint32 words at ((u * K / 64 + ks) * 128):
- * word 2 r + cb is entry r (< 64) of the wave's 32-row column block cb,
- * {byte offset of the weight in the wave's 4 KiB fragment image | value << 16},
- * offset >= 4096 for an unused word.  The Python layer (usaf_amd/moe.py
+ * word 32 j + r is entry r (< 32) of the wave's fragment register j (lanes
+ * 16 j..16 j + 15 store them): {byte offset | value << 16}, the offset into the
+ * 2 KiB image of register j, which holds lane l's copy of column block cb (the
+ * wave's weight rows 32 cb + l % 32, k = 32 (l / 32) + 8 j + [0, 8) of the
+ * k-step) at byte (64 cb + l) * 16, element k at 2 (k % 8) within it; unused
+ * words hold an offset in [2048, 4096) (a scratch area of the wave's LDS
+ * epilogue tile).  The Python layer (usaf_amd/moe.py overlay_entries,
  * Q4Overlay) builds the tables once per set of positions.  A GEMM with an overlay
  * runs the 4-bit LDS-DMA kernel only (NotImplemented otherwise).
  *
- * usaf_hip_overlay_refresh writes new values into one or two such tables:
- * word words_a[i] of table_a (words_b[i] of table_b) takes the 16-bit `dtype`
- * (fp16 or bf16) value of fp16(p[i]) -- the reference's fp16 weight after the
- * scatter -- in its high half.  Words outside [0, n_words) set *bad_flag
- * (optional) and are skipped.  Replaces the per-step master scatter of
- * moe_loader.py:425-443 (sync_resident) for weights the fused GEMMs read.
+ * usaf_hip_overlay_refresh writes new values into one or two such tables: for
+ * j < n, word words_a[j] of table_a takes the 16-bit `dtype` (fp16 or bf16)
+ * value of fp16(p[index_a[j]]) -- the reference's fp16 weight after the
+ * scatter -- in its high half (index_a NULL: p[j]); likewise words_b, index_b,
+ * table_b.  Ordering j by word keeps each table's writes together.  Words
+ * outside [0, n_words) or indices outside [0, n) set *bad_flag (optional) and
+ * are skipped.  Replaces the per-step master scatter of moe_loader.py:425-443
+ * (sync_resident) for weights the fused GEMMs read.
  */
-int usaf_hip_overlay_refresh(const float* p, int64_t n, const int32_t* words_a, uint32_t* table_a, int64_t n_words_a,
-                             const int32_t* words_b, uint32_t* table_b, int64_t n_words_b, int32_t dtype,
-                             int32_t* bad_flag, void* stream);
+int usaf_hip_overlay_refresh(const float* p, int64_t n, const int32_t* words_a, const int32_t* index_a,
+                             uint32_t* table_a, int64_t n_words_a, const int32_t* words_b, const int32_t* index_b,
+                             uint32_t* table_b, int64_t n_words_b, int32_t dtype, int32_t* bad_flag, void* stream);
 
 /* ---- sparse gradient path and optimizer ----------------------------------- */
 
@@ -432,6 +438,23 @@ int usaf_hip_topk_abs(const void* x, int32_t dtype, int64_t n, int64_t k, int64_
  */
 int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, float* v, int64_t n, double lr, double beta1,
                               double beta2, double eps, double weight_decay, int64_t step, void* stream);
+
+/* usaf_hip_sparse_adam_step gated on the device, for training loops that launch
+ * the update before the host has read the step's finite flag (train.py:649-672
+ * applies SparseAdam only to finite steps): the update is skipped unless
+ * finite[0] != 0 and halt[0] == 0 (either pointer may be NULL = open).  The
+ * step number is t = step_count[0] + 1, where step_count (int32, device) is the
+ * number of steps applied so far; its bias corrections are bias_table[2 (t - 1)]
+ * = fp32(1 - beta1^t) and bias_table[2 (t - 1) + 1] = fp32(1 - beta2^t),
+ * computed by the caller in double as the reference's Python scalars are.
+ * t > table_steps skips the update and sets *bad_flag (optional).
+ * usaf_hip_count_step advances step_count by one under the same gate; call it
+ * once after all of a step's gated launches. */
+int usaf_hip_sparse_adam_step_gated(float* p, const float* grad, float* m, float* v, int64_t n, double lr, double beta1,
+                                    double beta2, double eps, double weight_decay, const int32_t* finite,
+                                    const int32_t* halt, const int32_t* step_count, const float* bias_table,
+                                    int64_t table_steps, int32_t* bad_flag, void* stream);
+int usaf_hip_count_step(const int32_t* finite, const int32_t* halt, int32_t* step_count, void* stream);
 
 /* torch.optim.SGD.step with momentum (dampening 0, no Nesterov) for one tensor, the
  * router's optimizer in the reference trainer (train.py:493-498, 667-672):

@@ -3,7 +3,11 @@ finite flag (LaggedSteps), against the same steps in the reference loop's order
 (train.py:649-672: read the flag, then step the optimizers; moe_train_step_sync):
 identical parameters, optimizer state and step counts, through a non-finite
 step (skipped) and a routing that overflows the static slot capacity
-(recomputed with exact bucketing)."""
+(recomputed with exact bucketing).  The lagged loop gates SparseAdam on the
+device (step count and bias corrections on the GPU); the synchronous loop
+steps it from the host.  Both refresh the overlay tables of the fused GEMMs
+from the masters after each applied step, so every forward after the first
+multiplies trained weights."""
 import pytest
 import torch
 
@@ -34,7 +38,7 @@ def _set_dy(L, dy0, step, nan_step):
 
 def _state(L):
     opt = L["opt"]
-    out = {"router_w": L["router_w"].detach().clone(), "sgd_buf": L["sgd"]._buf[0].clone(), "adam_step": opt._step}
+    out = {"router_w": L["router_w"].detach().clone(), "sgd_buf": L["sgd"]._buf[0].clone(), "adam_step": opt.step_count}
     for n in opt._active_ids:
         out[f"master:{n}"] = opt._named[n].detach().clone()
         out[f"m:{n}"] = opt._m[n].clone()

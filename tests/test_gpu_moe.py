@@ -383,6 +383,38 @@ def test_sparse_adam_vs_oracle(gpu_device):
     assert rel_err(opt._v["w"], v_ref) <= 1e-6
 
 
+def test_sparse_adam_device_gate(gpu_device):
+    """Gated on the device (finite / halt flags, GPU step count and bias table):
+    the same parameters and moments as the host-stepped optimizer that skips the
+    same steps, and the count of applied steps."""
+    _say("SparseAdam gated on the device: 5 launches, one non-finite, one halted")
+    n = 100_003
+    g = torch.Generator().manual_seed(8)
+    p0 = torch.randn(n, generator=g) * 0.02
+    grads = [torch.randn(n, generator=g).to(gpu_device) * 1e-3 for _ in range(5)]
+    gates = [(1, 0), (1, 0), (0, 0), (1, 1), (1, 0)]  # (finite, halt) per launch
+    host = torch.nn.Parameter(p0.clone().to(gpu_device), requires_grad=False)
+    dev_p = torch.nn.Parameter(p0.clone().to(gpu_device), requires_grad=False)
+    kw = dict(lr=2e-4, weight_decay=0.005, compact_params=True)
+    A = SparseAdam({"w": host}, active_idx={"w": torch.arange(n)}, **kw)
+    B = SparseAdam({"w": dev_p}, active_idx={"w": torch.arange(n)}, **kw)
+    for grad, (fin, halt) in zip(grads, gates):
+        if fin and not halt:
+            A.step(compact_grads={"w": grad})
+        f = torch.tensor([fin], dtype=torch.int32, device=gpu_device)
+        h = torch.tensor([halt], dtype=torch.int32, device=gpu_device)
+        B.step(compact_grads={"w": grad}, finite=f, halt=h)
+    torch.cuda.synchronize()
+    assert B.step_count == A.step_count == 3
+    assert int(B.bad.item()) == 0
+    assert torch.equal(dev_p, host) and torch.equal(B._m["w"], A._m["w"]) and torch.equal(B._v["w"], A._v["w"])
+    # an ungated call after gated ones keeps using (and advancing) the device count
+    B.step(compact_grads={"w": grads[0]})
+    A.step(compact_grads={"w": grads[0]})
+    torch.cuda.synchronize()
+    assert B.step_count == 4 and torch.equal(dev_p, host)
+
+
 def test_sparse_adam_full_params(gpu_device):
     _say("SparseAdam compact_params=False")
     p = torch.nn.Parameter(torch.ones(10, device=gpu_device))

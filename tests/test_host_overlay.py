@@ -5,7 +5,7 @@ the fused 4-bit GEMM kernel gives that weight.
 The brute force walks the kernel's own assignment forward -- tile unit
 (expert, n-tile, wave) -> column block cb and lane -> weight row (wrow of
 moe_gemm_q4_kernel) and k-step -> fragment register j, dword q, half b -> byte
-(64 j + lane) * 16 + 4 q + 2 b of the wave's image -- and the table builder,
+(64 cb + lane) * 16 + 4 q + 2 b of register j's image -- and the table builder,
 which inverts it, must agree position by position."""
 import itertools
 
@@ -16,7 +16,7 @@ from usaf_amd.moe import _OVL_CAP, overlay_entries
 
 
 def kernel_assignment(kind, E, R, C, inter):
-    """{(e, row, col) of W: (unit group key, column block, image byte offset)}
+    """{(e, row, col) of W: (unit group key, fragment register, image byte offset)}
     enumerated the way the kernel fills its fragments."""
     if kind == "gate_up_fwd":
         N, K, n_nt = inter, C, (inter + 127) // 128
@@ -40,10 +40,10 @@ def kernel_assignment(kind, E, R, C, inter):
         for ks, h, j, q, hb in itertools.product(range(nk), range(2), range(4), range(4), range(2)):
             k = ks * 64 + 32 * h + 8 * j + 2 * q + hb
             lane = l32 + 32 * h
-            off = (64 * j + lane) * 16 + 4 * q + 2 * hb
+            off = (64 * cb + lane) * 16 + 4 * q + 2 * hb
             r, c = (n_row, k) if kind in ("gate_up_fwd", "down_fwd") else (k, n_row)
             unit = (e * n_nt + nt) * 4 + w
-            out[(e, r, c)] = (unit * nk + ks, cb, off)
+            out[(e, r, c)] = (unit * nk + ks, j, off)
     return out
 
 
@@ -59,28 +59,28 @@ def test_entries_match_kernel_fragments(kind, shape, inter):
     assert len(ref) == E * R * C  # every weight is held exactly once
     g = torch.Generator().manual_seed(5)
     numel = E * R * C
-    idx = torch.randperm(numel, generator=g)[: numel // 50].sort().values
+    idx = torch.randperm(numel, generator=g)[: numel // 100].sort().values
     word, off, n_words = overlay_entries(kind, idx, shape, inter)
     assert word.min() >= 0 and word.max() < n_words
     assert len(set(word.tolist())) == idx.numel()  # one word per position
     for f, wd, o in zip(idx.tolist(), word.tolist(), off.tolist()):
         e, rem = divmod(f, R * C)
         r, c = divmod(rem, C)
-        group, cb, want_off = ref[(e, r, c)]
-        assert wd // 128 == group and wd % 2 == cb and o == want_off, (kind, e, r, c)
-    # ranks: the positions of one (group, column block) take words 0, 1, ... in position order
-    seen = {}
-    for wd in word.tolist():
-        key = (wd // 128, wd % 2)
-        seen[key] = seen.get(key, 0) + 1
-    for wd in word.tolist():
-        assert (wd % 128) // 2 < seen[(wd // 128, wd % 2)]
+        group, j, want_off = ref[(e, r, c)]
+        assert wd // 128 == group and (wd % 128) // 32 == j and o == want_off, (kind, e, r, c)
+    # ranks: the positions of one (group, register) take words 32 j + 0, 1, ... in position order
+    prev = {}
+    for f, wd in zip(idx.tolist(), word.tolist()):
+        key = (wd // 128, (wd % 128) // 32)
+        assert wd % 32 == prev.get(key, -1) + 1
+        prev[key] = wd % 32
 
 
 def test_entries_reject_dense_blocks():
-    # one 32-row x 64-k block of a wave holds 2048 weights; 65 trained positions in it overflow
+    # fragment register 0 of a wave covers k = 0..7 and 32..39 of its 64 rows (1024
+    # weights); 33 trained positions in it overflow, 32 fit
     shape = (1, 256, 128)
-    idx = torch.tensor(sorted(r * 128 + k for r in range(32) for k in range(3)))[: _OVL_CAP + 1]
+    idx = torch.tensor(sorted(r * 128 + k for r in range(64) for k in (0, 33)))[: _OVL_CAP + 1]
     with pytest.raises(ValueError, match="more than"):
         overlay_entries("down_fwd", idx, shape, 128)
-    overlay_entries("down_fwd", idx[:_OVL_CAP], shape, 128)  # 64 fit
+    overlay_entries("down_fwd", idx[:_OVL_CAP], shape, 128)

@@ -78,9 +78,12 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_sddmm_masked": [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p,
                               _c_p],
     "usaf_hip_sparse_adam_step": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_d, _c_d, _c_d, _c_d, _c_i64, _c_p],
+    "usaf_hip_sparse_adam_step_gated": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_d, _c_d, _c_d, _c_d, _c_p, _c_p, _c_p,
+                                        _c_p, _c_i64, _c_p, _c_p],
+    "usaf_hip_count_step": [_c_p, _c_p, _c_p, _c_p],
     "usaf_hip_scale_check": [_c_p, _c_p, _c_i64, _c_f32, _c_p, _c_p],
     "usaf_hip_overlay_scatter": [_c_p, _c_i32, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p],
-    "usaf_hip_overlay_refresh": [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i32, _c_p, _c_p],
+    "usaf_hip_overlay_refresh": [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p, _c_p],
 }
 # entry points that return a value instead of a status
 _VALUE_FUNCS: dict[str, tuple] = {

@@ -1139,34 +1139,36 @@ __global__ __launch_bounds__(NK_THREADS) void moe_gemm_nk_kernel(const GemmArgs 
 // steps and epilogue.
 // =====================================================================================
 constexpr int Q_BM = 256, Q_BN = 256, Q_THREADS = 256;
-constexpr int Q_MAX_E = 256;
+constexpr int Q_MAX_E = 255;
 constexpr int Q_A_BYTES = Q_BM * BK * 2;                 // activation rows of one k-step
 constexpr int Q_C_BYTES = Q_BN * BK / 2;                 // codes of one k-step
 constexpr int Q_Z_BYTES = Q_BN * 4;                      // scale|zero pairs of one k-step
-constexpr int Q_STAGE = Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES;
+constexpr int Q_O_BYTES = 4 * 128 * 4;                  // overlay entries of one k-step (4 waves x 128 words)
+constexpr int Q_STAGE = Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES + Q_O_BYTES;
 constexpr int Q_A_LOADS = Q_A_BYTES / (16 * Q_THREADS);  // 8 x 16 B per thread
 constexpr int Q_DMAS = 3 + Q_A_LOADS;                    // DMA instructions per thread per k-step
 constexpr int Q_OVL_DMAS = 2;                            // + overlay entries of one k-step (2 x 256 B per wave)
 // Overlay (trained values over the 4-bit weights): per wave and k-step one
-// group of 128 entries (64 per 32-row column block), each a 32-bit word
-// {byte offset into the wave's 4 KiB fragment image | value << 16}; an offset
-// >= 4096 marks an unused entry.  Two groups per wave are in LDS at a time.
+// group of 128 entries, each a 32-bit word {byte offset | value << 16}.  Lane l
+// holds words 2 l and 2 l + 1: entries of fragment register j = l / 16, with
+// offsets into that register's 2 KiB image (both column blocks); unused words
+// point into [2048, 4096) of the wave's epilogue tile, which the k-steps do not
+// read.  The entries travel with the codes of their k-step, in the same stage.
 constexpr int Q_OVL_GROUP = 128 * 4;                     // bytes of one wave's entries per k-step
-constexpr int Q_IMG_BYTES = 64 * 4 * 16;                 // one column block of a wave's weight fragments
-// Dynamic LDS (the DMA targets): 3 stages | s_h, s_l, s_off tables | token rows
-// [2][Q_BM] | overlay entries [4 waves][2][Q_OVL_GROUP].
+constexpr int Q_IMG_J = 2 * 64 * 16;                     // one fragment register of both column blocks
+// Dynamic LDS (the DMA targets): 3 stages | s_h, s_l, s_off tables | token rows [2][Q_BM].
+// A stage: activations | codes | scale|zero words | overlay entries.
 // The epilogue tiles are a separate static array: the compiler then knows that
 // their stores cannot collide with DMA writes still in flight and does not
 // drain the DMAs before them.
 constexpr int Q_TAB_OFF = 3 * Q_STAGE;
 constexpr int Q_TOK_OFF = Q_TAB_OFF + 3 * (Q_MAX_E + 1) * 4;
-constexpr int Q_OVL_OFF = Q_TOK_OFF + 2 * Q_BM * 4;
-constexpr size_t kQSmemBytes = (size_t)Q_OVL_OFF + 4 * 2 * Q_OVL_GROUP;
+constexpr size_t kQSmemBytes = (size_t)Q_TOK_OFF + 2 * Q_BM * 4;
 constexpr int Q_EPW = 104;                      // staging row stride, 16-bit elements (96 columns + pad)
 constexpr int Q_EP_ELEMS = 32 * Q_EPW;          // one wave's 32 x 96 staging tile
 static_assert(kQSmemBytes + 4 * Q_EP_ELEMS * 2 <= 160 * 1024, "LDS budget");
 static_assert(4 * Q_EP_ELEMS * 2 >= Q_THREADS * 4, "the prefix scratch lives in the epilogue tiles");
-static_assert(Q_EP_ELEMS * 2 >= Q_IMG_BYTES, "the fragment image of the overlay lives in the wave's epilogue tile");
+static_assert(Q_EP_ELEMS * 2 >= 2 * Q_IMG_J, "the overlay's fragment image and dummy area live in the wave's epilogue tile");
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -1175,11 +1177,13 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 // distinct banks.
 __device__ __forceinline__ int q_swz(int r) { return r & 7; }
 
-__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds_dst, 16, 0, 0);
+// LDS DMA (global_load_lds): lane l's 16 (4) bytes at base + off land at
+// lds_dst + 16 l (4 l); base and lds_dst are wave-uniform.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(base) + off, (lds_void_ptr)lds_dst, 16, 0, 0);
 }
-__device__ __forceinline__ void dma4(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds_dst, 4, 0, 0);
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(base) + off, (lds_void_ptr)lds_dst, 4, 0, 0);
 }
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -1192,12 +1196,13 @@ struct QTile {
 // z(k) | z(k+1) << 16} pairs from wsz (one 128-column group of n per 256 B per k-step).
 // OVL: trained values replace some of the dequantized weights (the reference's
 // overlay scatter into the fp16 weights, usaf/moe_loader.py:218-221, 425-443).
-// The entries of a k-step ride the activation stream (two more DMAs per step,
-// into the wave's own LDS slots).  After a wave has dequantized a k-step into
-// its fragment registers, it writes each 32-row column block of them to an
-// image in its epilogue tile, stores the entries' values over it (one 16-bit
-// LDS store per lane) and reads the fragments back: every weight the MFMAs see
-// is then the trained value where an entry names it.
+// The entries of a k-step ride the code stream (two more DMAs per step, into
+// the code stage).  As soon as a wave has dequantized fragment register j of
+// the next k-step (both column blocks), it writes the two registers to a 2 KiB
+// image in its epilogue tile, stores over it the values of its entries that
+// fall in register j (16-bit LDS stores) and reads the registers back, four
+// such round trips spread over the k-step's MFMA regions: every weight the
+// MFMAs see is then the trained value where an entry names it.
 template <int EPI, int DT, bool BT, bool OVL>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
@@ -1269,7 +1274,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   int a_ord = 0, a_kt = 0;
   bool a_enter = false;                       // entered a new tile at the last advance: refresh a_off
   uint32_t a_off[Q_A_LOADS];                  // byte offsets of this thread's chunks at k-step 0
-  uint32_t o_off = 0;                         // OVL: byte offset of this lane's entry word at k-step 0 of the tile
+  uint32_t o_off = 0;                         // OVL: byte offset of this lane's entry word at k-step 0 of the code stream's tile
   const int a_lc = (tid & 7) ^ q_swz(tid >> 3);  // logical chunk of this thread's DMA slot
   const uint32_t lda_b = (uint32_t)g.lda * 2;
   auto c_setup = [&](const QTile& t) {
@@ -1277,6 +1282,11 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     const int64_t base = (int64_t)t.e * g.w_rows;
     c_off0 = (uint32_t)((((base + wrow(t, b0)) * g.K) >> 1) + 16 * (tid & 1));
     c_off1 = (uint32_t)((((base + wrow(t, b1)) * g.K) >> 1) + 16 * (tid & 1));
+    if constexpr (OVL) {
+      // entries of tile unit ((e * n_nt + nt) * 4 + wave): nk groups of Q_OVL_GROUP bytes
+      const uint32_t unit = (uint32_t)(((int64_t)t.e * n_nt + t.nt) * 4 + wave);
+      o_off = unit * (uint32_t)nk * Q_OVL_GROUP + (uint32_t)lane * 4;
+    }
     if constexpr (BT) {
       // thread t fetches word t & 63 of group (tile's first group + ((t >> 6) & 1));
       // threads 128..255 repeat 0..127 into the unused upper half
@@ -1293,16 +1303,10 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   auto tok_fill = [&](const QTile& t, int buf) {
     if (g.a_rows) {
       const int r = tid < t.valid ? tid : t.valid - 1;
-      dma4(g.a_rows + t.m_beg + r, s_tok + buf * Q_BM + wave * 64);
+      dma4(g.a_rows + t.m_beg, (uint32_t)r * 4, s_tok + buf * Q_BM + wave * 64);
     }
   };
   auto a_refresh = [&](int ord) {
-    if constexpr (OVL) {
-      // entries of tile unit ((e * n_nt + nt) * 4 + wave): nk groups of Q_OVL_GROUP bytes
-      const QTile t = decode(ord);
-      const uint32_t unit = (uint32_t)(((int64_t)t.e * n_nt + t.nt) * 4 + wave);
-      o_off = unit * (uint32_t)nk * Q_OVL_GROUP + (uint32_t)lane * 4;
-    }
     if (g.a_rows) {
       const int32_t* src = s_tok + (ord & 1) * Q_BM;
 #pragma unroll
@@ -1319,30 +1323,30 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // one DMA instruction of a k-step: d = 0, 1 the code chunks, 2 the scale|zero
   // word (into stage sc_stage), 3 <= d < Q_DMAS activation chunk d - 3 (into
   // stage sa_stage), OVL: d = Q_DMAS, Q_DMAS + 1 the two halves of the wave's
-  // overlay entries of the activation stream's k-step (into entry slot o_slot)
-  auto dma_one = [&](int d, int sc_stage, int sa_stage, int o_slot) {
+  // overlay entries of the code stream's k-step (into stage sc_stage)
+  auto dma_one = [&](int d, int sc_stage, int sa_stage) {
     sc_stage = uni(sc_stage);
     sa_stage = uni(sa_stage);
     const int c_kt_u = uni(c_kt), a_kt_u = uni(a_kt);
     if (OVL && d >= Q_DMAS) {
       const int h = d - Q_DMAS;
-      uint8_t* so = qsm + Q_OVL_OFF + (wave * 2 + uni(o_slot)) * Q_OVL_GROUP + h * 256;
-      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.ovl) + a_kt_u * Q_OVL_GROUP + h * 256;
-      dma4(base + o_off, so);
+      uint8_t* so = qsm + sc_stage * Q_STAGE + Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES + wave * Q_OVL_GROUP + h * 256;
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.ovl) + c_kt_u * Q_OVL_GROUP + h * 256;
+      dma4(base, o_off, so);
     } else if (d < 2) {
       uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
       const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wq) + c_kt_u * 32;
-      dma16(base + (d ? c_off1 : c_off0), sc + (d * 256 + wave * 64) * 16);
+      dma16(base, d ? c_off1 : c_off0, sc + (d * 256 + wave * 64) * 16);
     } else if (d == 2) {
       uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
       // per k-step: one scale|zero word per weight row, or (BT) 32 k-pairs x 2 words per group
       const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wsz) + (BT ? c_kt_u * 256 : (c_kt_u >> 1) * 4);
-      dma4(base + z_off, sc + Q_C_BYTES + wave * 64 * 4);
+      dma4(base, z_off, sc + Q_C_BYTES + wave * 64 * 4);
     } else {
       const int c = d - 3;
       uint8_t* sa = qsm + sa_stage * Q_STAGE;
       const uint8_t* base = reinterpret_cast<const uint8_t*>(g.A) + a_kt_u * (BK * 2);
-      dma16(base + a_off[c], sa + (c * 256 + wave * 64) * 16);
+      dma16(base, a_off[c], sa + (c * 256 + wave * 64) * 16);
     }
   };
   // start of a k-step: the activation stream picks up the rows of the tile it
@@ -1435,33 +1439,45 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   uint16_t* const sEp = q_ep + wave * Q_EP_ELEMS;
   const uint32_t sEp_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sEp;
 
-  // OVL: the trained values of entry slot `slot` over weight fragment set BSX.
-  // Per column block: the 16 fragment registers go to the image as 4 x 1 KiB
-  // (lane l's 16 bytes of sub-step j at (64 j + l) * 16), one 16-bit store per
-  // lane puts entry l of the block over it, and the fragments are read back.
-  // The stores are explicit ds_write instructions (a compiler-visible LDS store
-  // would make it drain the DMAs in flight first); the LDS operations of one
-  // wave complete in order, so each read sees the stores before it.
-  auto ovl_patch = [&](auto bsx_c, int slot) {
-    constexpr int BSX = decltype(bsx_c)::value;
-    const uint8_t* ent = qsm + Q_OVL_OFF + (wave * 2 + uni(slot)) * Q_OVL_GROUP;
-    const uint32_t e0 = *reinterpret_cast<const uint32_t*>(ent + lane * 8);
-    const uint32_t e1 = *reinterpret_cast<const uint32_t*>(ent + lane * 8 + 4);
+  // OVL: the entries of the wave's next k-step (stage `stage`): this lane's two
+  // words, {byte offset in the 8 KiB fragment image | value << 16}.
+  auto ovl_entries = [&](int stage, uint32_t& e0, uint32_t& e1) {
+    const uint8_t* ent = qsm + uni(stage) * Q_STAGE + Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES + wave * Q_OVL_GROUP;
+    e0 = *reinterpret_cast<const uint32_t*>(ent + lane * 8);
+    e1 = *reinterpret_cast<const uint32_t*>(ent + lane * 8 + 4);
+  };
+  // OVL: fragment register j of set BSX (both column blocks) through the image:
+  // lane l's 16 bytes of column block cb at (64 cb + l) * 16; lanes 16 j..16 j + 15
+  // store their two entries over it (exec narrowed to them inside one asm block,
+  // no branch), and the registers are read back.  The stores are explicit
+  // ds_write instructions (a compiler-visible LDS store would make it drain the
+  // DMAs in flight first); the LDS operations of one wave complete in order, so
+  // the reads see the stores before them.  a0/a1: LDS addresses of the lane's
+  // two entries, d0/d1: their values.
+  auto ovl_patch_j = [&](auto bsx_c, auto j_c, uint32_t a0, uint32_t d0, uint32_t a1, uint32_t d1) {
+    constexpr int BSX = decltype(bsx_c)::value, J = decltype(j_c)::value;
+    constexpr uint32_t lo = J == 0 ? 0x0000FFFFu : (J == 1 ? 0xFFFF0000u : 0u);
+    constexpr uint32_t hi = J == 2 ? 0x0000FFFFu : (J == 3 ? 0xFFFF0000u : 0u);
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int cb = 0; cb < 2; ++cb)
+      asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(sEp_lds + (uint32_t)lane * 16), "v"(wf[BSX][cb][J]),
+                   "i"(cb * 1024)
+                   : "memory");
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\t"
+        "s_mov_b32 exec_lo, %5\n\t"
+        "s_mov_b32 exec_hi, %6\n\t"
+        "s_nop 1\n\t"
+        "ds_write_b16 %1, %2\n\t"
+        "ds_write_b16 %3, %4\n\t"
+        "s_mov_b64 exec, %0"
+        : "=&s"(saved)
+        : "v"(a0), "v"(d0), "v"(a1), "v"(d1), "i"(lo), "i"(hi)
+        : "memory");
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(sEp_lds + (uint32_t)lane * 16), "v"(wf[BSX][cb][j]),
-                     "i"(j * 1024)
-                     : "memory");
-      const uint32_t en = cb ? e1 : e0;
-      const uint32_t off = en & 0xFFFFu;
-      if (off < (uint32_t)Q_IMG_BYTES)
-        asm volatile("ds_write_b16 %0, %1" ::"v"(sEp_lds + off), "v"(en >> 16) : "memory");
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        wf[BSX][cb][j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(sEp) + (64 * j + lane) * 16);
-    }
+    for (int cb = 0; cb < 2; ++cb)
+      wf[BSX][cb][J] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(sEp) + (64 * cb + lane) * 16);
   };
 
   // ---- one k-step: MFMAs of k-step gs (activations in stage s0, weights in
@@ -1481,6 +1497,15 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     u32x4 cq[2], kz[8];
     uint32_t csz[2];
     codes_read(s1, cq, csz, kz);
+    uint32_t oa0 = 0, od0 = 0, oa1 = 0, od1 = 0;
+    if constexpr (OVL) {
+      uint32_t e0, e1;
+      ovl_entries(s1, e0, e1);
+      oa0 = sEp_lds + (e0 & 0xFFFFu);
+      od0 = e0 >> 16;
+      oa1 = sEp_lds + (e1 & 0xFFFFu);
+      od1 = e1 >> 16;
+    }
     const uint8_t* sa = qsm + s0 * Q_STAGE;
     auto frag = [&](int f) -> u32x4 {
       const int i = f % NRB, j = f / NRB;
@@ -1502,27 +1527,44 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       }
 #pragma unroll
       for (int dd = 0; dd < DPR; ++dd)
-        if (r * DPR + dd < QD) dma_one(r * DPR + dd, s0, s2, BS);
+        if (r * DPR + dd < QD) dma_one(r * DPR + dd, s0, s2);
       if (r >= 1) {
+        // the pairs of k-step gs + 1 in register-major order: pair p is half-word
+        // pair q of fragment register j of column block cb
 #pragma unroll
         for (int pp = 0; pp < PPR; ++pp) {
           const int p = (r - 1) * PPR + pp;
           if (p < 32) {
-            const int cb = p >> 4, wd = (p >> 2) & 3, q = p & 3;
+            const int wd = p >> 3, cb = (p >> 2) & 1, q = p & 3;
             uint32_t v;
             if constexpr (BT) {
               f16x2 s2, z2;
-              kz_pair(kz, p & 15, s2, z2);
+              kz_pair(kz, 4 * wd + q, s2, z2);
               v = dq_pair<DT>(cq[cb][wd], q, s2, z2);
             } else {
-              if ((p & 15) == 0) {
-                s2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
-                z2v[cb] = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
+              if (p == 0) {
+#pragma unroll
+                for (int c2 = 0; c2 < 2; ++c2) {
+                  s2v[c2] = __builtin_bit_cast(f16x2, (csz[c2] & 0xFFFFu) * 0x10001u);
+                  z2v[c2] = __builtin_bit_cast(f16x2, (csz[c2] >> 16) * 0x10001u);
+                }
               }
               v = dq_pair<DT>(cq[cb][wd], q, s2v[cb], z2v[cb]);
             }
             asm volatile("" : "+v"(v));  // computed here, next to the MFMAs, not sunk to its first use
             wf[BS ^ 1][cb][wd][q] = v;
+            // register wd of both column blocks complete: its trained values, now
+            if constexpr (OVL) {
+              if ((p & 7) == 7) {  // p is a constant after unrolling: one case survives
+                using BX = std::integral_constant<int, BS ^ 1>;
+                switch (p >> 3) {
+                  case 0: ovl_patch_j(BX{}, std::integral_constant<int, 0>{}, oa0, od0, oa1, od1); break;
+                  case 1: ovl_patch_j(BX{}, std::integral_constant<int, 1>{}, oa0, od0, oa1, od1); break;
+                  case 2: ovl_patch_j(BX{}, std::integral_constant<int, 2>{}, oa0, od0, oa1, od1); break;
+                  default: ovl_patch_j(BX{}, std::integral_constant<int, 3>{}, oa0, od0, oa1, od1); break;
+                }
+              }
+            }
           }
         }
       }
@@ -1530,18 +1572,12 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     }
     advance();
     // this step's 11 DMAs (13 with OVL) may stay in flight; everything older
-    // (the stages the next step reads, the token rows, the entries of k-step
-    // gs + 1) has landed in this wave, and after the barrier in all waves.
-    // sched_barrier keeps the step's register work on its side of the barrier.
+    // (the stages the next step reads, the token rows) has landed in this wave,
+    // and after the barrier in all waves.  sched_barrier keeps the step's
+    // register work on its side of the barrier.
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (OVL) {
-      asm volatile("s_waitcnt vmcnt(13)" ::: "memory");
-      ovl_patch(std::integral_constant<int, BS ^ 1>{}, BS ^ 1);  // k-step gs + 1: entries in slot (gs + 1) & 1
-      __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_barrier" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(11)\n\ts_barrier" ::: "memory");
-    }
+    if constexpr (OVL) asm volatile("s_waitcnt vmcnt(13)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(11)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -1720,7 +1756,8 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     a_refresh(0);
   }
   constexpr int QD = Q_DMAS + (OVL ? Q_OVL_DMAS : 0);
-  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0, 0);  // codes 0
+  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0);  // codes 0
+  for (int d = Q_DMAS; d < QD; ++d) dma_one(d, 0, 0);  // OVL: their entries
   if (nk == 2 && n_my > 1) {                       // the code stream enters tile 1 after codes 1
     c_next = decode(1);
     tok_fill(c_next, 1);
@@ -1734,14 +1771,22 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       c_kt = nk - 1;
     }
   }
-  for (int d = 0; d < QD; ++d) dma_one(d, 1, 0, 0);  // codes 1, activations (and entries) 0
+  for (int d = 0; d < QD; ++d) dma_one(d, 1, 0);  // codes (and entries) 1, activations 0
   advance();
   pre_step();
-  for (int d = 0; d < QD; ++d) dma_one(d, 2, 1, 1);  // codes 2, activations (and entries) 1
+  for (int d = 0; d < QD; ++d) dma_one(d, 2, 1);  // codes (and entries) 2, activations 1
   advance();
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   dequant_all(I0{}, 0);
-  if constexpr (OVL) ovl_patch(I0{}, 0);   // k-step 0: entries in slot 0
+  if constexpr (OVL) {  // k-step 0: its entries are in stage 0
+    uint32_t e0, e1;
+    ovl_entries(0, e0, e1);
+    const uint32_t a0 = sEp_lds + (e0 & 0xFFFFu), d0 = e0 >> 16, a1 = sEp_lds + (e1 & 0xFFFFu), d1 = e1 >> 16;
+    ovl_patch_j(I0{}, std::integral_constant<int, 0>{}, a0, d0, a1, d1);
+    ovl_patch_j(I0{}, std::integral_constant<int, 1>{}, a0, d0, a1, d1);
+    ovl_patch_j(I0{}, std::integral_constant<int, 2>{}, a0, d0, a1, d1);
+    ovl_patch_j(I0{}, std::integral_constant<int, 3>{}, a0, d0, a1, d1);
+  }
   asm volatile("s_barrier" ::: "memory");  // stage 0's codes are refilled by k-step 0
 
   // ---- tiles ----

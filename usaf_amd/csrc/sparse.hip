@@ -496,23 +496,61 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
 //   m = fma(1-b1, g, m*b1)             mul_; add_(alpha=) is one fused multiply-add
 //   v = v*b2 + ((1-b2)*g)*g            mul_; addcmul_ multiplies then adds
 //   p = p + (-lr) * ((m/bias1) / (sqrt(v/bias2) + eps))
+// One element of SparseAdam.step (sparse_optim.py:113-134): L2 decay folded into
+// the gradient, m/v moving averages, bias-corrected update, in the reference's
+// fp32 operation order.
+__device__ __forceinline__ void adam_element(float* __restrict__ p, const float* __restrict__ grad,
+                                             float* __restrict__ m, float* __restrict__ v, int64_t i, float lr,
+                                             float b1, float omb1, float b2, float omb2, float eps, float wd,
+                                             float bias1, float bias2) {
+#pragma clang fp contract(off)
+  float gi = grad[i];
+  const float pi = p[i];
+  if (wd > 0.f) gi = gi + wd * pi;
+  const float mi = __builtin_fmaf(omb1, gi, m[i] * b1);
+  const float vi = v[i] * b2 + (omb2 * gi) * gi;
+  m[i] = mi;
+  v[i] = vi;
+  const float upd = (mi / bias1) / (sqrtf(vi / bias2) + eps);
+  p[i] = pi + (-lr) * upd;
+}
+
 __global__ __launch_bounds__(256) void sparse_adam_kernel(float* __restrict__ p, const float* __restrict__ grad,
                                                           float* __restrict__ m, float* __restrict__ v, int64_t n,
                                                           float lr, float b1, float omb1, float b2, float omb2,
                                                           float eps, float wd, float bias1, float bias2) {
-#pragma clang fp contract(off)
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    float gi = grad[i];
-    const float pi = p[i];
-    if (wd > 0.f) gi = gi + wd * pi;
-    const float mi = __builtin_fmaf(omb1, gi, m[i] * b1);
-    const float vi = v[i] * b2 + (omb2 * gi) * gi;
-    m[i] = mi;
-    v[i] = vi;
-    const float upd = (mi / bias1) / (sqrtf(vi / bias2) + eps);
-    p[i] = pi + (-lr) * upd;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    adam_element(p, grad, m, v, i, lr, b1, omb1, b2, omb2, eps, wd, bias1, bias2);
+}
+
+// The same step gated on the device: skipped unless finite[0] != 0 and
+// halt[0] == 0 (the trainer's finite gate, train.py:649-672, decided without a
+// host read); the step number is count[0] + 1 (count = steps applied so far,
+// advanced by count_step_kernel after the step's launches) and its bias
+// corrections come from the host-computed table bias[2 (t - 1) + {0, 1}].
+__global__ __launch_bounds__(256) void sparse_adam_gated_kernel(
+    float* __restrict__ p, const float* __restrict__ grad, float* __restrict__ m, float* __restrict__ v, int64_t n,
+    float lr, float b1, float omb1, float b2, float omb2, float eps, float wd, const int32_t* __restrict__ finite,
+    const int32_t* __restrict__ halt, const int32_t* __restrict__ count, const float* __restrict__ bias,
+    int64_t bias_steps, int32_t* __restrict__ bad) {
+  if ((finite && *finite == 0) || (halt && *halt != 0)) return;
+  const int64_t t = (int64_t)count[0] + 1;
+  if (t < 1 || t > bias_steps) {
+    if (bad && blockIdx.x == 0 && threadIdx.x == 0) bad[0] = 1;
+    return;
   }
+  const float bias1 = bias[2 * (t - 1)], bias2 = bias[2 * (t - 1) + 1];
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    adam_element(p, grad, m, v, i, lr, b1, omb1, b2, omb2, eps, wd, bias1, bias2);
+}
+
+// count[0] += 1 when the step's gate is open (one thread).
+__global__ void count_step_kernel(const int32_t* __restrict__ finite, const int32_t* __restrict__ halt,
+                                  int32_t* __restrict__ count) {
+  if ((finite && *finite == 0) || (halt && *halt != 0)) return;
+  count[0] = count[0] + 1;
 }
 
 // torch.optim.SGD's single-tensor step with momentum (dampening 0, no Nesterov)
@@ -586,30 +624,38 @@ __global__ __launch_bounds__(256) void overlay_scatter_kernel(uint16_t* __restri
 }
 
 // Trained values into the overlay entries of the fused 4-bit GEMMs: entry word
-// wa[i] of table ta (and wb[i] of tb) takes DT(fp16(p[i])) in its high half --
-// the reference's fp16 weight after the overlay scatter (moe_loader.py:218-221),
-// then the activation dtype, as the GEMMs convert every dequantized weight.
-// Words outside a table set *bad and are skipped.
+// wa[j] of table ta takes DT(fp16(p[ia[j]])) in its high half (likewise wb, ib,
+// tb) -- the reference's fp16 weight after the overlay scatter
+// (moe_loader.py:218-221), then the activation dtype, as the GEMMs convert every
+// dequantized weight.  The caller orders j by word, so that neighbouring
+// threads write neighbouring words and each cache line of a table is written
+// by one burst; ia / ib NULL read p[j].  Words outside a table or indices
+// outside [0, n) set *bad and are skipped.
+template <int DT>
+__device__ __forceinline__ void overlay_put(const float* __restrict__ p, int64_t n, int64_t j,
+                                            const int32_t* __restrict__ w, const int32_t* __restrict__ idx,
+                                            uint16_t* __restrict__ t, int64_t nw, int32_t* __restrict__ bad) {
+  const int64_t i = idx ? (int64_t)idx[j] : j;
+  const int64_t wd = w[j];
+  if (i < 0 || i >= n || wd < 0 || wd >= nw) {
+    if (bad) bad[0] = 1;
+    return;
+  }
+  const uint16_t h = f32_to_f16_bits(p[i]);
+  t[2 * wd + 1] = DT == USAF_F16 ? h : f32_to_bf16_bits(f16_bits_to_f32(h));
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void overlay_refresh_kernel(const float* __restrict__ p, int64_t n,
-                                                              const int32_t* __restrict__ wa, uint16_t* __restrict__ ta,
+                                                              const int32_t* __restrict__ wa,
+                                                              const int32_t* __restrict__ ia, uint16_t* __restrict__ ta,
                                                               int64_t na, const int32_t* __restrict__ wb,
-                                                              uint16_t* __restrict__ tb, int64_t nb,
-                                                              int32_t* __restrict__ bad) {
+                                                              const int32_t* __restrict__ ib, uint16_t* __restrict__ tb,
+                                                              int64_t nb, int32_t* __restrict__ bad) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const uint16_t h = f32_to_f16_bits(p[i]);
-    const uint16_t v = DT == USAF_F16 ? h : f32_to_bf16_bits(f16_bits_to_f32(h));
-    if (ta) {
-      const int64_t w = wa[i];
-      if (w >= 0 && w < na) ta[2 * w + 1] = v;
-      else if (bad) bad[0] = 1;
-    }
-    if (tb) {
-      const int64_t w = wb[i];
-      if (w >= 0 && w < nb) tb[2 * w + 1] = v;
-      else if (bad) bad[0] = 1;
-    }
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += stride) {
+    if (ta) overlay_put<DT>(p, n, j, wa, ia, ta, na, bad);
+    if (tb) overlay_put<DT>(p, n, j, wb, ib, tb, nb, bad);
   }
 }
 
@@ -820,6 +866,27 @@ extern "C" int usaf_hip_sparse_adam_step(float* p, const float* grad, float* m, 
   return check_launch("sparse_adam_step");
 }
 
+extern "C" int usaf_hip_sparse_adam_step_gated(float* p, const float* grad, float* m, float* v, int64_t n,
+                                               double lr, double beta1, double beta2, double eps,
+                                               double weight_decay, const int32_t* finite, const int32_t* halt,
+                                               const int32_t* step_count, const float* bias_table,
+                                               int64_t table_steps, int32_t* bad_flag, void* stream) {
+  if (n < 0 || table_steps < 0) return set_error(USAF_ERR_INVALID, "sparse_adam_step_gated: negative size");
+  if (n == 0) return clear_error();
+  if (!p || !grad || !m || !v || !step_count || !bias_table)
+    return set_error(USAF_ERR_INVALID, "sparse_adam_step_gated: null pointer");
+  sparse_adam_gated_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(
+      p, grad, m, v, n, (float)lr, (float)beta1, (float)(1.0 - beta1), (float)beta2, (float)(1.0 - beta2),
+      (float)eps, (float)weight_decay, finite, halt, step_count, bias_table, table_steps, bad_flag);
+  return check_launch("sparse_adam_step_gated");
+}
+
+extern "C" int usaf_hip_count_step(const int32_t* finite, const int32_t* halt, int32_t* step_count, void* stream) {
+  if (!step_count) return set_error(USAF_ERR_INVALID, "count_step: null pointer");
+  count_step_kernel<<<1, 1, 0, as_stream(stream)>>>(finite, halt, step_count);
+  return check_launch("count_step");
+}
+
 extern "C" int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momentum_buf, int64_t n, int32_t dtype,
                                           double lr, double momentum, double weight_decay, int32_t first_step,
                                           const int32_t* finite, const int32_t* halt, void* stream) {
@@ -859,20 +926,23 @@ extern "C" int usaf_hip_scale_check(const float* in, float* out, int64_t n, floa
   return check_launch("scale_check");
 }
 
-extern "C" int usaf_hip_overlay_refresh(const float* p, int64_t n, const int32_t* words_a, uint32_t* table_a,
-                                        int64_t n_words_a, const int32_t* words_b, uint32_t* table_b,
-                                        int64_t n_words_b, int32_t dtype, int32_t* bad_flag, void* stream) {
+extern "C" int usaf_hip_overlay_refresh(const float* p, int64_t n, const int32_t* words_a, const int32_t* index_a,
+                                        uint32_t* table_a, int64_t n_words_a, const int32_t* words_b,
+                                        const int32_t* index_b, uint32_t* table_b, int64_t n_words_b, int32_t dtype,
+                                        int32_t* bad_flag, void* stream) {
   if (n < 0 || n_words_a < 0 || n_words_b < 0) return set_error(USAF_ERR_INVALID, "overlay_refresh: negative size");
   if (n == 0) return clear_error();
   if (!p || (table_a && !words_a) || (table_b && !words_b))
     return set_error(USAF_ERR_INVALID, "overlay_refresh: null pointer");
   hipStream_t st = as_stream(stream);
   if (dtype == USAF_F16)
-    overlay_refresh_kernel<USAF_F16><<<grid_for(n), 256, 0, st>>>(p, n, words_a, (uint16_t*)table_a, n_words_a,
-                                                                   words_b, (uint16_t*)table_b, n_words_b, bad_flag);
+    overlay_refresh_kernel<USAF_F16><<<grid_for(n), 256, 0, st>>>(p, n, words_a, index_a, (uint16_t*)table_a, n_words_a,
+                                                                   words_b, index_b, (uint16_t*)table_b, n_words_b,
+                                                                   bad_flag);
   else if (dtype == USAF_BF16)
-    overlay_refresh_kernel<USAF_BF16><<<grid_for(n), 256, 0, st>>>(p, n, words_a, (uint16_t*)table_a, n_words_a,
-                                                                    words_b, (uint16_t*)table_b, n_words_b, bad_flag);
+    overlay_refresh_kernel<USAF_BF16><<<grid_for(n), 256, 0, st>>>(p, n, words_a, index_a, (uint16_t*)table_a,
+                                                                    n_words_a, words_b, index_b, (uint16_t*)table_b,
+                                                                    n_words_b, bad_flag);
   else
     return set_error(USAF_ERR_INVALID, "overlay_refresh: dtype must be fp16 or bf16");
   return check_launch("overlay_refresh");

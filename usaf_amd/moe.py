@@ -110,7 +110,7 @@ class Q4Tensor:
 
 
 # grad-input GEMMs on the transposed copies: shapes and expert counts they serve
-_T_MAX_E = 256
+_T_MAX_E = 255
 
 
 # ---------------------------------------------------------------------------
@@ -123,7 +123,7 @@ _T_MAX_E = 256
 #   down_bwd     W = down^T (transposed copy), n = c, k = r
 #   gate_up_bwd  W = gate_up^T,                n = c, k = r
 _OVL_KINDS = {"gate_up": ("gate_up_fwd", "gate_up_bwd"), "down": ("down_fwd", "down_bwd")}
-_OVL_CAP = 64  # entries per (wave, k-step, 32-row column block): one 16-bit LDS store per lane
+_OVL_CAP = 32  # entries per (wave, k-step, fragment register): two 16-bit LDS stores by each of 16 lanes
 
 
 def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
@@ -135,13 +135,14 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     The GEMM's tile unit u = (e * n_nt + nt) * 4 + w is wave w of n-tile nt of
     expert e; the wave holds 64 weight rows as two 32-row column blocks cb, and
     per k-step of 64 contraction elements lane l32 + 32 h holds k = 32 h + 8 j +
-    [0, 8) of row 32 cb + l32 as fragment registers j = 0..3.  The fragment
-    image a lane writes puts register j at byte (64 j + lane) * 16, so the weight
-    at k-step offset kk = 32 h + 8 j + 2 q + b (b: low or high half of dword q)
-    sits at byte (64 j + l32 + 32 h) * 16 + 4 q + 2 b.  Entries of one
-    (u, k-step, cb) are ranked in position order; rank r goes to word
-    ((u * nk + ks) * 128) + 2 r + cb.  More than 64 positions in one 32 x 64 block
-    of a wave (3 % local density) raise ValueError."""
+    [0, 8) of row 32 cb + l32 as fragment registers j = 0..3.  Register j goes
+    through a 2 KiB image that puts lane l's copy of column block cb at byte
+    (64 cb + l) * 16, so the weight at k-step offset kk = 32 h + 8 j + 2 q + b
+    (b: low or high half of dword q) sits at byte (64 cb + l32 + 32 h) * 16 +
+    4 q + 2 b of register j's image.  The entries of one (u, k-step, j) are
+    ranked in position order; rank r goes to word (u * nk + ks) * 128 +
+    32 j + r (lanes 16 j..16 j + 15 store them).  More than 32 positions in one
+    register's 64 x 16 block of a wave (3 % local density) raise ValueError."""
     E, R, C = (int(d) for d in shape)
     idx = idx.reshape(-1).to(torch.int64)
     e = torch.div(idx, R * C, rounding_mode="floor")
@@ -175,9 +176,9 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     kk = k % 64
     lane = l32 + 32 * torch.div(kk, 32, rounding_mode="floor")
     j = torch.div(kk % 32, 8, rounding_mode="floor")
-    off = (64 * j + lane) * 16 + 4 * torch.div(kk % 8, 2, rounding_mode="floor") + 2 * (kk % 2)
+    off = (64 * cb + lane) * 16 + 4 * torch.div(kk % 8, 2, rounding_mode="floor") + 2 * (kk % 2)
     group = ((e * n_nt + nt) * 4 + w) * nk + ks
-    key = group * 2 + cb
+    key = group * 4 + j
     order = torch.argsort(key, stable=True)
     sk = key[order]
     first = torch.searchsorted(sk, sk)  # start of each key's run
@@ -185,11 +186,20 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     rank = torch.empty_like(rank_sorted)
     rank[order] = rank_sorted
     if rank.numel() and int(rank.max()) >= _OVL_CAP:
-        raise ValueError(f"overlay ({kind}): more than {_OVL_CAP} trained positions in one 32 x 64 weight block; "
+        raise ValueError(f"overlay ({kind}): more than {_OVL_CAP} trained positions in one 64 x 16 weight block; "
                          f"use dense expert weights with overlay_scatter for such masks")
-    word = group * 128 + 2 * rank + cb
+    word = group * 128 + 32 * j + rank
     n_words = E * n_nt * 4 * nk * 128
     return word.to(torch.int32), off.to(torch.int32), n_words
+
+
+def overlay_table(n_words: int, word: torch.Tensor, off: torch.Tensor) -> torch.Tensor:
+    """Entry table with offsets set, values 0: unused words point into the dummy
+    area [2048, 4096) of the wave's epilogue tile, one 16-bit slot per word."""
+    dev = word.device
+    table = 2048 + 2 * (torch.arange(n_words, dtype=torch.int32, device=dev) % 1024)
+    table[word.long()] = off
+    return table
 
 
 class Q4Overlay:
@@ -214,9 +224,10 @@ class Q4Overlay:
         self.tables = {}
         for kind in _OVL_KINDS[role]:
             word, off, n_words = overlay_entries(kind, idx.to(dev), shape, inter)
-            table = torch.full((n_words,), 0xFFFF, dtype=torch.int32, device=dev)
-            table[word.long()] = off
-            self.tables[kind] = (table, word, n_words)
+            # refresh order: by word, so that each cache line of the table is written in one burst
+            order = torch.argsort(word)
+            self.tables[kind] = (overlay_table(n_words, word, off), word[order].contiguous(),
+                                 order.to(torch.int32), n_words)
         self.bad = torch.zeros(1, dtype=torch.int32, device=dev)
         self.refresh(values)
 
@@ -232,9 +243,10 @@ class Q4Overlay:
         v = values.detach().reshape(-1)
         if v.dtype != torch.float32 or not v.is_contiguous() or v.numel() != self.n:
             raise ValueError(f"overlay refresh needs {self.n} contiguous fp32 values")
-        (ta, wa, na), (tb, wb, nb) = (self.tables[k] for k in _OVL_KINDS[self.role])
-        N.call("usaf_hip_overlay_refresh", v.data_ptr(), self.n, wa.data_ptr(), ta.data_ptr(), na, wb.data_ptr(),
-               tb.data_ptr(), nb, N.dtype_code(self.dtype), self.bad.data_ptr(), N.stream_ptr(v.device))
+        (ta, wa, ia, na), (tb, wb, ib, nb) = (self.tables[k] for k in _OVL_KINDS[self.role])
+        N.call("usaf_hip_overlay_refresh", v.data_ptr(), self.n, wa.data_ptr(), ia.data_ptr(), ta.data_ptr(), na,
+               wb.data_ptr(), ib.data_ptr(), tb.data_ptr(), nb, N.dtype_code(self.dtype), self.bad.data_ptr(),
+               N.stream_ptr(v.device))
 
 
 class ExpertWeights:

@@ -39,6 +39,12 @@ class SparseAdam:
         self.weight_decay = weight_decay
         self._named: dict[str, torch.nn.Parameter] = dict(named_params)
         self._step = 0
+        # device-gated steps (step(finite=..., halt=...)): the applied-step count
+        # lives on the GPU, with a table of the bias corrections of steps 1..cap
+        self._count: torch.Tensor | None = None
+        self._bias: torch.Tensor | None = None
+        self._launched = 0  # gated launches so far: an upper bound of the device count
+        self.bad = None
         self._active_ids: list[str] = []
         self._idx: dict[str, torch.Tensor] = {}
         self._m: dict[str, torch.Tensor] = {}
@@ -88,13 +94,47 @@ class SparseAdam:
                 else:
                     param.grad.zero_()
 
-    def step(self, compact_grads: dict[str, torch.Tensor] | None = None):
+    def _gate_state(self, dev: torch.device) -> None:
+        """Device step count and a bias-correction table covering every step a
+        gated launch can reach (grown by doubling; the growth copies from the host)."""
+        if self._count is None:
+            self._count = torch.full((1,), self._step, dtype=torch.int32, device=dev)
+            self._launched = self._step
+            self.bad = torch.zeros(1, dtype=torch.int32, device=dev)
+        need = self._launched + 1
+        cap = 0 if self._bias is None else self._bias.numel() // 2
+        if need > cap:
+            cap = max(4096, 2 * cap)
+            while cap < need:
+                cap *= 2
+            beta1, beta2 = self.betas
+            # the reference's Python-float scalars, used by fp32 tensor ops as fp32
+            tab = [x for t in range(1, cap + 1) for x in (1 - beta1 ** t, 1 - beta2 ** t)]
+            self._bias = torch.tensor(tab, dtype=torch.float32).to(dev)
+
+    @property
+    def step_count(self) -> int:
+        """Steps applied so far (reads the device count after gated steps)."""
+        return int(self._count.item()) if self._count is not None else self._step
+
+    def step(self, compact_grads: dict[str, torch.Tensor] | None = None, finite: torch.Tensor | None = None,
+             halt: torch.Tensor | None = None):
         """One Adam step over the active elements (sparse_optim.py:86-134).
 
         compact_grads: optional name -> 1-D gradient aligned with ``active_idx``
         (e.g. ``SparseGradStore.compact``), used instead of ``param.grad``.
+        finite / halt: optional int32 GPU flags; given (or after the first such
+        call), the step is decided on the device -- applied only if finite[0] != 0
+        and halt[0] == 0, the trainer's finite gate (train.py:649-672) -- and the
+        step count and bias corrections live on the GPU, so the update can be
+        launched before the host has read the flags.
         """
-        self._step += 1
+        for t, what in ((finite, "finite"), (halt, "halt")):
+            if t is not None and (not t.is_cuda or t.dtype != torch.int32 or t.numel() < 1):
+                raise TypeError(f"SparseAdam: {what} must be an int32 GPU tensor")
+        gated = finite is not None or halt is not None or self._count is not None
+        if not gated:
+            self._step += 1
         beta1, beta2 = self.betas
         for name in self._active_ids:
             param = self._named[name]
@@ -119,12 +159,24 @@ class SparseAdam:
             if grad.numel() != target.numel():
                 raise ValueError(f"SparseAdam: gradient for {name} has {grad.numel()} entries, expected "
                                  f"{target.numel()}")
-            N.call("usaf_hip_sparse_adam_step", target.data_ptr(), grad.data_ptr(), self._m[name].data_ptr(),
-                   self._v[name].data_ptr(), target.numel(), float(self.lr), float(beta1), float(beta2),
-                   float(self.eps), float(self.weight_decay), self._step, N.stream_ptr(dev))
+            if gated:
+                self._gate_state(dev)
+                N.call("usaf_hip_sparse_adam_step_gated", target.data_ptr(), grad.data_ptr(),
+                       self._m[name].data_ptr(), self._v[name].data_ptr(), target.numel(), float(self.lr),
+                       float(beta1), float(beta2), float(self.eps), float(self.weight_decay), N.ptr(finite),
+                       N.ptr(halt), self._count.data_ptr(), self._bias.data_ptr(), self._bias.numel() // 2,
+                       self.bad.data_ptr(), N.stream_ptr(dev))
+            else:
+                N.call("usaf_hip_sparse_adam_step", target.data_ptr(), grad.data_ptr(), self._m[name].data_ptr(),
+                       self._v[name].data_ptr(), target.numel(), float(self.lr), float(beta1), float(beta2),
+                       float(self.eps), float(self.weight_decay), self._step, N.stream_ptr(dev))
             if not self.compact_params:
                 flat = param.data.reshape(-1)
                 flat.scatter_(0, self._idx[name], target.to(param.dtype))
+        if gated and self._count is not None:
+            N.call("usaf_hip_count_step", N.ptr(finite), N.ptr(halt), self._count.data_ptr(),
+                   N.stream_ptr(self._count.device))
+            self._launched += 1
 
     def refresh(self, model):
         """Re-bind current model Parameters by name (sparse_optim.py:136-150)."""
@@ -143,13 +195,16 @@ class SparseAdam:
     def state_dict(self) -> dict:
         """m/v/step for checkpoints (CPU copies, as the reference stores them)."""
         return {
-            "step": self._step,
+            "step": self.step_count,
             "m": {n: t.detach().cpu().clone() for n, t in self._m.items()},
             "v": {n: t.detach().cpu().clone() for n, t in self._v.items()},
         }
 
     def load_state_dict(self, sd: dict) -> None:
         self._step = int(sd["step"])
+        if self._count is not None:
+            self._count.fill_(self._step)
+            self._launched = self._step
         for n, t in sd["m"].items():
             if n in self._m and t.numel() == self._m[n].numel():
                 self._m[n] = t.detach().to(self._m[n].device, torch.float32).clone()
