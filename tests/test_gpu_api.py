@@ -12,7 +12,7 @@ import torch.nn as nn
 
 from oracle import moe as M
 from oracle.codec_torch import dequant_opseq
-from usaf_amd.moe_loader import QuantizedExpertCache, setup_quantized_streaming
+from usaf_amd.moe_loader import QuantizedExpertCache, get_quantized_cache, setup_quantized_streaming
 from usaf_amd.quantization import quantize_state_dict
 
 pytestmark = pytest.mark.gpu
@@ -181,6 +181,61 @@ def test_quantized_streaming_fused_block(gpu_device):
     torch.cuda.synchronize()
     assert rel_err(out, ref) <= 1e-2
     assert getattr(block.experts, "_usaf_q4", None) is None   # detached again by the post-hook
+
+
+def test_quantized_streaming_fused_sync_resident(gpu_device):
+    """The reference's training loop scatters the optimizer masters into the expert
+    weights after each step (train.py:666 cache.sync_resident); the fused streaming
+    block must then multiply the trained values: bit-exact weights through the
+    overlay tables, the block output against the oracle on the scattered weights."""
+    _say("setup_quantized_streaming (fused) + sync_resident(masters) -> block on the trained weights, bf16")
+    from usaf_amd.qwen3moe_dml import patch_qwen3moe_for_dml
+    patch_qwen3moe_for_dml()
+    dt = torch.bfloat16
+    block = _tiny_qwen3_moe(seed=9)
+    layer = nn.Module()
+    layer.mlp = block
+    model = nn.Module()
+    model.model = nn.Module()
+    model.model.layers = nn.ModuleList([layer])
+    model = model.to(dt)
+    experts_sd = {k: v.detach().half() for k, v in model.state_dict().items() if ".mlp.experts." in k}
+    qd = quantize_state_dict(experts_sd, device=gpu_device)
+    setup_quantized_streaming(model, qd, gpu_device, verbose=False)
+    cache = get_quantized_cache(model)
+    g = torch.Generator().manual_seed(10)
+    active, masters, w_eff = {}, {}, {}
+    for local in ("gate_up_proj", "down_proj"):
+        name = f"model.layers.0.mlp.experts.{local}"
+        w16 = _oracle_dequant(qd[name])
+        n = w16.numel()
+        idx = torch.randperm(n, generator=g)[: n // 200].sort().values
+        vals = w16.reshape(-1)[idx].float() + torch.randn(idx.numel(), generator=g) * 0.05
+        active[name] = idx.to(gpu_device)
+        masters[name] = torch.nn.Parameter(vals.to(gpu_device), requires_grad=False)
+        w = w16.clone()
+        w.reshape(-1)[idx] = vals.half()  # the reference's scatter into its fp16 weights
+        w_eff[local] = w.to(dt)
+    cache.sync_resident(active, masters)
+    hs = torch.randn(1, 128, 256, generator=g).to(dt)
+    ref = _reference_block(hs, block.gate.weight.detach().cpu(), w_eff["gate_up_proj"], w_eff["down_proj"], 2, True)
+    out = model.model.layers[0].mlp(hs.to(gpu_device))
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) <= 1e-2
+    # a second sync (the next optimizer step) refreshes the same tables
+    for name in masters:
+        masters[name].data.mul_(0.5)
+    cache.sync_resident(active, masters)
+    for local in ("gate_up_proj", "down_proj"):
+        name = f"model.layers.0.mlp.experts.{local}"
+        w = _oracle_dequant(qd[name]).clone()
+        w.reshape(-1)[active[name].cpu()] = masters[name].detach().cpu().half()
+        w_eff[local] = w.to(dt)
+    ref = _reference_block(hs, block.gate.weight.detach().cpu(), w_eff["gate_up_proj"], w_eff["down_proj"], 2, True)
+    out = model.model.layers[0].mlp(hs.to(gpu_device))
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) <= 1e-2
+    assert len(cache.fused_overlays) == 2
 
 
 def _tiny_olmoe(E=8, H=256, I=128, k=2, seed=0, norm=False):

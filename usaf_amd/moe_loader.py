@@ -23,7 +23,7 @@ import torch.nn as nn
 
 from . import _native as N
 from .importance import TopKImportanceStore  # noqa: F401  (moe_loader.py:584-631, GPU selection)
-from .moe import Q4Tensor
+from .moe import Q4Overlay, Q4Tensor
 from .olmoe_streaming import _record_grad, apply_captured_expert_grads  # noqa: F401  (moe_loader.py:778-802)
 from .quantization import dequantize_4bit
 
@@ -100,6 +100,10 @@ class QuantizedExpertCache:
         self._build_index()
         self._resident: Dict[str, Dict[str, torch.Tensor]] = {}
         self._resident_active = False
+        # fused path: trained values of 4-bit tensors as overlay tables the fused GEMMs
+        # read (Q4Overlay), refreshed by sync_resident; built for this activation dtype
+        self.fused_overlays: Dict[str, Any] = {}
+        self.fused_dtype: Optional[torch.dtype] = None
         self.hits = 0
         self.misses = 0
 
@@ -124,6 +128,15 @@ class QuantizedExpertCache:
             entry = self._q_dict.get(full_name)
             if entry is not None:
                 out[local] = entry
+        return out
+
+    def get_q4_overlays(self, expert_module_name: str) -> Dict[str, Any]:
+        """The fused overlays (Q4Overlay) of a module's 4-bit tensors, by local name."""
+        out = {}
+        for full_name, local in self._expert_to_params.get(expert_module_name, []):
+            ov = self.fused_overlays.get(full_name)
+            if ov is not None:
+                out[local] = ov
         return out
 
     # ---- dequantized copies --------------------------------------------------------
@@ -241,10 +254,34 @@ class QuantizedExpertCache:
         self._scatter_masters(active_idx, masters)
 
     def sync_resident(self, active_idx, masters) -> None:
-        """moe_loader.py:425-443: propagate optimizer masters into the resident copies."""
+        """moe_loader.py:425-443: propagate optimizer masters into the resident copies
+        and, for 4-bit tensors the fused GEMMs read (setup_quantized_streaming with
+        fused=True), into their overlay tables."""
+        self._sync_fused(active_idx, masters)
         if not self._resident_active:
             return
         self._scatter_masters(active_idx, masters)
+
+    def _sync_fused(self, active_idx, masters) -> None:
+        if self.fused_dtype is None:
+            return
+        for fname, aidx in active_idx.items():
+            entry = self._q_dict.get(fname)
+            local = fname.rsplit(".", 1)[-1]
+            if not isinstance(entry, Q4Tensor) or local not in ("gate_up_proj", "down_proj") or not entry.fused_ok():
+                continue
+            vals = masters[fname]
+            vals = (vals.data if isinstance(vals, torch.nn.Parameter) else vals).reshape(-1)
+            vals = vals.to(device=self._device, dtype=torch.float32).contiguous()
+            ov = self.fused_overlays.get(fname)
+            if ov is None or ov.n != aidx.numel():
+                role = local.replace("_proj", "")
+                shape = entry.shape
+                inter = int(shape[1]) // 2 if role == "gate_up" else int(shape[2])
+                self.fused_overlays[fname] = Q4Overlay(role, aidx.to(self._device), shape, inter, self.fused_dtype,
+                                                       vals)
+            else:
+                ov.refresh(vals)
 
     def _scatter_masters(self, active_idx, masters) -> None:
         for fname, aidx in active_idx.items():
@@ -467,10 +504,16 @@ def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], 
     grads: Dict[str, torch.Tensor] = {}
     model._expert_grads = grads
 
+    if fused:
+        dtypes = {p.dtype for p in resident if p.is_floating_point()}
+        act = torch.bfloat16 if torch.bfloat16 in dtypes else torch.float16
+        cache.fused_dtype = act  # the overlay tables hold trained values in the activation dtype
+
     def attach(mod_name: str):
         def pre_hook(module: nn.Module, _args) -> None:
             if fused:
                 module._usaf_q4 = cache.get_q4(mod_name)
+                module._usaf_q4_overlays = cache.get_q4_overlays(mod_name)
             else:
                 for pname, param in cache.get_expert_weights(mod_name).items():
                     module._parameters[pname] = param
@@ -483,6 +526,7 @@ def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], 
     def detach(module: nn.Module, _args, output):
         module._parameters.clear()
         module._usaf_q4 = None
+        module._usaf_q4_overlays = None
         state["resident"] -= 1
         return output
 

@@ -24,7 +24,7 @@ from __future__ import annotations
 
 import torch
 
-from .moe import ExpertWeights, Q4Tensor, RouteTopKFn, routed_experts
+from .moe import ExpertWeights, RouteTopKFn, routed_experts
 
 
 def _expert_weights(module) -> ExpertWeights:
@@ -33,7 +33,11 @@ def _expert_weights(module) -> ExpertWeights:
         gu, dn = q4.get("gate_up_proj"), q4.get("down_proj")
         if gu is None or dn is None:
             raise RuntimeError("module._usaf_q4 must hold gate_up_proj and down_proj")
-        return ExpertWeights(gu if isinstance(gu, Q4Tensor) else gu, dn if isinstance(dn, Q4Tensor) else dn)
+        ew = ExpertWeights(gu, dn)
+        # trained values over the 4-bit weights (QuantizedExpertCache.sync_resident)
+        for local, ov in (getattr(module, "_usaf_q4_overlays", None) or {}).items():
+            ew.overlays[local.replace("_proj", "")] = ov
+        return ew
     gu = getattr(module, "gate_up_proj", None)
     dn = getattr(module, "down_proj", None)
     if gu is None or dn is None:
