@@ -638,16 +638,41 @@ def probe_kernels(dev) -> None:
     L = build_moe(dev)
     bench_moe_kernels(L, 1)
     torch.cuda.synchronize()
+    # one training step of the bench loop: every other kernel of the step once
+    # (sampled gradients, blocked transposes, combines, router, optimizers, overlay refresh)
+    loop = LaggedSteps(L)
+    loop.step()
+    loop.flush()
+    torch.cuda.synchronize()
+
+
+KERNEL_SOURCES = ("usaf_amd/csrc/moe_gemm.hip", "usaf_amd/csrc/codec.hip", "usaf_amd/csrc/sparse.hip")
+
+
+def kernel_source_hash() -> str:
+    """sha256 over the kernel sources the traffic counters were measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    root = os.path.dirname(os.path.abspath(__file__))
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(root, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
 
 
 def _load_traffic() -> dict:
     """Per-launch HBM bytes of the hot kernels measured with rocprofv3 counters
-    (profiles/hbm_traffic_qwen3_cfg2.md gives the commands); {} if absent."""
+    (profiles/hbm_traffic_qwen3_cfg2.md gives the commands), only when they were
+    measured on the kernel sources of this tree; {} if absent or stale."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f).get("bytes_per_launch", {})
+            data = json.load(f)
     except (OSError, ValueError):
         return {}
+    if data.get("source_sha256") != kernel_source_hash():
+        _log("traffic: the committed counter measurements are of other kernel sources; reporting traffic as null")
+        return {}
+    return data.get("bytes_per_launch", {})
 
 
 def main() -> int:

@@ -1173,9 +1173,12 @@ static_assert(Q_EP_ELEMS * 2 >= 2 * Q_IMG_J, "the overlay's fragment image and d
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // 16-byte chunk of an activation row: logical chunk c of row r sits at physical
-// chunk c ^ (r & 7), so the 8 rows a fragment read touches per LDS cycle hit
-// distinct banks.
-__device__ __forceinline__ int q_swz(int r) { return r & 7; }
+// chunk c ^ ((r >> 1) & 7).  A fragment read takes 16 consecutive rows (one
+// 16-byte chunk each) per 256-byte LDS cycle; two 128-byte rows share the 64
+// banks, so the 16 chunks hit distinct banks when the even rows and the odd
+// rows each take 8 distinct chunks.  (c ^ (r & 7) gives rows r and r + 8 the
+// same chunk: a 2-way conflict in every cycle.)
+__device__ __forceinline__ int q_swz(int r) { return (r >> 1) & 7; }
 
 // LDS DMA (global_load_lds): lane l's 16 (4) bytes at base + off land at
 // lds_dst + 16 l (4 l); base and lds_dst are wave-uniform.
