@@ -320,15 +320,16 @@ int usaf_hip_moe_gate_up_bwd_t(const void* dgu, int64_t I, const int32_t* offset
  * `overlay` (NULL: none) of usaf_hip_moe_gate_up_fwd, usaf_hip_moe_down_fwd,
  * usaf_hip_moe_down_bwd_t and usaf_hip_moe_gate_up_bwd_t is that GEMM's entry
  * table of `overlay_words` uint32 words (at least the count below, else
- * USAF_ERR_INVALID): for each (expert e, n-tile nt, wave w in 0..3) unit u = (e * n_nt + nt)
- * * 4 + w and each k-step ks (64 contraction elements; n_nt = ceil(I / 128) for
- * gate_up_fwd, else ceil(N / 256)), 128 uint32 words at ((u * K / 64 + ks) * 128):
- * word 32 j + r is entry r (< 32) of the wave's fragment register j (lanes
- * 16 j..16 j + 15 store them): {byte offset | value << 16}, the offset into the
- * 2 KiB image of register j, which holds lane l's copy of column block cb (the
- * wave's weight rows 32 cb + l % 32, k = 32 (l / 32) + 8 j + [0, 8) of the
- * k-step) at byte (64 cb + l) * 16, element k at 2 (k % 8) within it; unused
- * words hold an offset in [2048, 4096) (a scratch area of the wave's LDS
+ * USAF_ERR_INVALID): for each (expert e, n-tile nt, wave w in 0..7) unit u = (e * n_nt + nt)
+ * * 8 + w and each k-step ks (64 contraction elements; n_nt = ceil(I / 128) for
+ * gate_up_fwd, else ceil(N / 256)), 64 uint32 words at ((u * K / 64 + ks) * 64):
+ * word 16 j + r is entry r (< 16) of the wave's fragment register j (lane
+ * 16 j + r stores it): {byte offset | value << 16}, the offset into the 1 KiB
+ * image of register j, which holds lane l's copy (the wave's weight row l % 32,
+ * k = 32 (l / 32) + 8 j + [0, 8) of the k-step) at byte 16 l, element k at
+ * 2 (k % 8) within it.  Wave w's 32 rows are the n-tile's rows 32 w + [0, 32)
+ * (gate_up_fwd: gate rows n = 128 nt + 16 w + [0, 16), then the up rows I + n);
+ * unused words hold an offset in [1024, 2048) (a scratch area of the wave's LDS
  * epilogue tile).  The Python layer (usaf_amd/moe.py overlay_entries,
  * Q4Overlay) builds the tables once per set of positions.  A GEMM with an overlay
  * runs the 4-bit LDS-DMA kernel only (NotImplemented otherwise).

@@ -3,9 +3,9 @@ every trained position must land on the lane, fragment register and half that
 the fused 4-bit GEMM kernel gives that weight.
 
 The brute force walks the kernel's own assignment forward -- tile unit
-(expert, n-tile, wave) -> column block cb and lane -> weight row (wrow of
-moe_gemm_q4_kernel) and k-step -> fragment register j, dword q, half b -> byte
-(64 cb + lane) * 16 + 4 q + 2 b of register j's image -- and the table builder,
+(expert, n-tile, wave) and lane -> weight row (wrow of moe_gemm_q4_kernel:
+tile row 32 w + l32) and k-step -> fragment register j, dword q, half b -> byte
+(l32 + 32 h) * 16 + 4 q + 2 b of register j's image -- and the table builder,
 which inverts it, must agree position by position."""
 import itertools
 
@@ -26,13 +26,13 @@ def kernel_assignment(kind, E, R, C, inter):
         N, K, n_nt = C, R, (C + 255) // 256
     nk = K // 64
     out = {}
-    for e, nt, w, cb, l32 in itertools.product(range(E), range(n_nt), range(4), range(2), range(32)):
-        b = 64 * w + 32 * cb + l32  # tile row
+    for e, nt, w, l32 in itertools.product(range(E), range(n_nt), range(8), range(32)):
+        b = 32 * w + l32  # tile row
         if kind == "gate_up_fwd":
-            n = nt * 128 + (b >> 6) * 32 + (b & 31)
+            n = nt * 128 + (b >> 5) * 16 + (b & 15)
             if n >= inter:
                 continue
-            n_row = (inter if (b >> 5) & 1 else 0) + n
+            n_row = (inter if b & 16 else 0) + n
         else:
             n_row = nt * 256 + b
             if n_row >= N:
@@ -40,9 +40,9 @@ def kernel_assignment(kind, E, R, C, inter):
         for ks, h, j, q, hb in itertools.product(range(nk), range(2), range(4), range(4), range(2)):
             k = ks * 64 + 32 * h + 8 * j + 2 * q + hb
             lane = l32 + 32 * h
-            off = (64 * cb + lane) * 16 + 4 * q + 2 * hb
+            off = lane * 16 + 4 * q + 2 * hb
             r, c = (n_row, k) if kind in ("gate_up_fwd", "down_fwd") else (k, n_row)
-            unit = (e * n_nt + nt) * 4 + w
+            unit = (e * n_nt + nt) * 8 + w
             out[(e, r, c)] = (unit * nk + ks, j, off)
     return out
 
@@ -67,20 +67,20 @@ def test_entries_match_kernel_fragments(kind, shape, inter):
         e, rem = divmod(f, R * C)
         r, c = divmod(rem, C)
         group, j, want_off = ref[(e, r, c)]
-        assert wd // 128 == group and (wd % 128) // 32 == j and o == want_off, (kind, e, r, c)
-    # ranks: the positions of one (group, register) take words 32 j + 0, 1, ... in position order
+        assert wd // 64 == group and (wd % 64) // 16 == j and o == want_off, (kind, e, r, c)
+    # ranks: the positions of one (group, register) take words 16 j + 0, 1, ... in position order
     prev = {}
     for f, wd in zip(idx.tolist(), word.tolist()):
-        key = (wd // 128, (wd % 128) // 32)
-        assert wd % 32 == prev.get(key, -1) + 1
-        prev[key] = wd % 32
+        key = (wd // 64, (wd % 64) // 16)
+        assert wd % 16 == prev.get(key, -1) + 1
+        prev[key] = wd % 16
 
 
 def test_entries_reject_dense_blocks():
-    # fragment register 0 of a wave covers k = 0..7 and 32..39 of its 64 rows (1024
-    # weights); 33 trained positions in it overflow, 32 fit
+    # fragment register 0 of a wave covers k = 0..7 and 32..39 of its 32 rows (512
+    # weights); 17 trained positions in it overflow, 16 fit
     shape = (1, 256, 128)
-    idx = torch.tensor(sorted(r * 128 + k for r in range(64) for k in (0, 33)))[: _OVL_CAP + 1]
+    idx = torch.tensor(sorted(r * 128 + k for r in range(32) for k in (0, 33)))[: _OVL_CAP + 1]
     with pytest.raises(ValueError, match="more than"):
         overlay_entries("down_fwd", idx, shape, 128)
     overlay_entries("down_fwd", idx[:_OVL_CAP], shape, 128)

@@ -1118,44 +1118,49 @@ __global__ __launch_bounds__(NK_THREADS) void moe_gemm_nk_kernel(const GemmArgs 
 //
 //   C[m, n] = sum_k A[row(m), k] * W_e[n, k]
 //
-// 256 threads = 4 waves, one per SIMD, one block per CU, persistent over a
-// per-die tile list.  Tile: up to 320 slots of one expert (10 blocks of 32) x
-// 256 weight rows; wave w owns weight rows [64w, 64w + 64) (two 32-row blocks)
-// for every slot, so each weight element is dequantized once per tile.
+// 512 threads = 8 waves, two per SIMD, one block per CU, persistent over a
+// per-die tile list.  Tile: up to 256 slots of one expert (8 blocks of 32) x
+// 256 weight rows; wave w owns weight rows [32w, 32w + 32) for every slot, so
+// each weight element is dequantized once per tile.  The two waves of a SIMD
+// fill each other's stalls (barrier, LDS and DMA counters) and share the
+// issue cycles the matrix core leaves: one wave per SIMD cannot issue the
+// dequant VALU work under its own MFMAs.
 // The MFMA takes the weights as its A operand (32 n x 16 k) and the slots as
 // its B operand (32 m x 16 k): a lane's accumulator then holds 4 consecutive
-// output columns of one slot, which go to global memory as 8-byte stores with
-// no LDS round trip.
+// output columns of one slot.
 // Every global read is a global_load_lds (DMA into LDS, no VGPR staging)
 // into a 3-stage ring, stage s = k-step % 3:
 //   activations  256 rows x 128 B (16-byte chunks XOR-swizzled by row)
 //   codes        256 weight rows x 32 B, scale|zero 256 x 4 B
+//   (OVL) overlay entries, 64 words per wave
 // At k-step gs a thread issues the codes of gs + 3 and the activations of
-// gs + 2 (11 DMA instructions), multiplies k-step gs, and dequantizes the
+// gs + 2 (6 or 7 DMA instructions), multiplies k-step gs, and dequantizes the
 // codes of gs + 1 into the other register set of weight fragments; the step
-// ends with s_waitcnt vmcnt(11) (everything but this step's DMAs landed) and
-// a workgroup barrier.  The load streams run straight across tile boundaries,
-// so the next tile's first k-steps are in flight during this tile's last
-// steps and epilogue.
+// ends with a vmcnt wait (everything older than this step's DMAs has landed)
+// and a workgroup barrier.  The load streams run straight across tile
+// boundaries, so the next tile's first k-steps are in flight during this
+// tile's last steps and epilogue.
 // =====================================================================================
-constexpr int Q_BM = 256, Q_BN = 256, Q_THREADS = 256;
+constexpr int Q_BM = 256, Q_BN = 256, Q_THREADS = 512, Q_WAVES = Q_THREADS / 64;
 constexpr int Q_MAX_E = 255;
 constexpr int Q_A_BYTES = Q_BM * BK * 2;                 // activation rows of one k-step
 constexpr int Q_C_BYTES = Q_BN * BK / 2;                 // codes of one k-step
-constexpr int Q_Z_BYTES = Q_BN * 4;                      // scale|zero pairs of one k-step
-constexpr int Q_O_BYTES = 4 * 128 * 4;                  // overlay entries of one k-step (4 waves x 128 words)
+constexpr int Q_Z_BYTES = Q_BN * 4;                      // scale|zero words of one k-step
+constexpr int Q_OVL_WORDS = 64;                          // overlay entries per wave and k-step
+constexpr int Q_O_BYTES = Q_WAVES * Q_OVL_WORDS * 4;     // overlay entries of one k-step
 constexpr int Q_STAGE = Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES + Q_O_BYTES;
-constexpr int Q_A_LOADS = Q_A_BYTES / (16 * Q_THREADS);  // 8 x 16 B per thread
-constexpr int Q_DMAS = 3 + Q_A_LOADS;                    // DMA instructions per thread per k-step
-constexpr int Q_OVL_DMAS = 2;                            // + overlay entries of one k-step (2 x 256 B per wave)
+constexpr int Q_A_LOADS = Q_A_BYTES / (16 * Q_THREADS);  // 4 x 16 B per thread
+// DMA instructions per thread and k-step: d = 0 the scale|zero word, d = 1
+// the code chunk, d = 2.. the activation chunks;
+// OVL: d = Q_DMAS the wave's overlay entries of the code stream's k-step
+constexpr int Q_DMAS = 2 + Q_A_LOADS;
 // Overlay (trained values over the 4-bit weights): per wave and k-step one
-// group of 128 entries, each a 32-bit word {byte offset | value << 16}.  Lane l
-// holds words 2 l and 2 l + 1: entries of fragment register j = l / 16, with
-// offsets into that register's 2 KiB image (both column blocks); unused words
-// point into [2048, 4096) of the wave's epilogue tile, which the k-steps do not
-// read.  The entries travel with the codes of their k-step, in the same stage.
-constexpr int Q_OVL_GROUP = 128 * 4;                     // bytes of one wave's entries per k-step
-constexpr int Q_IMG_J = 2 * 64 * 16;                     // one fragment register of both column blocks
+// group of 64 entries, each a 32-bit word {byte offset | value << 16}.  Lane l
+// holds word l, an entry of fragment register j = l / 16 whose offset points
+// into that register's 1 KiB image (lane l' at byte 16 l'); unused words point
+// into [1024, 2048) of the wave's epilogue tile, which the k-steps do not read.
+// The entries travel with the codes of their k-step, in the same stage.
+constexpr int Q_IMG = 64 * 16;                           // one fragment register of the wave
 // Dynamic LDS (the DMA targets): 3 stages | s_h, s_l, s_off tables | token rows [2][Q_BM].
 // A stage: activations | codes | scale|zero words | overlay entries.
 // The epilogue tiles are a separate static array: the compiler then knows that
@@ -1164,11 +1169,11 @@ constexpr int Q_IMG_J = 2 * 64 * 16;                     // one fragment registe
 constexpr int Q_TAB_OFF = 3 * Q_STAGE;
 constexpr int Q_TOK_OFF = Q_TAB_OFF + 3 * (Q_MAX_E + 1) * 4;
 constexpr size_t kQSmemBytes = (size_t)Q_TOK_OFF + 2 * Q_BM * 4;
-constexpr int Q_EPW = 104;                      // staging row stride, 16-bit elements (96 columns + pad)
-constexpr int Q_EP_ELEMS = 32 * Q_EPW;          // one wave's 32 x 96 staging tile
-static_assert(kQSmemBytes + 4 * Q_EP_ELEMS * 2 <= 160 * 1024, "LDS budget");
-static_assert(4 * Q_EP_ELEMS * 2 >= Q_THREADS * 4, "the prefix scratch lives in the epilogue tiles");
-static_assert(Q_EP_ELEMS * 2 >= 2 * Q_IMG_J, "the overlay's fragment image and dummy area live in the wave's epilogue tile");
+constexpr int Q_EPW = 48;                       // staging row stride, 16-bit elements (48 or 32 columns)
+constexpr int Q_EP_ELEMS = 32 * Q_EPW;          // one wave's 32-slot staging tile
+static_assert(kQSmemBytes + Q_WAVES * Q_EP_ELEMS * 2 <= 160 * 1024, "LDS budget");
+static_assert(Q_WAVES * Q_EP_ELEMS * 2 >= Q_THREADS * 4, "the prefix scratch lives in the epilogue tiles");
+static_assert(Q_EP_ELEMS * 2 >= 2 * Q_IMG, "the overlay's fragment image and dummy area live in the wave's epilogue tile");
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -1181,12 +1186,20 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 __device__ __forceinline__ int q_swz(int r) { return (r >> 1) & 7; }
 
 // LDS DMA (global_load_lds): lane l's 16 (4) bytes at base + off land at
-// lds_dst + 16 l (4 l); base and lds_dst are wave-uniform.
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(base) + off, (lds_void_ptr)lds_dst, 16, 0, 0);
+// lds_dst + 16 l (4 l); base and lds_dst are wave-uniform.  Issued as inline
+// asm: with the compiler's own LDS-DMA intrinsic in the code it stops counting
+// the wave's LDS reads and waits for all of them (lgkmcnt(0)) before every use
+// of a fragment, which drains the fragment prefetches several times a k-step.
+// The DMAs count in vmcnt only; the k-step's explicit vmcnt wait covers them,
+// and any wait the compiler places for its own loads is at least as strict
+// with them in flight (vector memory loads complete in order).  M0 takes the
+// LDS address; one wait state separates the M0 write from the DMA.
+// lds: LDS byte address (uniform); base: uniform global pointer.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off), "s"(base) : "m0");
 }
-__device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(base) + off, (lds_void_ptr)lds_dst, 4, 0, 0);
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off), "s"(base) : "m0");
 }
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -1199,21 +1212,25 @@ struct QTile {
 // z(k) | z(k+1) << 16} pairs from wsz (one 128-column group of n per 256 B per k-step).
 // OVL: trained values replace some of the dequantized weights (the reference's
 // overlay scatter into the fp16 weights, usaf/moe_loader.py:218-221, 425-443).
-// The entries of a k-step ride the code stream (two more DMAs per step, into
-// the code stage).  As soon as a wave has dequantized fragment register j of
-// the next k-step (both column blocks), it writes the two registers to a 2 KiB
-// image in its epilogue tile, stores over it the values of its entries that
-// fall in register j (16-bit LDS stores) and reads the registers back, four
-// such round trips spread over the k-step's MFMA regions: every weight the
-// MFMAs see is then the trained value where an entry names it.
+// The entries of a k-step ride the code stream (one more DMA per thread and
+// step, into the code stage).  As soon as a wave has dequantized fragment
+// register j of the next k-step, it writes the register to a 1 KiB image in
+// its epilogue tile, stores over it the values of its entries that fall in
+// register j (one 16-bit LDS store by each of 16 lanes) and reads the register
+// back, four such round trips spread over the k-step's MFMA regions: every
+// weight the MFMAs see is then the trained value where an entry names it.
+// SwiGLU forward: wave w holds gate rows n = 16 w + [0, 16) of the n-tile as
+// its rows 0-15 and the up rows I + n as rows 16-31, so accumulator registers
+// r and r + 8 of a lane are gate and up of the same column and slot.
 template <int EPI, int DT, bool BT, bool OVL>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
-  __shared__ __attribute__((aligned(16))) uint16_t q_ep[4 * Q_EP_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t q_ep[Q_WAVES * Q_EP_ELEMS];
   int32_t* const s_h = reinterpret_cast<int32_t*>(qsm + Q_TAB_OFF);  // [Q_MAX_E + 1] heavy m-tile prefix
   int32_t* const s_l = s_h + Q_MAX_E + 1;                             // [Q_MAX_E + 1] light m-tile prefix
   int32_t* const s_off = s_l + Q_MAX_E + 1;                           // [Q_MAX_E + 1] expert offsets
   int32_t* const s_tok = reinterpret_cast<int32_t*>(qsm + Q_TOK_OFF); // [2][Q_BM] activation rows
+  const uint32_t qsm_lds = (uint32_t)(uintptr_t)(lds_void_ptr)qsm;   // LDS address of the dynamic area (DMA targets)
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, half = lane >> 5;
   const int wave = uni(tid >> 6);
   const int E = g.E;
@@ -1225,10 +1242,13 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     lds_barrier();
   }
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
-  TileWalk walk(s_h[E] + s_l[E], n_nt);
-  walk.set_heavy(s_h[E]);
+  // the tile counts come from LDS: readfirstlane tells the compiler they are
+  // uniform, so that the stream state below lives in scalar registers
+  const int n_heavy = uni(s_h[E]);
+  TileWalk walk(n_heavy + uni(s_l[E]), n_nt);
+  walk.set_heavy(n_heavy);
   const int n_grp = (int)(g.N / 128);  // BT: 128-column groups of n
-  const int n_my = walk.snake_count();
+  const int n_my = uni(walk.snake_count());
   if (n_my == 0) return;  // block-uniform
 
   // tile ordinal -> expert, first slot, rows, n-tile (the m-tile list of
@@ -1241,11 +1261,11 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     int64_t mt, nt;
     walk.decode(walk.snake_unit(rev ? n_my - 1 - ord : ord), mt, nt);
     int e, j;
-    if (mt < s_h[E]) {
+    if (mt < n_heavy) {
       e = prefix_owner(s_h, E, mt);
       j = (int)mt - s_h[e];
     } else {
-      e = prefix_owner(s_l, E, mt - s_h[E]);
+      e = prefix_owner(s_l, E, mt - n_heavy);
       j = (s_off[e + 1] - s_off[e] + Q_BM - 1) / Q_BM - 1;
     }
     QTile t;
@@ -1259,8 +1279,8 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // weight row of tile row b (0..255); columns past N (or I) read row 0 and are never stored
   auto wrow = [&](const QTile& t, int b) -> int64_t {
     if constexpr (EPI == EPI_SWIGLU_FWD) {
-      const int64_t n = (int64_t)t.nt * 128 + (b >> 6) * 32 + (b & 31);
-      return n < g.inter ? (((b >> 5) & 1) ? g.inter : 0) + n : 0;
+      const int64_t n = (int64_t)t.nt * 128 + (b >> 5) * 16 + (b & 15);
+      return n < g.inter ? ((b & 16) ? g.inter : 0) + n : 0;
     } else {
       const int64_t n = (int64_t)t.nt * Q_BN + b;
       return n < g.N ? n : 0;
@@ -1269,87 +1289,84 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
 
   // ---- load streams.  Each DMA address is a wave-uniform base plus a 32-bit
   //      per-lane byte offset (the host checks that the operands fit) ----
+  // scale|zero words of a k-step: one per weight row (4 waves' worth), or (BT)
+  // 64 per 128-row group of n (two groups per tile: 2 waves' worth)
+  constexpr int Z_WAVES = BT ? 2 : 4;
   // code stream: the codes of a k-step run one k-step ahead of its activations
   int c_ord = 0, c_kt = 0;
-  uint32_t c_off0 = 0, c_off1 = 0, z_off = 0;  // byte offsets of this thread's code chunks / scale|zero word at k-step 0
-  QTile c_next;                               // the tile the code stream enters next
+  uint32_t c_off = 0, z_off = 0;  // byte offsets of this thread's code chunk / scale|zero word at k-step 0
+  QTile c_next;                   // the tile the code stream enters next
   // activation stream
   int a_ord = 0, a_kt = 0;
-  bool a_enter = false;                       // entered a new tile at the last advance: refresh a_off
-  uint32_t a_off[Q_A_LOADS];                  // byte offsets of this thread's chunks at k-step 0
-  uint32_t o_off = 0;                         // OVL: byte offset of this lane's entry word at k-step 0 of the code stream's tile
+  bool a_enter = false;           // entered a new tile at the last advance: refresh a_off
+  uint32_t a_off[Q_A_LOADS];      // byte offsets of this thread's chunks at k-step 0
+  uint32_t o_off = 0;             // OVL: byte offset of this lane's entry word at k-step 0 of the code stream's tile
   const int a_lc = (tid & 7) ^ q_swz(tid >> 3);  // logical chunk of this thread's DMA slot
   const uint32_t lda_b = (uint32_t)g.lda * 2;
   auto c_setup = [&](const QTile& t) {
-    const int b0 = tid >> 1, b1 = 128 + (tid >> 1);
     const int64_t base = (int64_t)t.e * g.w_rows;
-    c_off0 = (uint32_t)((((base + wrow(t, b0)) * g.K) >> 1) + 16 * (tid & 1));
-    c_off1 = (uint32_t)((((base + wrow(t, b1)) * g.K) >> 1) + 16 * (tid & 1));
+    c_off = (uint32_t)((((base + wrow(t, tid >> 1)) * g.K) >> 1) + 16 * (tid & 1));
     if constexpr (OVL) {
-      // entries of tile unit ((e * n_nt + nt) * 4 + wave): nk groups of Q_OVL_GROUP bytes
-      const uint32_t unit = (uint32_t)(((int64_t)t.e * n_nt + t.nt) * 4 + wave);
-      o_off = unit * (uint32_t)nk * Q_OVL_GROUP + (uint32_t)lane * 4;
+      // entries of tile unit ((e * n_nt + nt) * 8 + wave): nk groups of 64 words
+      const uint32_t unit = (uint32_t)(((int64_t)t.e * n_nt + t.nt) * Q_WAVES + wave);
+      o_off = unit * (uint32_t)nk * (Q_OVL_WORDS * 4) + (uint32_t)lane * 4;
     }
     if constexpr (BT) {
-      // thread t fetches word t & 63 of group (tile's first group + ((t >> 6) & 1));
-      // threads 128..255 repeat 0..127 into the unused upper half
+      // thread t fetches word t & 63 of group (tile's first group + ((t >> 6) & 1))
       int grp = t.nt * (Q_BN / 128) + ((tid >> 6) & 1);
       grp = grp < n_grp ? grp : n_grp - 1;
       z_off = (uint32_t)((((int64_t)t.e * n_grp + grp) * (g.K / 2) * 2 + (tid & 63)) * 4);
     } else {
-      z_off = (uint32_t)((((base + wrow(t, tid)) * g.K) >> 7) * 4);
+      z_off = (uint32_t)((((base + wrow(t, tid & 255)) * g.K) >> 7) * 4);
     }
   };
   // with a row map, the activation rows of tile t are fetched into token buffer
-  // buf by a DMA (visible to all threads after the next barrier); without one
-  // the row is the slot itself
+  // buf by a DMA of waves 0-3 (visible to all threads after the next barrier);
+  // without one the row is the slot itself
   auto tok_fill = [&](const QTile& t, int buf) {
-    if (g.a_rows) {
+    if (g.a_rows && wave < 4) {
       const int r = tid < t.valid ? tid : t.valid - 1;
-      dma4(g.a_rows + t.m_beg, (uint32_t)r * 4, s_tok + buf * Q_BM + wave * 64);
+      // (buf can come out of a vector register: readfirstlane puts the address in a scalar one)
+      dma4(g.a_rows + t.m_beg, (uint32_t)r * 4, (uint32_t)uni((int)(qsm_lds + Q_TOK_OFF + (buf * Q_BM + wave * 64) * 4)));
     }
   };
   auto a_refresh = [&](int ord) {
     if (g.a_rows) {
       const int32_t* src = s_tok + (ord & 1) * Q_BM;
 #pragma unroll
-      for (int c = 0; c < Q_A_LOADS; ++c) a_off[c] = (uint32_t)src[32 * c + (tid >> 3)] * lda_b + a_lc * 16;
+      for (int c = 0; c < Q_A_LOADS; ++c) a_off[c] = (uint32_t)src[64 * c + (tid >> 3)] * lda_b + a_lc * 16;
     } else {
       const QTile t = decode(ord);
 #pragma unroll
       for (int c = 0; c < Q_A_LOADS; ++c) {
-        const int r = 32 * c + (tid >> 3);
+        const int r = 64 * c + (tid >> 3);
         a_off[c] = (uint32_t)(t.m_beg + (r < t.valid ? r : t.valid - 1)) * lda_b + a_lc * 16;
       }
     }
   };
-  // one DMA instruction of a k-step: d = 0, 1 the code chunks, 2 the scale|zero
-  // word (into stage sc_stage), 3 <= d < Q_DMAS activation chunk d - 3 (into
-  // stage sa_stage), OVL: d = Q_DMAS, Q_DMAS + 1 the two halves of the wave's
-  // overlay entries of the code stream's k-step (into stage sc_stage)
+  // one DMA instruction of a k-step (d as for Q_DMAS): codes, scale|zero and
+  // entries into stage sc_stage, activations into stage sa_stage
   auto dma_one = [&](int d, int sc_stage, int sa_stage) {
     sc_stage = uni(sc_stage);
     sa_stage = uni(sa_stage);
     const int c_kt_u = uni(c_kt), a_kt_u = uni(a_kt);
-    if (OVL && d >= Q_DMAS) {
-      const int h = d - Q_DMAS;
-      uint8_t* so = qsm + sc_stage * Q_STAGE + Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES + wave * Q_OVL_GROUP + h * 256;
-      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.ovl) + c_kt_u * Q_OVL_GROUP + h * 256;
-      dma4(base, o_off, so);
-    } else if (d < 2) {
-      uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
-      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wq) + c_kt_u * 32;
-      dma16(base, d ? c_off1 : c_off0, sc + (d * 256 + wave * 64) * 16);
-    } else if (d == 2) {
-      uint8_t* sc = qsm + sc_stage * Q_STAGE + Q_A_BYTES;
-      // per k-step: one scale|zero word per weight row, or (BT) 32 k-pairs x 2 words per group
+    const uint32_t sc = qsm_lds + sc_stage * Q_STAGE + Q_A_BYTES;
+    if (OVL && d == Q_DMAS) {
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.ovl) + c_kt_u * (Q_OVL_WORDS * 4);
+      dma4(base, o_off, sc + Q_C_BYTES + Q_Z_BYTES + wave * (Q_OVL_WORDS * 4));
+    } else if (d == 0) {
+      // per k-step: one scale|zero word per weight row, or (BT) 32 k-pairs x 2 words
+      // per group; the waves past Z_WAVES fetch the same words to the same place
+      // (a branch here would split the step's schedule)
       const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wsz) + (BT ? c_kt_u * 256 : (c_kt_u >> 1) * 4);
-      dma4(base, z_off, sc + Q_C_BYTES + wave * 64 * 4);
+      dma4(base, z_off, sc + Q_C_BYTES + (wave & (Z_WAVES - 1)) * 256);
+    } else if (d == 1) {
+      const uint8_t* base = reinterpret_cast<const uint8_t*>(g.wq) + c_kt_u * 32;
+      dma16(base, c_off, sc + wave * 64 * 16);
     } else {
-      const int c = d - 3;
-      uint8_t* sa = qsm + sa_stage * Q_STAGE;
+      const int c = d - 2;
       const uint8_t* base = reinterpret_cast<const uint8_t*>(g.A) + a_kt_u * (BK * 2);
-      dma16(base, a_off[c], sa + (c * 256 + wave * 64) * 16);
+      dma16(base, a_off[c], qsm_lds + sa_stage * Q_STAGE + (c * Q_THREADS + wave * 64) * 16);
     }
   };
   // start of a k-step: the activation stream picks up the rows of the tile it
@@ -1367,20 +1384,24 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     }
   };
   // end of a k-step: advance both streams (past the last tile they repeat the
-  // last k-step into a stage nobody reads)
+  // last k-step into a stage nobody reads).  The stream state goes through
+  // readfirstlane: it is uniform, and the compiler then keeps it in scalar
+  // registers and branches on it with scalar branches.
   auto advance = [&]() {
-    if (++c_kt == nk) {
+    c_kt = uni(c_kt + 1);
+    if (c_kt == nk) {
       if (c_ord + 1 < n_my) {
-        ++c_ord;
+        c_ord = uni(c_ord + 1);
         c_kt = 0;
         c_setup(c_next);
       } else {
         c_kt = nk - 1;
       }
     }
-    if (++a_kt == nk) {
+    a_kt = uni(a_kt + 1);
+    if (a_kt == nk) {
       if (a_ord + 1 < n_my) {
-        ++a_ord;
+        a_ord = uni(a_ord + 1);
         a_kt = 0;
         a_enter = true;
       } else {
@@ -1389,25 +1410,30 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     }
   };
 
-  // ---- weight fragments: wf[slot][column block][sub-step j]; lane half h holds
-  //      k = 32h + 8j + [0, 8) of weight row 32cb + l32 of the wave ----
-  u32x4 wf[2][2][4];
-  // codes of the lane's weight rows and their scale|zero: one pair per row, or
+  // ---- weight fragments: wf[set][sub-step j]; lane half h holds
+  //      k = 32h + 8j + [0, 8) of weight row 32 wave + l32 ----
+  u32x4 wf[2][4];
+  // per-lane LDS byte offsets within a stage (the stage offset is uniform):
+  // activation fragment j of slot block i at fb_j + 4096 i (the swizzle of row
+  // 32 i + l32 does not depend on i), the lane's codes, its scale|zero word
+  uint32_t fb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fb[j] = (uint32_t)(128 * l32 + 16 * ((4 * half + j) ^ q_swz(l32)));
+  const uint32_t cb_off = (uint32_t)(Q_A_BYTES + (2 * (32 * wave + l32) + half) * 16);
+  const uint32_t zb_off = (uint32_t)(Q_A_BYTES + Q_C_BYTES + (32 * wave + l32) * 4);
+  // codes of the lane's weight row and its scale|zero: one pair per row, or
   // (BT) the 16 k-pairs {s2, z2} of k = 32 half + [0, 32) of the wave's group
-  // (a wave's 64 columns never straddle a 128-column group)
-  auto codes_read = [&](int stage, u32x4 (&cq)[2], uint32_t (&csz)[2], u32x4 (&kz)[8]) {
-    const uint8_t* sc = qsm + stage * Q_STAGE + Q_A_BYTES;
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int b = 64 * wave + 32 * cb + l32;
-      cq[cb] = *reinterpret_cast<const u32x4*>(sc + (2 * b + half) * 16);
-      if constexpr (!BT) csz[cb] = *reinterpret_cast<const uint32_t*>(sc + Q_C_BYTES + b * 4);
-    }
-    if constexpr (BT) {
-      const uint8_t* zg = sc + Q_C_BYTES + ((wave >> 1) * 64 + 32 * half) * 4;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) kz[i] = *reinterpret_cast<const u32x4*>(zg + 16 * i);
-    }
+  // (a wave's 32 rows never straddle a 128-row group)
+  auto codes_read = [&](int stage, u32x4& cq, uint32_t& csz) {
+    const uint8_t* st = qsm + stage * Q_STAGE;
+    cq = *reinterpret_cast<const u32x4*>(st + cb_off);
+    if constexpr (!BT) csz = *reinterpret_cast<const uint32_t*>(st + zb_off);
+  };
+  // BT: the k-pair words of fragment register wd (kz[2 wd], kz[2 wd + 1])
+  auto kz_read = [&](int stage, int wd, u32x4 (&kz)[8]) {
+    const uint8_t* zg = qsm + stage * Q_STAGE + Q_A_BYTES + Q_C_BYTES + ((wave >> 2) * 64 + 32 * half) * 4;
+    kz[2 * wd] = *reinterpret_cast<const u32x4*>(zg + 32 * wd);
+    kz[2 * wd + 1] = *reinterpret_cast<const u32x4*>(zg + 32 * wd + 16);
   };
   // k-pair p4 (= 4 wd + q, k = 32 half + 2 p4) of the BT words: {s2, z2}
   auto kz_pair = [&](const u32x4 (&kz)[8], int p4, f16x2& s2, f16x2& z2) {
@@ -1417,24 +1443,23 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   };
   auto dequant_all = [&](auto bs_c, int stage) {
     constexpr int BS = decltype(bs_c)::value;
-    u32x4 cq[2], kz[8];
-    uint32_t csz[2];
-    codes_read(stage, cq, csz, kz);
+    u32x4 cq, kz[8];
+    uint32_t csz = 0;
+    codes_read(stage, cq, csz);
+    if constexpr (BT) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      if constexpr (BT) {
+      for (int wd = 0; wd < 4; ++wd) kz_read(stage, wd, kz);
 #pragma unroll
-        for (int p = 0; p < 16; ++p) {
-          f16x2 s2, z2;
-          kz_pair(kz, p, s2, z2);
-          wf[BS][cb][p >> 2][p & 3] = dq_pair<DT>(cq[cb][p >> 2], p & 3, s2, z2);
-        }
-      } else {
-        const f16x2 s2 = __builtin_bit_cast(f16x2, (csz[cb] & 0xFFFFu) * 0x10001u);
-        const f16x2 z2 = __builtin_bit_cast(f16x2, (csz[cb] >> 16) * 0x10001u);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wf[BS][cb][j] = dq8<DT>(cq[cb][j], s2, z2);
+      for (int p = 0; p < 16; ++p) {
+        f16x2 s2, z2;
+        kz_pair(kz, p, s2, z2);
+        wf[BS][p >> 2][p & 3] = dq_pair<DT>(cq[p >> 2], p & 3, s2, z2);
       }
+    } else {
+      const f16x2 s2 = __builtin_bit_cast(f16x2, (csz & 0xFFFFu) * 0x10001u);
+      const f16x2 z2 = __builtin_bit_cast(f16x2, (csz >> 16) * 0x10001u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wf[BS][j] = dq8<DT>(cq[j], s2, z2);
     }
   };
 
@@ -1442,131 +1467,136 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   uint16_t* const sEp = q_ep + wave * Q_EP_ELEMS;
   const uint32_t sEp_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sEp;
 
-  // OVL: the entries of the wave's next k-step (stage `stage`): this lane's two
-  // words, {byte offset in the 8 KiB fragment image | value << 16}.
-  auto ovl_entries = [&](int stage, uint32_t& e0, uint32_t& e1) {
-    const uint8_t* ent = qsm + uni(stage) * Q_STAGE + Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES + wave * Q_OVL_GROUP;
-    e0 = *reinterpret_cast<const uint32_t*>(ent + lane * 8);
-    e1 = *reinterpret_cast<const uint32_t*>(ent + lane * 8 + 4);
+  // OVL: this lane's entry word of the wave's next k-step (stage `stage`)
+  auto ovl_entry = [&](int stage) -> uint32_t {
+    const uint8_t* ent = qsm + uni(stage) * Q_STAGE + Q_A_BYTES + Q_C_BYTES + Q_Z_BYTES + wave * (Q_OVL_WORDS * 4);
+    return *reinterpret_cast<const uint32_t*>(ent + lane * 4);
   };
-  // OVL: fragment register j of set BSX (both column blocks) through the image:
-  // lane l's 16 bytes of column block cb at (64 cb + l) * 16; lanes 16 j..16 j + 15
-  // store their two entries over it (exec narrowed to them inside one asm block,
-  // no branch), and the registers are read back.  The stores are explicit
-  // ds_write instructions (a compiler-visible LDS store would make it drain the
-  // DMAs in flight first); the LDS operations of one wave complete in order, so
-  // the reads see the stores before them.  a0/a1: LDS addresses of the lane's
-  // two entries, d0/d1: their values.
-  auto ovl_patch_j = [&](auto bsx_c, auto j_c, uint32_t a0, uint32_t d0, uint32_t a1, uint32_t d1) {
+  // OVL: fragment register j of set BSX through the image: lane l's 16 bytes
+  // at l * 16; lanes 16 j..16 j + 15 store their entry over it, the other lanes
+  // store into the dummy area (a lane-mask select of the address, no exec
+  // change), and the register is read back.  The stores are explicit ds_write
+  // instructions (a compiler-visible LDS store would make it drain the DMAs in
+  // flight first); the LDS operations of one wave complete in order, so the
+  // read sees the stores before it.  a: LDS address of the lane's entry, d: its value.
+  const uint32_t img_lds = sEp_lds + (uint32_t)lane * 16;
+  const uint32_t dummy_lds = sEp_lds + Q_IMG + (uint32_t)lane * 2;
+  const int my_j = lane >> 4;
+  auto ovl_patch_j = [&](auto bsx_c, auto j_c, uint32_t a, uint32_t d) {
     constexpr int BSX = decltype(bsx_c)::value, J = decltype(j_c)::value;
-    constexpr uint32_t lo = J == 0 ? 0x0000FFFFu : (J == 1 ? 0xFFFF0000u : 0u);
-    constexpr uint32_t hi = J == 2 ? 0x0000FFFFu : (J == 3 ? 0xFFFF0000u : 0u);
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-      asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(sEp_lds + (uint32_t)lane * 16), "v"(wf[BSX][cb][J]),
-                   "i"(cb * 1024)
-                   : "memory");
-    uint64_t saved;
-    asm volatile(
-        "s_mov_b64 %0, exec\n\t"
-        "s_mov_b32 exec_lo, %5\n\t"
-        "s_mov_b32 exec_hi, %6\n\t"
-        "s_nop 1\n\t"
-        "ds_write_b16 %1, %2\n\t"
-        "ds_write_b16 %3, %4\n\t"
-        "s_mov_b64 exec, %0"
-        : "=&s"(saved)
-        : "v"(a0), "v"(d0), "v"(a1), "v"(d1), "i"(lo), "i"(hi)
-        : "memory");
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-      wf[BSX][cb][J] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(sEp) + (64 * cb + lane) * 16);
+    const uint32_t addr = my_j == J ? a : dummy_lds;
+    asm volatile("ds_write_b128 %0, %1\n\tds_write_b16 %2, %3" ::"v"(img_lds), "v"(wf[BSX][J]), "v"(addr), "v"(d)
+                 : "memory");
+    wf[BSX][J] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(sEp) + lane * 16);
+  };
+  auto ovl_patch_wd = [&](auto bsx_c, int wd, uint32_t a, uint32_t d) {
+    switch (wd) {  // wd is a constant after unrolling: one case survives
+      case 0: ovl_patch_j(bsx_c, std::integral_constant<int, 0>{}, a, d); break;
+      case 1: ovl_patch_j(bsx_c, std::integral_constant<int, 1>{}, a, d); break;
+      case 2: ovl_patch_j(bsx_c, std::integral_constant<int, 2>{}, a, d); break;
+      default: ovl_patch_j(bsx_c, std::integral_constant<int, 3>{}, a, d); break;
+    }
   };
 
   // ---- one k-step: MFMAs of k-step gs (activations in stage s0, weights in
-  //      slot BS) with the dequant of k-step gs + 1 (codes in stage s1) into
-  //      slot BS ^ 1; the k-step's DMAs (codes of gs + 3 into stage s0,
-  //      activations of gs + 2 into stage s2) are spread over its regions so
-  //      that the four waves do not queue them on the memory pipe at once ----
-  auto step = [&](auto bs_c, auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value][2], int s0, int s1, int s2) {
+  //      set BS) with the dequant of k-step gs + 1 (codes in stage s1) into
+  //      set BS ^ 1; the k-step's DMAs (codes of gs + 3 into stage s0,
+  //      activations of gs + 2 into stage s2) are spread over its regions ----
+  constexpr int QD = Q_DMAS + (OVL ? 1 : 0);  // DMA instructions of a full step
+  auto step = [&](auto bs_c, auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value], int s0, int s1, int s2) {
     constexpr int BS = decltype(bs_c)::value, NRB = decltype(nrb_c)::value;
-    constexpr int NF = 4 * NRB;     // activation fragments, f = j * NRB + i
-    constexpr int R = NF / 2;       // regions of two fragments (four MFMAs)
-    constexpr int PF = 4;           // fragment prefetch distance
-    constexpr int PPR = (32 + R - 2) / (R - 1);  // weight pairs dequantized per region (regions 1..R-1)
-    constexpr int QD = Q_DMAS + (OVL ? Q_OVL_DMAS : 0);  // DMA instructions of the step
-    constexpr int DPR = (QD + R - 1) / R;        // DMAs issued per region
+    constexpr int NF = 4 * NRB;   // activation fragments = MFMAs, f = j * NRB + i
+    constexpr int R = NF / 2;     // regions of two MFMAs
+    constexpr int PF = 4;         // fragment prefetch distance
+    constexpr int NP = 16;        // weight pairs per lane and k-step
+    // Pair p goes to region 1 + p (R - 1) / NP and DMA d to region d R / QD:
+    // spread evenly, so that every region holds about the same MFMA, VALU and
+    // memory work and the two waves of a SIMD overlap them in any phase.
+    auto rp = [](int p) { return 1 + p * (R - 1) / NP; };
+    auto rd = [](int d) { return d * R / QD; };
     pre_step();
-    u32x4 cq[2], kz[8];
-    uint32_t csz[2];
-    codes_read(s1, cq, csz, kz);
-    uint32_t oa0 = 0, od0 = 0, oa1 = 0, od1 = 0;
+    u32x4 cq, kz[8];
+    uint32_t csz = 0;
+    codes_read(s1, cq, csz);
+    // BT: the words of register wd are read one region before its first pair
+    if constexpr (BT) kz_read(s1, 0, kz);
+    uint32_t oa = 0, od = 0;
     if constexpr (OVL) {
-      uint32_t e0, e1;
-      ovl_entries(s1, e0, e1);
-      oa0 = sEp_lds + (e0 & 0xFFFFu);
-      od0 = e0 >> 16;
-      oa1 = sEp_lds + (e1 & 0xFFFFu);
-      od1 = e1 >> 16;
+      const uint32_t e = ovl_entry(s1);
+      oa = sEp_lds + (e & 0xFFFFu);
+      od = e >> 16;
     }
     const uint8_t* sa = qsm + s0 * Q_STAGE;
     auto frag = [&](int f) -> u32x4 {
       const int i = f % NRB, j = f / NRB;
-      const int m = 32 * i + l32;
-      return *reinterpret_cast<const u32x4*>(sa + m * 128 + 16 * ((4 * half + j) ^ q_swz(m)));
+      return *reinterpret_cast<const u32x4*>(sa + fb[j] + 4096 * i);
     };
     u32x4 af[NF];
 #pragma unroll
     for (int f = 0; f < PF; ++f) af[f] = frag(f);
-    f16x2 s2v[2], z2v[2];
+    f16x2 s2v = {}, z2v = {};
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+      // The two waves of a SIMD run the same step; the older one wins every
+      // issue tie and would finish the step far ahead, leaving the younger to
+      // run the step's tail alone.  Each wave lowers its priority as it passes
+      // the quarter marks of the step, so the leader yields to the other.
+      if (r * 4 % R == 0) {
+        switch (r * 4 / R) {  // a constant after unrolling
+          case 0: __builtin_amdgcn_s_setprio(3); break;
+          case 1: __builtin_amdgcn_s_setprio(2); break;
+          case 2: __builtin_amdgcn_s_setprio(1); break;
+          default: __builtin_amdgcn_s_setprio(0); break;
+        }
+      }
 #pragma unroll
       for (int gg = 0; gg < 2; ++gg) {
         const int f = 2 * r + gg, i = f % NRB, j = f / NRB;
         if (f + PF < NF) af[f + PF] = frag(f + PF);
-        acc[i][0] = mfma32<DT>(wf[BS][0][j], af[f], acc[i][0]);
-        acc[i][1] = mfma32<DT>(wf[BS][1][j], af[f], acc[i][1]);
+        acc[i] = mfma32<DT>(wf[BS][j], af[f], acc[i]);
       }
 #pragma unroll
-      for (int dd = 0; dd < DPR; ++dd)
-        if (r * DPR + dd < QD) dma_one(r * DPR + dd, s0, s2);
-      if (r >= 1) {
-        // the pairs of k-step gs + 1 in register-major order: pair p is half-word
-        // pair q of fragment register j of column block cb
+      for (int d = 0; d < QD; ++d)
+        if (rd(d) == r) dma_one(d, s0, s2);
+      if constexpr (BT) {
 #pragma unroll
-        for (int pp = 0; pp < PPR; ++pp) {
-          const int p = (r - 1) * PPR + pp;
-          if (p < 32) {
-            const int wd = p >> 3, cb = (p >> 2) & 1, q = p & 3;
-            uint32_t v;
+        for (int wd = 1; wd < 4; ++wd)
+          if (rp(4 * wd) - 1 == r) kz_read(s1, wd, kz);
+      }
+      if (r >= 1) {
+        // this region's pairs p (half-word pair q = p & 3 of fragment register
+        // wd = p >> 2), computed together (independent chains) and pinned here
+        uint32_t v[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          if (rp(p) == r) {
+            const int wd = p >> 2, q = p & 3;
+            // the code word passes an empty asm here, so the pair's arithmetic
+            // cannot be hoisted into an earlier region
+            uint32_t cw = cq[wd];
+            asm volatile("" : "+v"(cw));
             if constexpr (BT) {
               f16x2 s2, z2;
-              kz_pair(kz, 4 * wd + q, s2, z2);
-              v = dq_pair<DT>(cq[cb][wd], q, s2, z2);
+              kz_pair(kz, p, s2, z2);
+              v[p] = dq_pair<DT>(cw, q, s2, z2);
             } else {
               if (p == 0) {
-#pragma unroll
-                for (int c2 = 0; c2 < 2; ++c2) {
-                  s2v[c2] = __builtin_bit_cast(f16x2, (csz[c2] & 0xFFFFu) * 0x10001u);
-                  z2v[c2] = __builtin_bit_cast(f16x2, (csz[c2] >> 16) * 0x10001u);
-                }
+                s2v = __builtin_bit_cast(f16x2, (csz & 0xFFFFu) * 0x10001u);
+                z2v = __builtin_bit_cast(f16x2, (csz >> 16) * 0x10001u);
               }
-              v = dq_pair<DT>(cq[cb][wd], q, s2v[cb], z2v[cb]);
+              v[p] = dq_pair<DT>(cw, q, s2v, z2v);
             }
-            asm volatile("" : "+v"(v));  // computed here, next to the MFMAs, not sunk to its first use
-            wf[BS ^ 1][cb][wd][q] = v;
-            // register wd of both column blocks complete: its trained values, now
+          }
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          if (rp(p) == r) {
+            const int wd = p >> 2, q = p & 3;
+            asm volatile("" : "+v"(v[p]));  // computed here, next to the MFMAs, not sunk to its first use
+            wf[BS ^ 1][wd][q] = v[p];
+            // register wd complete: its trained values, now
             if constexpr (OVL) {
-              if ((p & 7) == 7) {  // p is a constant after unrolling: one case survives
-                using BX = std::integral_constant<int, BS ^ 1>;
-                switch (p >> 3) {
-                  case 0: ovl_patch_j(BX{}, std::integral_constant<int, 0>{}, oa0, od0, oa1, od1); break;
-                  case 1: ovl_patch_j(BX{}, std::integral_constant<int, 1>{}, oa0, od0, oa1, od1); break;
-                  case 2: ovl_patch_j(BX{}, std::integral_constant<int, 2>{}, oa0, od0, oa1, od1); break;
-                  default: ovl_patch_j(BX{}, std::integral_constant<int, 3>{}, oa0, od0, oa1, od1); break;
-                }
-              }
+              if (q == 3) ovl_patch_wd(std::integral_constant<int, BS ^ 1>{}, wd, oa, od);
             }
           }
         }
@@ -1574,20 +1604,20 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       __builtin_amdgcn_sched_barrier(0);
     }
     advance();
-    // this step's 11 DMAs (13 with OVL) may stay in flight; everything older
-    // (the stages the next step reads, the token rows) has landed in this wave,
-    // and after the barrier in all waves.  sched_barrier keeps the step's
-    // register work on its side of the barrier.
+    // this step's QD DMAs may stay in flight; everything older (the stages the
+    // next step reads, the token rows) has landed in this wave, and after the
+    // barrier in all waves.  sched_barrier keeps the step's register work on
+    // its side of the barrier.
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (OVL) asm volatile("s_waitcnt vmcnt(13)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(11)\n\ts_barrier" ::: "memory");
+    if constexpr (OVL) asm volatile("s_waitcnt vmcnt(7)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
+  static_assert(QD == (OVL ? 7 : 6), "the step's vmcnt wait counts its DMAs");
 
   // ---- epilogue: per 32-slot block, the wave's dtype results go through its
-  //      own LDS tile ([32 slots][96 columns]: gate, up, act or the 64 output
-  //      columns) and out as 16-byte row stores, 4-8 lanes per row segment ----
-  // lane's accumulator values r = 4q..4q+3 of weight block cb -> columns 32cb + 8q + 4half + [0,4) of slot l32.
+  //      own LDS tile ([32 slots][Q_EPW]) and out as 16-byte row stores ----
+  // lane's accumulator values r = 4q..4q+3 -> columns 8q + 4half + [0,4) of slot l32.
   // Written with an explicit ds_write_b64: the compiler would otherwise drain
   // every DMA in flight (the next tile's first k-steps) before an LDS store.
   // The wave's own LDS operations complete in order, so the reads below see it.
@@ -1596,11 +1626,12 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     const uint64_t v = (uint64_t)lo | ((uint64_t)hi << 32);
     asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(v) : "memory");
   };
-  auto epilogue = [&](auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value][2], const QTile& t) {
+  auto epilogue = [&](auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value], const QTile& t) {
     constexpr int NRB = decltype(nrb_c)::value;
     if constexpr (EPI == EPI_SWIGLU_FWD) {
-      const int64_t n0 = (int64_t)t.nt * 128 + wave * 32;
-      if (n0 >= g.inter) return;
+      // staging columns: gate [0, 16), up [16, 32), act [32, 48) of the wave's 16 n
+      const int64_t n0 = (int64_t)t.nt * 128 + wave * 16;
+      if (n0 >= g.inter) return;  // I % 16 == 0
       // blocked act^T: the expert's block holds, per feature n, ld = round_up(se, 16)
       // slots (zero past se); tblk points at feature n0's row of it
       uint16_t* tblk = nullptr;
@@ -1616,54 +1647,58 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       for (int i = 0; i < NRB; ++i) {
         if (32 * i >= t.valid) break;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 2; ++q) {
           uint32_t gb[2], ub[2], ab[2];
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) {
-            gb[h2] = pack2<DT>(acc[i][0][4 * q + 2 * h2], acc[i][0][4 * q + 2 * h2 + 1]);
-            ub[h2] = pack2<DT>(acc[i][1][4 * q + 2 * h2], acc[i][1][4 * q + 2 * h2 + 1]);
+            gb[h2] = pack2<DT>(acc[i][4 * q + 2 * h2], acc[i][4 * q + 2 * h2 + 1]);
+            ub[h2] = pack2<DT>(acc[i][8 + 4 * q + 2 * h2], acc[i][8 + 4 * q + 2 * h2 + 1]);
             const f32x2 gf = unpack2<DT>(gb[h2]), uf = unpack2<DT>(ub[h2]);
             const f32x2 sf = unpack2<DT>(pack2<DT>(silu_fast(gf.x), silu_fast(gf.y)));
             ab[h2] = pack2<DT>(sf.x * uf.x, sf.y * uf.y);
           }
           const int col = 8 * q + 4 * half;
           stage4(col, gb[0], gb[1]);
-          stage4(32 + col, ub[0], ub[1]);
-          stage4(64 + col, ab[0], ab[1]);
+          stage4(16 + col, ub[0], ub[1]);
+          stage4(32 + col, ab[0], ab[1]);
         }
-        // 32 rows x 3 x 64 B: lane l takes 16-byte chunk l & 3 of row (l >> 2) + 16p
+        // gate and up: 32 rows x 2 x 32 B; lane l takes row (l >> 2) + 16p,
+        // gate or up by bit 1, 16-byte chunk l & 1
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           const int rr = (lane >> 2) + 16 * p;
           if (32 * i + rr < t.valid) {
             const int64_t m = t.m_beg + 32 * i + rr;
-            const int ch = (lane & 3) * 8;
-            const u32x4 gv = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
-            const u32x4 uv = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + 32 + ch);
-            const u32x4 av = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + 64 + ch);
-            *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + n0 + ch) = gv;
-            *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + g.inter + n0 + ch) = uv;
-            *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n0 + ch) = av;
+            const int part = (lane >> 1) & 1, ch = (lane & 1) * 8;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + 16 * part + ch);
+            *reinterpret_cast<u32x4*>(g.out2 + m * g.ldo2 + (part ? g.inter : 0) + n0 + ch) = v;
+          }
+        }
+        // act: 32 rows x 32 B; lane l takes row l >> 1, chunk l & 1
+        {
+          const int rr = lane >> 1;
+          if (32 * i + rr < t.valid) {
+            const int64_t m = t.m_beg + 32 * i + rr;
+            const int ch = (lane & 1) * 8;
+            *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n0 + ch) =
+                *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + 32 + ch);
           }
         }
         if (tblk) {
-          // the staged act columns read down the slots: chunk c = lane + 64 p is
-          // feature c >> 2, slots 8 (c & 3) + [0, 8) of block i, one 16-byte store
-          // per chunk; slots at or past se (padding up to ld) are zero
+          // the staged act columns read down the slots: lane l is feature l >> 2,
+          // slots 8 (l & 3) + [0, 8) of block i, one 16-byte store; slots at or
+          // past se (padding up to ld) are zero
+          const int f = lane >> 2, sg = lane & 3;
+          const int j = jt + 32 * i + 8 * sg;
+          if (j < ld) {
+            uint32_t w[4];
 #pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            const int c = lane + 64 * p, f = c >> 2, sg = c & 3;
-            const int j = jt + 32 * i + 8 * sg;
-            if (j < ld) {
-              uint32_t w[4];
-#pragma unroll
-              for (int k2 = 0; k2 < 4; ++k2) {
-                const uint32_t lo = j + 2 * k2 < se ? sEp[(8 * sg + 2 * k2) * Q_EPW + 64 + f] : 0u;
-                const uint32_t hi = j + 2 * k2 + 1 < se ? sEp[(8 * sg + 2 * k2 + 1) * Q_EPW + 64 + f] : 0u;
-                w[k2] = lo | (hi << 16);
-              }
-              *reinterpret_cast<u32x4*>(tblk + f * (int64_t)ld + j) = u32x4{w[0], w[1], w[2], w[3]};
+            for (int k2 = 0; k2 < 4; ++k2) {
+              const uint32_t lo = j + 2 * k2 < se ? sEp[(8 * sg + 2 * k2) * Q_EPW + 32 + f] : 0u;
+              const uint32_t hi = j + 2 * k2 + 1 < se ? sEp[(8 * sg + 2 * k2 + 1) * Q_EPW + 32 + f] : 0u;
+              w[k2] = lo | (hi << 16);
             }
+            *reinterpret_cast<u32x4*>(tblk + f * (int64_t)ld + j) = u32x4{w[0], w[1], w[2], w[3]};
           }
         }
       }
@@ -1674,22 +1709,20 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       // into dgu[m, n] and dgu[m, I + n].  da goes through the LDS tile; the
       // math then runs on 16-byte row chunks (8 columns) next to coalesced gu
       // loads and dgu stores, in a loop that is not unrolled (code size)
-      const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 64;
-      if (n0 >= g.N) return;  // N % 64 == 0
+      const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 32;
+      if (n0 >= g.N) return;  // N % 32 == 0
 #pragma unroll
       for (int i = 0; i < NRB; ++i) {
         if (32 * i >= t.valid) break;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            stage4(32 * cb + 8 * q + 4 * half, pack2<DT>(acc[i][cb][4 * q], acc[i][cb][4 * q + 1]),
-                   pack2<DT>(acc[i][cb][4 * q + 2], acc[i][cb][4 * q + 3]));
+        for (int q = 0; q < 4; ++q)
+          stage4(8 * q + 4 * half, pack2<DT>(acc[i][4 * q], acc[i][4 * q + 1]),
+                 pack2<DT>(acc[i][4 * q + 2], acc[i][4 * q + 3]));
         const int rows_left = t.valid - 32 * i;
-        const int ch = (lane & 7) * 8;
+        const int ch = (lane & 3) * 8;
 #pragma unroll 1
-        for (int p = 0; p < 4; ++p) {
-          const int rr = (lane >> 3) + 8 * p;
+        for (int p = 0; p < 2; ++p) {
+          const int rr = (lane >> 2) + 16 * p;
           if (rr < rows_left) {
             const int64_t m = t.m_beg + 32 * i + rr;
             const u32x4 dv = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
@@ -1718,28 +1751,26 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
         }
       }
     } else {
-      const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 64;
-      if (n0 >= g.N) return;  // N % 64 == 0: a wave's 64 columns are all valid or none
+      const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 32;
+      if (n0 >= g.N) return;  // N % 32 == 0: a wave's 32 columns are all valid or none
 #pragma unroll
       for (int i = 0; i < NRB; ++i) {
         if (32 * i >= t.valid) break;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            stage4(32 * cb + 8 * q + 4 * half, pack2<DT>(acc[i][cb][4 * q], acc[i][cb][4 * q + 1]),
-                   pack2<DT>(acc[i][cb][4 * q + 2], acc[i][cb][4 * q + 3]));
-        // 32 rows x 128 B: lane l takes 16-byte chunk l & 7 of row (l >> 3) + 8p
+        for (int q = 0; q < 4; ++q)
+          stage4(8 * q + 4 * half, pack2<DT>(acc[i][4 * q], acc[i][4 * q + 1]),
+                 pack2<DT>(acc[i][4 * q + 2], acc[i][4 * q + 3]));
+        // 32 rows x 64 B: lane l takes 16-byte chunk l & 3 of row (l >> 2) + 16p
         // (a wave-uniform row base plus one 32-bit lane offset)
         uint8_t* const rowbase = reinterpret_cast<uint8_t*>(g.out + ((int64_t)t.m_beg + 32 * i) * g.ldo + n0);
-        const uint32_t loff = (uint32_t)(((lane >> 3) * g.ldo + (lane & 7) * 8) * 2);
+        const uint32_t loff = (uint32_t)(((lane >> 2) * g.ldo + (lane & 3) * 8) * 2);
         const int rows_left = t.valid - 32 * i;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const int rr = (lane >> 3) + 8 * p;
+        for (int p = 0; p < 2; ++p) {
+          const int rr = (lane >> 2) + 16 * p;
           if (rr < rows_left)
-            *reinterpret_cast<u32x4*>(rowbase + (size_t)p * 16 * g.ldo + loff) =
-                *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + (lane & 7) * 8);
+            *reinterpret_cast<u32x4*>(rowbase + (size_t)p * 32 * g.ldo + loff) =
+                *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + (lane & 3) * 8);
         }
       }
     }
@@ -1758,10 +1789,10 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     a_refresh(0);
   }
-  constexpr int QD = Q_DMAS + (OVL ? Q_OVL_DMAS : 0);
-  for (int d = 0; d < 3; ++d) dma_one(d, 0, 0);  // codes 0
-  for (int d = Q_DMAS; d < QD; ++d) dma_one(d, 0, 0);  // OVL: their entries
-  if (nk == 2 && n_my > 1) {                       // the code stream enters tile 1 after codes 1
+  dma_one(0, 0, 0);                            // codes 0: scale|zero
+  dma_one(1, 0, 0);                            // codes 0
+  if constexpr (OVL) dma_one(Q_DMAS, 0, 0);    // their entries
+  if (nk == 2 && n_my > 1) {                   // the code stream enters tile 1 after codes 1
     c_next = decode(1);
     tok_fill(c_next, 1);
   }
@@ -1782,13 +1813,12 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   dequant_all(I0{}, 0);
   if constexpr (OVL) {  // k-step 0: its entries are in stage 0
-    uint32_t e0, e1;
-    ovl_entries(0, e0, e1);
-    const uint32_t a0 = sEp_lds + (e0 & 0xFFFFu), d0 = e0 >> 16, a1 = sEp_lds + (e1 & 0xFFFFu), d1 = e1 >> 16;
-    ovl_patch_j(I0{}, std::integral_constant<int, 0>{}, a0, d0, a1, d1);
-    ovl_patch_j(I0{}, std::integral_constant<int, 1>{}, a0, d0, a1, d1);
-    ovl_patch_j(I0{}, std::integral_constant<int, 2>{}, a0, d0, a1, d1);
-    ovl_patch_j(I0{}, std::integral_constant<int, 3>{}, a0, d0, a1, d1);
+    const uint32_t e = ovl_entry(0);
+    const uint32_t a = sEp_lds + (e & 0xFFFFu), d = e >> 16;
+    ovl_patch_j(I0{}, integral_constant<int, 0>{}, a, d);
+    ovl_patch_j(I0{}, integral_constant<int, 1>{}, a, d);
+    ovl_patch_j(I0{}, integral_constant<int, 2>{}, a, d);
+    ovl_patch_j(I0{}, integral_constant<int, 3>{}, a, d);
   }
   asm volatile("s_barrier" ::: "memory");  // stage 0's codes are refilled by k-step 0
 
@@ -1799,15 +1829,15 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     const int nrb = (t.valid + 31) >> 5;
     auto run = [&](auto nrb_c) {
       constexpr int NRB = decltype(nrb_c)::value;
-      f32x16 acc[NRB][2];
+      f32x16 acc[NRB];
 #pragma unroll
-      for (int i = 0; i < NRB; ++i) acc[i][0] = acc[i][1] = f32x16{};
+      for (int i = 0; i < NRB; ++i) acc[i] = f32x16{};
       for (int kt = 0; kt < nk; kt += 2) {
-        int s1 = s0 == 2 ? 0 : s0 + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+        int s1 = uni(s0 == 2 ? 0 : s0 + 1), s2 = uni(s1 == 2 ? 0 : s1 + 1);
         step(I0{}, nrb_c, acc, s0, s1, s2);
         s0 = s1;
         s1 = s2;
-        s2 = s2 == 2 ? 0 : s2 + 1;
+        s2 = uni(s2 == 2 ? 0 : s2 + 1);
         step(I1{}, nrb_c, acc, s0, s1, s2);
         s0 = s1;
       }
@@ -1866,11 +1896,11 @@ int launch_q4_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   return USAF_OK;
 }
 
-// Entry words of an overlay for this GEMM: 4 waves x (K / 64) k-steps x 128 per
+// Entry words of an overlay for this GEMM: 8 waves x (K / 64) k-steps x 64 per
 // (expert, n-tile); the kernel addresses them with 32-bit byte offsets.
 int64_t ovl_words(const GemmArgs& g, int epi) {
   const int64_t n_nt = epi == EPI_SWIGLU_FWD ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
-  return (int64_t)g.E * n_nt * 4 * (g.K / BK) * 128;
+  return (int64_t)g.E * n_nt * Q_WAVES * (g.K / BK) * Q_OVL_WORDS;
 }
 
 int check_ovl(const GemmArgs& g, int epi, const char* what) {

@@ -123,7 +123,8 @@ _T_MAX_E = 255
 #   down_bwd     W = down^T (transposed copy), n = c, k = r
 #   gate_up_bwd  W = gate_up^T,                n = c, k = r
 _OVL_KINDS = {"gate_up": ("gate_up_fwd", "gate_up_bwd"), "down": ("down_fwd", "down_bwd")}
-_OVL_CAP = 32  # entries per (wave, k-step, fragment register): two 16-bit LDS stores by each of 16 lanes
+_OVL_CAP = 16  # entries per (wave, k-step, fragment register): one 16-bit LDS store by each of 16 lanes
+_OVL_WAVES, _OVL_WORDS = 8, 64  # waves per n-tile, entry words per wave and k-step
 
 
 def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
@@ -132,17 +133,20 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     usaf_hip_moe_*(overlay=...) name it.  Returns (word int32 [n], byte offset
     int32 [n], table words).
 
-    The GEMM's tile unit u = (e * n_nt + nt) * 4 + w is wave w of n-tile nt of
-    expert e; the wave holds 64 weight rows as two 32-row column blocks cb, and
-    per k-step of 64 contraction elements lane l32 + 32 h holds k = 32 h + 8 j +
-    [0, 8) of row 32 cb + l32 as fragment registers j = 0..3.  Register j goes
-    through a 2 KiB image that puts lane l's copy of column block cb at byte
-    (64 cb + l) * 16, so the weight at k-step offset kk = 32 h + 8 j + 2 q + b
-    (b: low or high half of dword q) sits at byte (64 cb + l32 + 32 h) * 16 +
-    4 q + 2 b of register j's image.  The entries of one (u, k-step, j) are
-    ranked in position order; rank r goes to word (u * nk + ks) * 128 +
-    32 j + r (lanes 16 j..16 j + 15 store them).  More than 32 positions in one
-    register's 64 x 16 block of a wave (3 % local density) raise ValueError."""
+    The GEMM's tile unit u = (e * n_nt + nt) * 8 + w is wave w of n-tile nt of
+    expert e; the wave holds 32 weight rows l32 = 0..31 (tile rows 32 w + l32),
+    and per k-step of 64 contraction elements lane l32 + 32 h holds k = 32 h +
+    8 j + [0, 8) of its row as fragment registers j = 0..3.  Register j goes
+    through a 1 KiB image that puts lane l's copy at byte 16 l, so the weight at
+    k-step offset kk = 32 h + 8 j + 2 q + b (b: low or high half of dword q)
+    sits at byte (l32 + 32 h) * 16 + 4 q + 2 b of register j's image.  Tile
+    rows: n-tile nt covers weight rows 256 nt + [0, 256); for the SwiGLU
+    forward it covers n = 128 nt + [0, 128), wave w taking gate rows n = 128 nt
+    + 16 w + [0, 16) as its rows 0-15 and the up rows I + n as rows 16-31.
+    The entries of one (u, k-step, j) are ranked in position order; rank r goes
+    to word (u * nk + ks) * 64 + 16 j + r (lane 16 j + r stores it).  More than
+    16 positions in one register's 32 x 16 block of a wave (3 % local density)
+    raise ValueError."""
     E, R, C = (int(d) for d in shape)
     idx = idx.reshape(-1).to(torch.int64)
     e = torch.div(idx, R * C, rounding_mode="floor")
@@ -151,12 +155,12 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     c = rc - r * C
     if kind == "gate_up_fwd":
         n, k, K = r, c, C
-        cb = (n >= inter).to(torch.int64)
-        g = n - cb * inter
+        up = (n >= inter).to(torch.int64)
+        g = n - up * inter
         n_nt = (inter + 127) // 128
         nt = torch.div(g, 128, rounding_mode="floor")
-        w = torch.div(g % 128, 32, rounding_mode="floor")
-        l32 = g % 32
+        w = torch.div(g % 128, 16, rounding_mode="floor")
+        l32 = 16 * up + g % 16
     else:
         if kind == "down_fwd":
             n, k, N, K = r, c, R, C
@@ -166,8 +170,7 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
             raise ValueError(f"unknown overlay kind {kind!r}")
         n_nt = (N + 255) // 256
         nt = torch.div(n, 256, rounding_mode="floor")
-        w = torch.div(n % 256, 64, rounding_mode="floor")
-        cb = torch.div(n % 64, 32, rounding_mode="floor")
+        w = torch.div(n % 256, 32, rounding_mode="floor")
         l32 = n % 32
     if K % 128:
         raise ValueError(f"overlay: contraction length {K} is not a multiple of 128")
@@ -176,8 +179,8 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     kk = k % 64
     lane = l32 + 32 * torch.div(kk, 32, rounding_mode="floor")
     j = torch.div(kk % 32, 8, rounding_mode="floor")
-    off = (64 * cb + lane) * 16 + 4 * torch.div(kk % 8, 2, rounding_mode="floor") + 2 * (kk % 2)
-    group = ((e * n_nt + nt) * 4 + w) * nk + ks
+    off = lane * 16 + 4 * torch.div(kk % 8, 2, rounding_mode="floor") + 2 * (kk % 2)
+    group = ((e * n_nt + nt) * _OVL_WAVES + w) * nk + ks
     key = group * 4 + j
     order = torch.argsort(key, stable=True)
     sk = key[order]
@@ -186,18 +189,18 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     rank = torch.empty_like(rank_sorted)
     rank[order] = rank_sorted
     if rank.numel() and int(rank.max()) >= _OVL_CAP:
-        raise ValueError(f"overlay ({kind}): more than {_OVL_CAP} trained positions in one 64 x 16 weight block; "
+        raise ValueError(f"overlay ({kind}): more than {_OVL_CAP} trained positions in one 32 x 16 weight block; "
                          f"use dense expert weights with overlay_scatter for such masks")
-    word = group * 128 + 32 * j + rank
-    n_words = E * n_nt * 4 * nk * 128
+    word = group * _OVL_WORDS + 16 * j + rank
+    n_words = E * n_nt * _OVL_WAVES * nk * _OVL_WORDS
     return word.to(torch.int32), off.to(torch.int32), n_words
 
 
 def overlay_table(n_words: int, word: torch.Tensor, off: torch.Tensor) -> torch.Tensor:
     """Entry table with offsets set, values 0: unused words point into the dummy
-    area [2048, 4096) of the wave's epilogue tile, one 16-bit slot per word."""
+    area [1024, 2048) of the wave's epilogue tile, one 16-bit slot per word."""
     dev = word.device
-    table = 2048 + 2 * (torch.arange(n_words, dtype=torch.int32, device=dev) % 1024)
+    table = 1024 + 2 * (torch.arange(n_words, dtype=torch.int32, device=dev) % 512)
     table[word.long()] = off
     return table
 
