@@ -1708,9 +1708,22 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       //   d(gate) = DT(DT(da * u) * sig * (1 + g (1 - sig))),  da = DT(acc), sig = sigmoid(g)
       // into dgu[m, n] and dgu[m, I + n].  da goes through the LDS tile; the
       // math then runs on 16-byte row chunks (8 columns) next to coalesced gu
-      // loads and dgu stores, in a loop that is not unrolled (code size)
+      // loads and dgu stores, in a loop that is not unrolled (code size).  The
+      // units (row block i, half p) run in order, and the gu chunks of the next
+      // unit are loaded before the current unit's math, so that their latency
+      // hides behind it.
       const int64_t n0 = (int64_t)t.nt * Q_BN + wave * 32;
       if (n0 >= g.N) return;  // N % 32 == 0
+      const int ch = (lane & 3) * 8;
+      auto gu_row = [&](int u) -> const uint16_t* {  // this lane's gate chunk of unit u, or null
+        const int rr = 32 * (u >> 1) + (lane >> 2) + 16 * (u & 1);
+        return rr < t.valid ? g.aux + ((int64_t)t.m_beg + rr) * g.ld_aux + n0 + ch : nullptr;
+      };
+      u32x4 gn = {}, un = {};
+      if (const uint16_t* r0 = gu_row(0)) {
+        gn = *reinterpret_cast<const u32x4*>(r0);
+        un = *reinterpret_cast<const u32x4*>(r0 + g.inter);
+      }
 #pragma unroll
       for (int i = 0; i < NRB; ++i) {
         if (32 * i >= t.valid) break;
@@ -1718,16 +1731,20 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
         for (int q = 0; q < 4; ++q)
           stage4(8 * q + 4 * half, pack2<DT>(acc[i][4 * q], acc[i][4 * q + 1]),
                  pack2<DT>(acc[i][4 * q + 2], acc[i][4 * q + 3]));
-        const int rows_left = t.valid - 32 * i;
-        const int ch = (lane & 3) * 8;
 #pragma unroll 1
         for (int p = 0; p < 2; ++p) {
+          const int u = 2 * i + p;
+          const u32x4 gv = gn, uv = un;
+          if (u + 1 < 2 * NRB) {
+            if (const uint16_t* rn = gu_row(u + 1)) {
+              gn = *reinterpret_cast<const u32x4*>(rn);
+              un = *reinterpret_cast<const u32x4*>(rn + g.inter);
+            }
+          }
           const int rr = (lane >> 2) + 16 * p;
-          if (rr < rows_left) {
+          if (32 * i + rr < t.valid) {
             const int64_t m = t.m_beg + 32 * i + rr;
             const u32x4 dv = *reinterpret_cast<const u32x4*>(sEp + rr * Q_EPW + ch);
-            const u32x4 gv = *reinterpret_cast<const u32x4*>(g.aux + m * g.ld_aux + n0 + ch);
-            const u32x4 uv = *reinterpret_cast<const u32x4*>(g.aux + m * g.ld_aux + g.inter + n0 + ch);
             uint32_t dgw[4], duw[4];
 #pragma unroll
             for (int w2 = 0; w2 < 4; ++w2) {
