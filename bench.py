@@ -344,7 +344,8 @@ def moe_kernel_times(L, events: dict) -> dict:
     with torch.no_grad():
         logits = torch.nn.functional.linear(L["hs"], L["router_w"])
         w, _ = G.route_topk(logits, L["k"], False, torch.bfloat16, with_probs=False)
-        S = G.bucket_by_expert(w).n_slots  # the routing of the timed steps (static inputs, router step small)
+        bk = G.bucket_by_expert(w)  # the routing of the timed steps (static inputs, router step small)
+        S = bk.n_slots
     names = {"gate_up_fwd": "usaf_hip_moe_gate_up_fwd", "down_fwd": "usaf_hip_moe_down_fwd",
              "down_bwd": "usaf_hip_moe_down_bwd_t", "gate_up_bwd": "usaf_hip_moe_gate_up_bwd_t"}
     flops = {"gate_up_fwd": 2 * S * H * 2 * I, "down_fwd": 2 * S * I * H, "down_bwd": 2 * S * H * I,
@@ -358,6 +359,28 @@ def moe_kernel_times(L, events: dict) -> dict:
         out[key] = dict(ms=round(ms, 4), tflops=round(flops[key] / (ms * 1e-3) / 1e12, 1),
                         flop_per_launch=flops[key], launches=len(ev))
     out["slots"] = S
+    # the sampled weight gradient (two launches per step: gate_up, down).  Per
+    # active position: a row run and a column run of ld_e = round_up(S_e, 16)
+    # 16-bit operands (the expert's padded slot count), 2 S_e FLOP.  HBM bound
+    # by its distinct bytes: both blocked operands of each tensor once, the
+    # position lists (row code, column, compact index: 16 B) and the compact
+    # fp32 gradient read and written.
+    ev = events.get("usaf_hip_sddmm_blocked", [])
+    if ev:
+        n_steps = len(events["usaf_hip_moe_gate_up_fwd"])
+        ms_step = sum(a.elapsed_time(b) for a, b in ev) / n_steps
+        with torch.no_grad():
+            cnt = (bk.offsets[1:] - bk.offsets[:-1]).to(torch.int64)
+            ld_sum = int(((cnt + 15) // 16 * 16).sum())
+        pos = L["n_act"]["gate_up_proj"] + L["n_act"]["down_proj"]
+        operand_bytes = 2 * 2 * ld_sum * (L["n_act"]["gate_up_proj"] + L["n_act"]["down_proj"]) // E
+        distinct = 2 * ld_sum * ((2 * I + H) + (H + I)) + pos * (16 + 8)
+        gbs = distinct / (ms_step * 1e-3) / 1e9
+        out["sddmm"] = dict(ms_per_step=round(ms_step, 4), launches_per_step=len(ev) // n_steps, positions=pos,
+                            flop_per_step=2 * pos * S // E, operand_bytes_per_step=operand_bytes,
+                            operand_rate_gbs=round(operand_bytes / (ms_step * 1e-3) / 1e9, 1),
+                            roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                                          frac=round(gbs / HBM_PEAK_GBS, 4), algorithmic_bytes_per_step=distinct))
     return out
 
 
@@ -703,9 +726,14 @@ def main() -> int:
     _log(f"moe step: {mo['ms_per_step']:.3f} ms/step, {mo['tokens_per_s']:.0f} tokens/s, "
          f"{mo['tflops']:.1f} TFLOP/s algorithmic")
     for name, kv in mo["kernels"].items():
-        if isinstance(kv, dict):
+        if isinstance(kv, dict) and "tflops" in kv:
             _log(f"  {name}: {kv['ms']:.3f} ms, {kv['tflops']:.1f} TFLOP/s (average of {kv['launches']} launches "
                  f"inside the steps)")
+    sd = mo["kernels"].get("sddmm")
+    if sd:
+        _log(f"  sddmm: {sd['ms_per_step']:.3f} ms per step ({sd['launches_per_step']} launches, {sd['positions']:,} "
+             f"positions), {sd['roofline']['achieved']:.0f} GB/s of distinct bytes ({100 * sd['roofline']['frac']:.1f} % "
+             f"of HBM), operands delivered at {sd['operand_rate_gbs']:.0f} GB/s")
     _log("dequant: one Qwen3 MoE layer (603,979,776 elements) -> bf16")
     dq = bench_dequant(dev, args.steps, args.warmup)
     _log(f"dequant: {dq['ms_per_launch']:.3f} ms/launch, {dq['gbs']:.1f} GB/s")
@@ -731,7 +759,7 @@ def main() -> int:
         mx["cpu_baseline"] = cpu_baseline_mixtral()
         _log(f"cpu baseline mixtral: {mx['cpu_baseline']['value']} tokens/s")
 
-    kern = {n: v for n, v in mo["kernels"].items() if isinstance(v, dict)}
+    kern = {n: v for n, v in mo["kernels"].items() if isinstance(v, dict) and "tflops" in v}
     dom = max(kern, key=lambda n: kern[n]["ms"])
     dk = kern[dom]
     traffic = _load_traffic()

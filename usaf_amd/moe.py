@@ -455,13 +455,13 @@ def _capture(capture, which: str, dy: torch.Tensor, x: torch.Tensor, x_rows: Opt
 # the routed expert layer
 # ---------------------------------------------------------------------------
 
-# Optional per-launch timing of the fused GEMMs: None, or a dict that collects
-# entry-point name -> [(start, end) HIP events recorded on the launch stream].
-# bench.py sets it over its timed steps.
+# Optional per-launch timing of the fused GEMMs and the sampled gradient: None,
+# or a dict that collects entry-point name -> [(start, end) HIP events recorded
+# on the launch stream].  bench.py sets it over its timed steps.
 launch_events: Optional[dict] = None
 
 
-def _gemm_call(name, *args):
+def timed_call(name, *args):
     ev = launch_events
     if ev is None:
         N.call(name, *args)
@@ -512,12 +512,12 @@ class RoutedExpertsFn(torch.autograd.Function):
             act_blk = BlockedSlots(torch.empty(n_blk, dtype=dt, device=dev), I, b.offsets, b.blk_table)
         if S > 0:
             q, sz, w16 = ew._ptrs("gate_up", dt)
-            _gemm_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
+            timed_call("usaf_hip_moe_gate_up_fwd", hs.data_ptr(), T, H, b.token_idx.data_ptr(), b.offsets.data_ptr(),
                        S, E, I, q, sz, w16, code, gu.data_ptr(), act.data_ptr(),
                        None if act_blk is None else act_blk.data.data_ptr(),
                        None if act_blk is None else b.blk_table.data_ptr(), *ew._ovl("gate_up_fwd", dt), st)
             q, sz, w16 = ew._ptrs("down", dt)
-            _gemm_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
+            timed_call("usaf_hip_moe_down_fwd", act.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
                        code, y.data_ptr(), *ew._ovl("down_fwd", dt), st)
         out = combine(y, weights, b.pair_slot, dt)
         ctx.ew = ew
@@ -566,12 +566,12 @@ class RoutedExpertsFn(torch.autograd.Function):
         dgu = torch.empty(S, 2 * I, dtype=dt, device=dev)
         tq = ew._ptrs_t("down")
         if tq is not None:
-            _gemm_call("usaf_hip_moe_down_bwd_t", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
+            timed_call("usaf_hip_moe_down_bwd_t", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
                        *tq, code, dgu.data_ptr(), *ew._ovl("down_bwd", dt), st)
         else:
             _no_overlay(ew, "down")
             q, sz, w16 = ew._ptrs("down", dt)
-            _gemm_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
+            timed_call("usaf_hip_moe_down_bwd", dcur.data_ptr(), H, gu.data_ptr(), b.offsets.data_ptr(), S, E, I,
                        q, sz, w16, code, dgu.data_ptr(), st)
         if capture is not None:
             _capture(capture, "down_proj", dcur, act, None, b, (E, H, I), dt, dy_blocked=dcur_blk,
@@ -581,12 +581,12 @@ class RoutedExpertsFn(torch.autograd.Function):
         dx_slots = torch.empty(S, H, dtype=dt, device=dev)
         tq = ew._ptrs_t("gate_up")
         if tq is not None:
-            _gemm_call("usaf_hip_moe_gate_up_bwd_t", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *tq,
+            timed_call("usaf_hip_moe_gate_up_bwd_t", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, *tq,
                        code, dx_slots.data_ptr(), *ew._ovl("gate_up_bwd", dt), st)
         else:
             _no_overlay(ew, "gate_up")
             q, sz, w16 = ew._ptrs("gate_up", dt)
-            _gemm_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
+            timed_call("usaf_hip_moe_gate_up_bwd", dgu.data_ptr(), I, b.offsets.data_ptr(), S, E, H, q, sz, w16,
                        code, dx_slots.data_ptr(), st)
         if capture is not None:
             _capture(capture, "gate_up_proj", dgu, hs, b.token_idx, b, (E, 2 * I, H), dt)

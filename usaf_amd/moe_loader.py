@@ -23,7 +23,7 @@ import torch.nn as nn
 
 from . import _native as N
 from .importance import TopKImportanceStore  # noqa: F401  (moe_loader.py:584-631, GPU selection)
-from .moe import Q4Overlay, Q4Tensor
+from .moe import Q4Overlay, Q4Tensor, timed_call
 from .olmoe_streaming import _record_grad, apply_captured_expert_grads  # noqa: F401  (moe_loader.py:778-802)
 from .quantization import dequantize_4bit
 
@@ -438,9 +438,9 @@ class SparseGradStore:
             if rowT.offsets.data_ptr() != offsets.data_ptr() or colT.offsets.data_ptr() != offsets.data_ptr():
                 raise ValueError(f"{full_name}: blocked operands were built with other expert offsets")
             first = full_name in self._zero_pending
-            N.call("usaf_hip_sddmm_blocked", rowT.data.data_ptr(), colT.data.data_ptr(), rowT.table.data_ptr(), E, R, C,
-                   cols.numel(), row_code.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
-                   self._compact[full_name].data_ptr(), 0 if first else 1, N.stream_ptr(self.device))
+            timed_call("usaf_hip_sddmm_blocked", rowT.data.data_ptr(), colT.data.data_ptr(), rowT.table.data_ptr(), E,
+                       R, C, cols.numel(), row_code.data_ptr(), cols.data_ptr(), N.ptr(pos_map), N.dtype_code(dtype),
+                       self._compact[full_name].data_ptr(), 0 if first else 1, N.stream_ptr(self.device))
             self._zero_pending.discard(full_name)
             return
         if rowT.shape[0] != R or colT.shape[0] != C or rowT.shape[1] != colT.shape[1]:
