@@ -1748,19 +1748,15 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
             uint32_t dgw[4], duw[4];
 #pragma unroll
             for (int w2 = 0; w2 < 4; ++w2) {
+              // the two roundings to DT per element go through the pair
+              // conversion (round to nearest even, as round_to) and back
               const f32x2 da = unpack2<DT>(dv[w2]), gt = unpack2<DT>(gv[w2]), up = unpack2<DT>(uv[w2]);
-              float dg[2], du[2];
-#pragma unroll
-              for (int c = 0; c < 2; ++c) {
-                const float gx = c ? gt.y : gt.x, ux = c ? up.y : up.x, ax = c ? da.y : da.x;
-                const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * gx));
-                const float sg = round_to<DT>(gx * sig);
-                const float dsil = round_to<DT>(ax * ux);
-                dg[c] = (dsil * sig) * (1.0f + gx * (1.0f - sig));
-                du[c] = ax * sg;
-              }
-              dgw[w2] = pack2<DT>(dg[0], dg[1]);
-              duw[w2] = pack2<DT>(du[0], du[1]);
+              const float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * gt.x));
+              const float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * gt.y));
+              const f32x2 sg = unpack2<DT>(pack2<DT>(gt.x * s0, gt.y * s1));
+              const f32x2 dsil = unpack2<DT>(pack2<DT>(da.x * up.x, da.y * up.y));
+              dgw[w2] = pack2<DT>((dsil.x * s0) * (1.0f + gt.x * (1.0f - s0)), (dsil.y * s1) * (1.0f + gt.y * (1.0f - s1)));
+              duw[w2] = pack2<DT>(da.x * sg.x, da.y * sg.y);
             }
             *reinterpret_cast<u32x4*>(g.out + m * g.ldo + n0 + ch) = u32x4{dgw[0], dgw[1], dgw[2], dgw[3]};
             *reinterpret_cast<u32x4*>(g.out + m * g.ldo + g.inter + n0 + ch) = u32x4{duw[0], duw[1], duw[2], duw[3]};
