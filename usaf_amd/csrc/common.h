@@ -91,6 +91,26 @@ __device__ __forceinline__ float round_to(float v) {
   else return bf16_bits_to_f32(f32_to_bf16_bits(v));
 }
 
+// Conversions on pairs: fp32 -> two 16-bit values of DT (round to nearest
+// even, as round_to; one v_cvt_pk_bf16_f32 for bf16) packed low/high, and back.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (DT == USAF_BF16) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  } else {
+    const f16x2 h = {(f16)a, (f16)b};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+template <int DT>
+__device__ __forceinline__ f32x2 unpack2(uint32_t w) {
+  if constexpr (DT == USAF_BF16) return f32x2{__uint_as_float(w << 16), __uint_as_float(w & 0xFFFF0000u)};
+  else {
+    const f16x2 h = __builtin_bit_cast(f16x2, w);
+    return f32x2{(float)h.x, (float)h.y};
+  }
+}
 // ---- 64-slot x 64-feature transposes through LDS ---------------------------------
 // The tile is stored feature-major, 32 dwords (64 slots) per feature row; a dword
 // holds two consecutive slots.  Writer thread (sp, cg) = (tid >> 3, tid & 7) has

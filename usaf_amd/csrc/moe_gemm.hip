@@ -164,26 +164,6 @@ __device__ __forceinline__ float bits_to_f32(uint16_t b) {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
-// Epilogue conversions on pairs: fp32 -> two 16-bit values of DT (round to
-// nearest even, one v_cvt_pk_bf16_f32 for bf16) packed low/high, and back.
-template <int DT>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  if constexpr (DT == USAF_BF16) {
-    const f32x2 v = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-  } else {
-    const f16x2 h = {(f16)a, (f16)b};
-    return __builtin_bit_cast(uint32_t, h);
-  }
-}
-template <int DT>
-__device__ __forceinline__ f32x2 unpack2(uint32_t w) {
-  if constexpr (DT == USAF_BF16) return f32x2{__uint_as_float(w << 16), __uint_as_float(w & 0xFFFF0000u)};
-  else {
-    const f16x2 h = __builtin_bit_cast(f16x2, w);
-    return f32x2{(float)h.x, (float)h.y};
-  }
-}
 // silu(x) = x / (1 + e^-x) with the hardware exp2 and reciprocal (about 1 ulp
 // of fp32 each, far below the 16-bit rounding that follows)
 __device__ __forceinline__ float silu_fast(float x) {

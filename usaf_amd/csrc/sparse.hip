@@ -334,16 +334,10 @@ __global__ __launch_bounds__(256) void combine_bwd_blocked_kernel(
           uint32_t dw[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const uint16_t g2[2] = {(uint16_t)gw[q], (uint16_t)(gw[q] >> 16)};
-            const uint16_t y2[2] = {(uint16_t)yw[q], (uint16_t)(yw[q] >> 16)};
-            uint16_t d2[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const float g = load_as_f32<DT>(g2, h);
-              store_from_f32<DT>(d2, h, g * wv[u]);
-              acc[u] += g * load_as_f32<DT>(y2, h);
-            }
-            dw[q] = d2[0] | ((uint32_t)d2[1] << 16);
+            const f32x2 g = unpack2<DT>(gw[q]), yv = unpack2<DT>(yw[q]);
+            dw[q] = pack2<DT>(g.x * wv[u], g.y * wv[u]);
+            acc[u] += g.x * yv.x;
+            acc[u] += g.y * yv.y;
           }
           d[u] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
           *reinterpret_cast<uint4*>(dcur + srow[u] * H + c) = d[u];
