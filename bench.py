@@ -669,7 +669,8 @@ def probe_kernels(dev) -> None:
     torch.cuda.synchronize()
 
 
-KERNEL_SOURCES = ("usaf_amd/csrc/moe_gemm.hip", "usaf_amd/csrc/codec.hip", "usaf_amd/csrc/sparse.hip")
+KERNEL_SOURCES = ("usaf_amd/csrc/moe_gemm.hip", "usaf_amd/csrc/codec.hip", "usaf_amd/csrc/sparse.hip",
+                  "usaf_amd/csrc/common.h")
 
 
 def kernel_source_hash() -> str:
