@@ -1183,6 +1183,8 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t ld
 }
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+constexpr int Q_MTE_CAP = 1024;  // m-tiles covered by the m-tile -> expert table
+
 struct QTile {
   int e, valid, m_beg, nt;  // all wave-uniform
 };
@@ -1206,6 +1208,7 @@ template <int EPI, int DT, bool BT, bool OVL>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
   __shared__ __attribute__((aligned(16))) uint16_t q_ep[Q_WAVES * Q_EP_ELEMS];
+  __shared__ uint8_t q_mte[Q_MTE_CAP];  // expert of m-tile mt (when the list fits)
   int32_t* const s_h = reinterpret_cast<int32_t*>(qsm + Q_TAB_OFF);  // [Q_MAX_E + 1] heavy m-tile prefix
   int32_t* const s_l = s_h + Q_MAX_E + 1;                             // [Q_MAX_E + 1] light m-tile prefix
   int32_t* const s_off = s_l + Q_MAX_E + 1;                           // [Q_MAX_E + 1] expert offsets
@@ -1225,11 +1228,22 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // the tile counts come from LDS: readfirstlane tells the compiler they are
   // uniform, so that the stream state below lives in scalar registers
   const int n_heavy = uni(s_h[E]);
-  TileWalk walk(n_heavy + uni(s_l[E]), n_nt);
+  const int n_mt = n_heavy + uni(s_l[E]);
+  TileWalk walk(n_mt, n_nt);
   walk.set_heavy(n_heavy);
   const int n_grp = (int)(g.N / 128);  // BT: 128-column groups of n
   const int n_my = uni(walk.snake_count());
   if (n_my == 0) return;  // block-uniform
+  // m-tile -> expert as a table (one LDS read per tile instead of a binary
+  // search over the prefix tables, about seven dependent LDS reads), built
+  // once; longer lists keep the search
+  const bool mte = n_mt <= Q_MTE_CAP;
+  if (mte) {
+    for (int mt = tid; mt < n_mt; mt += Q_THREADS)
+      q_mte[mt] = (uint8_t)(mt < n_heavy ? prefix_owner(s_h, E, mt) : prefix_owner(s_l, E, mt - n_heavy));
+    lds_barrier();
+  }
+  const int nnt = (int)n_nt;  // n-tiles per m-tile (the unit arithmetic below is 32-bit)
 
   // tile ordinal -> expert, first slot, rows, n-tile (the m-tile list of
   // mtile_decode: every full-size tile before every light remainder; tables in LDS)
@@ -1238,14 +1252,15 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // which halves the write burst of the epilogues.
   const bool rev = (walk.local_b & 1) != 0;
   auto decode = [&](int ord) {
-    int64_t mt, nt;
-    walk.decode(walk.snake_unit(rev ? n_my - 1 - ord : ord), mt, nt);
+    const int u = (int)walk.snake_unit(rev ? n_my - 1 - ord : ord);
+    const int mi = u / nnt, nt = u - mi * nnt;
+    const int mt = walk.xcd + walk.dies * mi;  // TileWalk::decode in 32 bits
     int e, j;
     if (mt < n_heavy) {
-      e = prefix_owner(s_h, E, mt);
-      j = (int)mt - s_h[e];
+      e = mte ? (int)q_mte[mt] : prefix_owner(s_h, E, mt);
+      j = mt - s_h[e];
     } else {
-      e = prefix_owner(s_l, E, mt - n_heavy);
+      e = mte ? (int)q_mte[mt] : prefix_owner(s_l, E, mt - n_heavy);
       j = (s_off[e + 1] - s_off[e] + Q_BM - 1) / Q_BM - 1;
     }
     QTile t;
