@@ -516,6 +516,51 @@ __device__ __forceinline__ void mtile_prefix(const GemmArgs& g, int32_t* s_h, in
   lds_barrier();
 }
 
+// mtile_prefix from expert offsets already in LDS (s_off[0..E]), by one wave:
+// lane l takes experts 4l .. 4l + 3 (E <= 256) and the prefixes come from
+// shuffle scans, with no block barrier.  Called by the 64 lanes of one wave.
+template <int BMV>
+__device__ __forceinline__ void mtile_prefix_wave(const int32_t* s_off, int E, int32_t* s_h, int32_t* s_l, int lane) {
+  int h[4], l[4], hs = 0, ls = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int e = 4 * lane + k;
+    h[k] = l[k] = 0;
+    if (e < E) {
+      const int S = s_off[e + 1] - s_off[e];
+      const int c = (S + BMV - 1) / BMV;
+      l[k] = (c > 0 && S - (c - 1) * BMV < BMV / 2) ? 1 : 0;
+      h[k] = c - l[k];
+    }
+    hs += h[k];
+    ls += l[k];
+  }
+  int hi = hs, li = ls;  // inclusive scans over the lanes
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int ho = __shfl_up(hi, d, 64), lo = __shfl_up(li, d, 64);
+    if (lane >= d) {
+      hi += ho;
+      li += lo;
+    }
+  }
+  int hr = hi - hs, lr = li - ls;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int e = 4 * lane + k;
+    if (e < E) {
+      s_h[e] = hr;
+      s_l[e] = lr;
+    }
+    hr += h[k];
+    lr += l[k];
+  }
+  if (lane == 63) {
+    s_h[E] = hi;
+    s_l[E] = li;
+  }
+}
+
 // largest e with pre[e] <= x (pre non-decreasing, pre[0] = 0 <= x)
 __device__ __forceinline__ int prefix_owner(const int32_t* pre, int E, int64_t x) {
   int lo = 0, hi = E - 1;
@@ -551,23 +596,26 @@ __device__ __forceinline__ void mtile_decode(const GemmArgs& g, const int32_t* s
 // m-tile -- which read the same activation rows -- run together on one die
 // and share its L2, and every die gets the same mix of heavy and light tiles.
 struct TileWalk {
-  int64_t n_mt, n_nt;
+  // counts of blocks, tiles and units: 32-bit (a 64-bit division is a long
+  // emulated sequence; these run in every prologue and tile decode)
+  int n_mt, n_nt;
   int dies, xcd;
-  int64_t per_xcd, local_b, count;  // blocks on this die, this block's rank, m-tiles of this die
-  __device__ TileWalk(int64_t n_mt_, int64_t n_nt_) : n_mt(n_mt_), n_nt(n_nt_) {
-    const int64_t nblk = gridDim.x;
-    dies = nblk < kXcds ? (int)nblk : kXcds;
-    xcd = (int)(blockIdx.x % dies);
+  int per_xcd, local_b, count;  // blocks on this die, this block's rank, m-tiles of this die
+  __device__ TileWalk(int64_t n_mt_, int64_t n_nt_) : n_mt((int)n_mt_), n_nt((int)n_nt_) {
+    const int nblk = (int)gridDim.x;
+    dies = nblk < kXcds ? nblk : kXcds;
+    xcd = (int)(blockIdx.x % (unsigned)dies);
     per_xcd = (nblk + dies - 1 - xcd) / dies;
-    local_b = blockIdx.x / dies;
+    local_b = (int)(blockIdx.x / (unsigned)dies);
     count = n_mt > xcd ? (n_mt - xcd + dies - 1) / dies : 0;
   }
   __device__ int64_t first() const { return local_b; }
-  __device__ int64_t end() const { return count * n_nt; }
+  __device__ int64_t end() const { return (int64_t)count * n_nt; }
   __device__ int64_t step() const { return per_xcd; }
   __device__ void decode(int64_t u, int64_t& mt, int64_t& nt) const {
-    mt = xcd + (int64_t)dies * (u / n_nt);
-    nt = u % n_nt;
+    const int q = (int)u / n_nt;
+    mt = xcd + (int64_t)dies * q;
+    nt = (int)u - q * n_nt;
   }
   // Pass p hands units [p * per_xcd, (p + 1) * per_xcd) to the die's blocks,
   // upward (block b takes position b), as a plain round-robin does.  When the
@@ -576,20 +624,21 @@ struct TileWalk {
   // tiles before light remainders, so the blocks left one heavy tile short
   // take the light ones first, and a second round of light units starts again
   // from them instead of from the blocks that ran the extra heavy tile.
-  int64_t pass_turn = INT64_MAX;  // first pass that runs downward (set by set_heavy)
+  int pass_turn = INT32_MAX;  // first pass that runs downward (set by set_heavy)
   __device__ void set_heavy(int64_t n_heavy_mt) {
-    const int64_t hd = n_heavy_mt > xcd ? (n_heavy_mt - xcd + dies - 1) / dies : 0;
-    const int64_t uh = hd * n_nt;
-    pass_turn = uh % per_xcd == 0 ? INT64_MAX : uh / per_xcd + 1;
+    const int nh = (int)n_heavy_mt;
+    const int hd = nh > xcd ? (nh - xcd + dies - 1) / dies : 0;
+    const int uh = hd * n_nt;
+    pass_turn = uh % per_xcd == 0 ? INT32_MAX : uh / per_xcd + 1;
   }
   __device__ bool down(int64_t p) const { return p >= pass_turn && ((p - pass_turn) & 1) == 0; }
   __device__ int64_t snake_unit(int64_t p) const {
-    return p * per_xcd + (down(p) ? per_xcd - 1 - local_b : local_b);
+    return (int)p * per_xcd + (down(p) ? per_xcd - 1 - local_b : local_b);
   }
   __device__ int snake_count() const {
-    const int64_t tot = end(), full = tot / per_xcd, rem = tot % per_xcd;
-    const int64_t pos = down(full) ? per_xcd - 1 - local_b : local_b;
-    return (int)(full + (pos < rem ? 1 : 0));
+    const int tot = count * n_nt, full = tot / per_xcd, rem = tot % per_xcd;
+    const int pos = down(full) ? per_xcd - 1 - local_b : local_b;
+    return full + (pos < rem ? 1 : 0);
   }
 };
 
@@ -1218,12 +1267,10 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   const int wave = uni(tid >> 6);
   const int E = g.E;
   const int nk = (int)(g.K / BK);  // even and >= 2: K % 128 == 0
-  {
-    int32_t* const s_part = reinterpret_cast<int32_t*>(q_ep);  // scratch, before any epilogue
-    mtile_prefix<Q_THREADS, Q_BM>(g, s_h, s_l, s_part, tid);
-    for (int e = tid; e <= E; e += Q_THREADS) s_off[e] = g.offsets[e];
-    lds_barrier();
-  }
+  for (int e = tid; e <= E; e += Q_THREADS) s_off[e] = g.offsets[e];  // one global read of the offsets
+  lds_barrier();
+  if (wave == 0) mtile_prefix_wave<Q_BM>(s_off, E, s_h, s_l, lane);
+  lds_barrier();
   const int64_t n_nt = (EPI == EPI_SWIGLU_FWD) ? (g.inter + 127) / 128 : (g.N + Q_BN - 1) / Q_BN;
   // the tile counts come from LDS: readfirstlane tells the compiler they are
   // uniform, so that the stream state below lives in scalar registers
