@@ -1285,9 +1285,11 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // search over the prefix tables, about seven dependent LDS reads), built
   // once; longer lists keep the search
   const bool mte = n_mt <= Q_MTE_CAP;
-  if (mte) {
-    for (int mt = tid; mt < n_mt; mt += Q_THREADS)
-      q_mte[mt] = (uint8_t)(mt < n_heavy ? prefix_owner(s_h, E, mt) : prefix_owner(s_l, E, mt - n_heavy));
+  if (mte) {  // expert e owns heavy m-tiles [s_h[e], s_h[e + 1]) and at most one light one
+    for (int e = tid; e < E; e += Q_THREADS) {
+      for (int mt = s_h[e]; mt < s_h[e + 1]; ++mt) q_mte[mt] = (uint8_t)e;
+      if (s_l[e + 1] > s_l[e]) q_mte[n_heavy + s_l[e]] = (uint8_t)e;
+    }
     lds_barrier();
   }
   const int nnt = (int)n_nt;  // n-tiles per m-tile (the unit arithmetic below is 32-bit)
