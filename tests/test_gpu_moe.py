@@ -573,6 +573,40 @@ def test_backward_transposed_vs_direct(gpu_device, E, H, I, T, k):
 
 # ---- per-expert blocked operands for the sampled gradient ---------------------------
 
+def test_q4_gemm_long_mtile_list(gpu_device):
+    """More m-tiles than the fused kernel's m-tile -> expert table holds (1,024):
+    the kernel then searches the prefix tables per tile.  down_fwd on synthetic
+    slot offsets (≈ 1,150 m-tiles, ragged experts) against an fp32 product of
+    the dequantized weights on the GPU (bf16 output: rel <= 1e-2)."""
+    _say("q4 down_fwd with > 1024 m-tiles (prefix-search path)")
+    from usaf_amd import _native as N
+    dev, dt = gpu_device, torch.bfloat16
+    E, H, I = 16, 128, 128
+    g = torch.Generator().manual_seed(21)
+    counts = (torch.randint(15000, 21000, (E,), generator=g) + torch.arange(E) * 7).tolist()
+    counts[3] = 0  # an empty expert in the list
+    S = sum(counts)
+    n_mt = sum((c + 255) // 256 for c in counts)
+    assert n_mt > 1024
+    offsets = torch.tensor([0] + list(torch.tensor(counts).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+    qd = G.Q4Tensor.quantize((torch.randn(E, H, I, generator=g) * 0.05).half().to(dev))
+    ew = G.ExpertWeights(G.Q4Tensor.quantize((torch.randn(E, 2 * I, H, generator=g) * 0.05).half().to(dev)), qd)
+    act = torch.randn(S, I, generator=g).to(dt).to(dev)
+    y = torch.empty(S, H, dtype=dt, device=dev)
+    q, sz, w16 = ew._ptrs("down", dt)
+    N.call("usaf_hip_moe_down_fwd", act.data_ptr(), I, offsets.data_ptr(), S, E, H, q, sz, w16, N.BF16, y.data_ptr(),
+           None, 0, N.stream_ptr(dev))
+    wd = qd.dequantize(torch.float16).to(dt).float()  # the GEMM's weight: DT(fp16 dequant)
+    ref = torch.empty(S, H, dtype=torch.float32, device=dev)
+    offs = offsets.tolist()
+    for e in range(E):
+        s0, s1 = offs[e], offs[e + 1]
+        if s1 > s0:
+            ref[s0:s1] = act[s0:s1].float() @ wd[e].t()
+    torch.cuda.synchronize()
+    assert rel_err(y, ref) <= 1e-2
+
+
 @pytest.mark.parametrize("gathered", [False, True])
 def test_gather_transpose_blocked_bit_exact(gpu_device, gathered):
     _say(f"gather_transpose_blocked gathered={gathered}")
