@@ -1735,11 +1735,16 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
           const int f = lane >> 2, sg = lane & 3;
           const int j = jt + 32 * i + 8 * sg;
           if (j < ld) {
-            uint32_t w[4];
+            // all eight staged values are read (rows 8 sg .. 8 sg + 7 of the
+            // 32-row tile: in bounds), back to back under one wait; the slots
+            // past se become zero by selects, not by skipped reads
+            uint32_t v[8], w[4];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = sEp[(8 * sg + k) * Q_EPW + 32 + f];
 #pragma unroll
             for (int k2 = 0; k2 < 4; ++k2) {
-              const uint32_t lo = j + 2 * k2 < se ? sEp[(8 * sg + 2 * k2) * Q_EPW + 32 + f] : 0u;
-              const uint32_t hi = j + 2 * k2 + 1 < se ? sEp[(8 * sg + 2 * k2 + 1) * Q_EPW + 32 + f] : 0u;
+              const uint32_t lo = j + 2 * k2 < se ? v[2 * k2] : 0u;
+              const uint32_t hi = j + 2 * k2 + 1 < se ? v[2 * k2 + 1] : 0u;
               w[k2] = lo | (hi << 16);
             }
             *reinterpret_cast<u32x4*>(tblk + f * (int64_t)ld + j) = u32x4{w[0], w[1], w[2], w[3]};
