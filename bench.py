@@ -197,13 +197,11 @@ def _fwd_bwd_check(L, finite, overflow, slot: int = 0) -> dict:
                       overflow=overflow)
     out.backward(L["dy"])
     dev = L["hs"].device
-    cg = {}
-    for name, v in store.compact.items():
-        o = L.setdefault(f"cg{slot}:{name}", torch.empty_like(v))
-        N.call("usaf_hip_scale_check", v.data_ptr(), o.data_ptr(), v.numel(), 1.0, finite.data_ptr(),
-               N.stream_ptr(dev))
-        cg[name] = o
-    return cg
+    flat = store.flat  # every compact gradient, one buffer: one check-and-copy launch
+    o = L.setdefault(f"cg{slot}", torch.empty_like(flat))
+    N.call("usaf_hip_scale_check", flat.data_ptr(), o.data_ptr(), flat.numel(), 1.0, finite.data_ptr(),
+           N.stream_ptr(dev))
+    return {name: o[start:start + n] for name, (start, n) in store.spans.items()}
 
 
 def moe_train_step_sync(L) -> bool:
@@ -245,8 +243,13 @@ class LaggedSteps:
     def __init__(self, L):
         dev = L["hs"].device
         self.L = L
-        self.flags = [torch.ones(2, dtype=torch.int32, device=dev) for _ in range(2)]  # finite, halt snapshot
-        self.halt = torch.zeros(1, dtype=torch.int32, device=dev)
+        # [finite of slot 0, halt, finite of slot 1]: each slot's finite flag sits
+        # next to the sticky halt flag, so one 8-byte copy to the host reads both
+        # in stream order (no device-side snapshot of halt)
+        self.flagbuf = torch.tensor([1, 0, 1], dtype=torch.int32, device=dev)
+        self.halt = self.flagbuf[1:2]
+        self.finite = [self.flagbuf[0:1], self.flagbuf[2:3]]
+        self.pair = [self.flagbuf[0:2], self.flagbuf[1:3]]  # slot 0: (finite, halt); slot 1: (halt, finite)
         self.host = [torch.zeros(2, dtype=torch.int32).pin_memory() for _ in range(2)]
         self.events = [torch.cuda.Event() for _ in range(2)]
         self.cg = [None, None]
@@ -255,25 +258,25 @@ class LaggedSteps:
         self.applied = self.skipped = self.recomputed = 0
 
     def _launch(self, i: int) -> None:
-        f = self.flags[i]
-        self.cg[i] = _fwd_bwd_check(self.L, f[:1], self.halt, slot=i)
-        f[1:].copy_(self.halt)
-        self.host[i].copy_(f, non_blocking=True)
+        f = self.finite[i]
+        self.cg[i] = _fwd_bwd_check(self.L, f, self.halt, slot=i)
+        self.host[i].copy_(self.pair[i], non_blocking=True)
         self.events[i].record()
-        self.L["sgd"].step(finite=f[:1], halt=self.halt)
-        self.L["opt"].step(compact_grads=self.cg[i], finite=f[:1], halt=self.halt)
+        self.L["sgd"].step(finite=f, halt=self.halt)
+        self.L["opt"].step(compact_grads=self.cg[i], finite=f, halt=self.halt)
         sync_overlays(self.L)
 
     def _resolve(self, j: int, relaunch=None) -> None:
         self.events[j].synchronize()
-        finite, halted = self.host[j].tolist()
+        a, b = self.host[j].tolist()
+        finite, halted = (a, b) if j == 0 else (b, a)
         if halted:
             # step j overflowed its static slots: no gated update ran since
             torch.cuda.synchronize()
             self.halt.zero_()
             self.recomputed += 1
-            f = self.flags[j]
-            self.cg[j] = _fwd_bwd_check(self.L, f[:1], None, slot=j)
+            f = self.finite[j]
+            self.cg[j] = _fwd_bwd_check(self.L, f, None, slot=j)
             finite = f.tolist()[0]
             if finite:
                 self.L["sgd"].step()

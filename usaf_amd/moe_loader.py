@@ -375,10 +375,19 @@ class SparseGradStore:
         self._zero_pending: set = set()
         self._csr: Dict[str, tuple] = {}
         self._maps: Dict[str, Dict[int, Tuple[torch.Tensor, torch.Tensor]]] = {}
+        # the compact gradients are consecutive slices of one buffer (``flat``), so
+        # that a whole-store pass (finite check, copy) is one launch
+        self.spans: Dict[str, Tuple[int, int]] = {}
+        total = 0
+        for name, idx in active_idx.items():
+            self.spans[name] = (total, int(idx.numel()))
+            total += int(idx.numel())
+        self._flat = torch.zeros(total, dtype=torch.float32, device=dev)
         for name, idx in active_idx.items():
             idx = idx.reshape(-1).to(device=dev, dtype=torch.long)
             shape = [int(s) for s in shapes[name]]
-            self._compact[name] = torch.zeros(idx.numel(), dtype=torch.float32, device=dev)
+            start, n = self.spans[name]
+            self._compact[name] = self._flat[start:start + n]
             if len(shape) < 2:
                 raise ValueError(f"{name}: expert tensors are [E, rows, ...], got shape {shape}")
             E, R = shape[0], shape[1]
@@ -409,6 +418,14 @@ class SparseGradStore:
         for name in list(self._zero_pending):
             self._materialize(name)
         return self._compact
+
+    @property
+    def flat(self) -> torch.Tensor:
+        """All compact gradients as one fp32 buffer: ``compact[name]`` is
+        ``flat[start:start + n]`` with ``(start, n) = spans[name]``."""
+        for name in list(self._zero_pending):
+            self._materialize(name)
+        return self._flat
 
     def _materialize(self, name: str) -> None:
         if name in self._zero_pending:
