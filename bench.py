@@ -144,15 +144,23 @@ def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfl
         del w
     experts = G.ExpertWeights(q["gate_up_proj"], q["down_proj"])
     prefix = "model.layers.0.mlp.experts"
-    active, masters, shapes = {}, {}, {}
+    active, masters, shapes, init = {}, {}, {}, {}
     for name, qt in q.items():
         numel = qt.numel()
         idx = torch.randperm(numel, device=dev, generator=gen)[: int(0.005 * numel)].sort().values
         full = f"{prefix}.{name}"
         active[full] = idx
         shapes[full] = tuple(qt.shape)
-        masters[full] = torch.nn.Parameter(qt.dequantize(torch.float16).reshape(-1)[idx].float(),
-                                           requires_grad=False)
+        init[full] = qt.dequantize(torch.float16).reshape(-1)[idx].float()
+    # the masters are consecutive slices of one buffer, in the order of the store's
+    # compact gradients and the optimizer's moments: SparseAdam updates both
+    # tensors with one launch
+    flat = torch.cat(list(init.values()))
+    start = 0
+    for full, v in init.items():
+        masters[full] = torch.nn.Parameter(flat[start:start + v.numel()], requires_grad=False)
+        start += v.numel()
+    del init
     store = SparseGradStore(active, shapes, device=dev)
     opt = SparseAdam(masters, active_idx=active, lr=2e-4, weight_decay=0.005, compact_params=True)
     # the masters are what the next forward multiplies: the reference scatters them into

@@ -11,6 +11,7 @@ import torch
 
 from oracle import moe as M
 from oracle.codec_torch import dequant_opseq
+from usaf_amd import _native as N
 from usaf_amd import moe as G
 from usaf_amd.moe_loader import SparseGradStore, overlay_scatter
 from usaf_amd.sparse_optim import SparseAdam
@@ -413,6 +414,66 @@ def test_sparse_adam_device_gate(gpu_device):
     A.step(compact_grads={"w": grads[0]})
     torch.cuda.synchronize()
     assert B.step_count == 4 and torch.equal(dev_p, host)
+
+
+def test_sparse_adam_one_launch_for_adjacent_tensors(gpu_device):
+    """Masters and gradients laid out as consecutive slices of one buffer (the
+    bench's layout): the step updates them in one launch, bit-equal to separate
+    tensors updated one by one, gated and ungated; a layout that breaks the
+    adjacency falls back to one launch per tensor with the same result."""
+    _say("SparseAdam over adjacent tensors: one launch, bit-equal to per-tensor launches")
+    sizes = {"a": 70_001, "b": 30_011}
+    g = torch.Generator().manual_seed(12)
+    p0 = {n: torch.randn(k, generator=g) * 0.02 for n, k in sizes.items()}
+    grads = [{n: torch.randn(k, generator=g) * 1e-3 for n, k in sizes.items()} for _ in range(3)]
+    kw = dict(lr=2e-4, weight_decay=0.005, compact_params=True)
+    idx = {n: torch.arange(k) for n, k in sizes.items()}
+    flat_p = torch.cat([p0["a"], p0["b"]]).to(gpu_device)
+    fused = {"a": torch.nn.Parameter(flat_p[:sizes["a"]], requires_grad=False),
+             "b": torch.nn.Parameter(flat_p[sizes["a"]:], requires_grad=False)}
+    single = {n: torch.nn.Parameter(p0[n].clone().to(gpu_device), requires_grad=False) for n in sizes}
+    A = SparseAdam(fused, active_idx=idx, **kw)
+    B = SparseAdam(single, active_idx=idx, **kw)
+    assert A._m["b"].data_ptr() == A._m["a"].data_ptr() + 4 * sizes["a"]
+    calls = []
+    real_call = N.call
+
+    def counting_call(fn, *args):
+        calls.append(fn)
+        return real_call(fn, *args)
+
+    one = torch.ones(1, dtype=torch.int32, device=gpu_device)
+    zero = torch.zeros(1, dtype=torch.int32, device=gpu_device)
+    for step, gr in enumerate(grads):
+        flat_g = torch.cat([gr["a"], gr["b"]]).to(gpu_device)
+        ga = {"a": flat_g[:sizes["a"]], "b": flat_g[sizes["a"]:]}
+        gb = {n: gr[n].to(gpu_device) for n in sizes}
+        gate = {} if step == 0 else {"finite": one, "halt": zero}
+        calls.clear()
+        N.call = counting_call
+        try:
+            A.step(compact_grads=ga, **gate)
+        finally:
+            N.call = real_call
+        assert sum(c.startswith("usaf_hip_sparse_adam_step") for c in calls) == 1
+        B.step(compact_grads=gb, **gate)
+    torch.cuda.synchronize()
+    for n in sizes:
+        assert torch.equal(fused[n], single[n]), n
+        assert torch.equal(A._m[n], B._m[n]) and torch.equal(A._v[n], B._v[n]), n
+    # gradients in separate buffers: one launch per tensor, same update
+    gsep = {n: grads[0][n].to(gpu_device) for n in sizes}
+    calls.clear()
+    N.call = counting_call
+    try:
+        A.step(compact_grads=gsep, finite=one, halt=zero)
+    finally:
+        N.call = real_call
+    B.step(compact_grads=gsep, finite=one, halt=zero)
+    torch.cuda.synchronize()
+    assert sum(c.startswith("usaf_hip_sparse_adam_step") for c in calls) == 2
+    for n in sizes:
+        assert torch.equal(fused[n], single[n]), n
 
 
 def test_sparse_adam_full_params(gpu_device):

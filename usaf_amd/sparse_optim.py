@@ -65,6 +65,21 @@ class SparseAdam:
         self._m[name] = torch.zeros(idx.numel(), device=dev, dtype=torch.float32)
         self._v[name] = torch.zeros(idx.numel(), device=dev, dtype=torch.float32)
 
+    def _pack_moments(self) -> None:
+        """m and v of all active tensors as consecutive slices of one buffer each
+        (when they share a device), so that a step over masters and gradients laid
+        out the same way is one launch."""
+        names = self._active_ids
+        if len(names) < 2 or len({self._m[n].device for n in names}) != 1:
+            return
+        for state in (self._m, self._v):
+            flat = torch.cat([state[n] for n in names])
+            start = 0
+            for n in names:
+                k = state[n].numel()
+                state[n] = flat[start:start + k]
+                start += k
+
     def _build_state_from_idx(self, active_idx: dict[str, torch.Tensor]):
         """sparse_optim.py:43-53."""
         self._active_ids, self._idx, self._m, self._v = [], {}, {}, {}
@@ -72,6 +87,7 @@ class SparseAdam:
             if name not in self._named or idx is None or idx.numel() == 0:
                 continue
             self._init_slot(name, idx.reshape(-1).to(dtype=torch.long))
+        self._pack_moments()
 
     def _build_state(self, active_mask: dict[str, torch.Tensor]):
         """sparse_optim.py:55-68."""
@@ -84,6 +100,7 @@ class SparseAdam:
             if idx.numel() == 0:
                 continue
             self._init_slot(name, idx)
+        self._pack_moments()
 
     def zero_grad(self, set_to_none: bool = False):
         for name in self._active_ids:
@@ -136,6 +153,7 @@ class SparseAdam:
         if not gated:
             self._step += 1
         beta1, beta2 = self.betas
+        jobs = []  # (name, target, grad) per active tensor with a gradient
         for name in self._active_ids:
             param = self._named[name]
             if compact_grads is None and param.grad is None:
@@ -159,24 +177,47 @@ class SparseAdam:
             if grad.numel() != target.numel():
                 raise ValueError(f"SparseAdam: gradient for {name} has {grad.numel()} entries, expected "
                                  f"{target.numel()}")
+            jobs.append((name, target, grad))
+        # the update is elementwise with one set of hyperparameters: tensors whose
+        # masters, gradients, m and v are each consecutive slices of one buffer
+        # (in the same order) take one launch over the whole span
+        runs = []
+        for job in jobs:
+            if runs and self.compact_params and self._follows(runs[-1][-1], job):
+                runs[-1].append(job)
+            else:
+                runs.append([job])
+        for run in runs:
+            name, target, grad = run[0]
+            dev = target.device
+            n = sum(t.numel() for _, t, _ in run)
             if gated:
                 self._gate_state(dev)
                 N.call("usaf_hip_sparse_adam_step_gated", target.data_ptr(), grad.data_ptr(),
-                       self._m[name].data_ptr(), self._v[name].data_ptr(), target.numel(), float(self.lr),
+                       self._m[name].data_ptr(), self._v[name].data_ptr(), n, float(self.lr),
                        float(beta1), float(beta2), float(self.eps), float(self.weight_decay), N.ptr(finite),
                        N.ptr(halt), self._count.data_ptr(), self._bias.data_ptr(), self._bias.numel() // 2,
                        self.bad.data_ptr(), N.stream_ptr(dev))
             else:
                 N.call("usaf_hip_sparse_adam_step", target.data_ptr(), grad.data_ptr(), self._m[name].data_ptr(),
-                       self._v[name].data_ptr(), target.numel(), float(self.lr), float(beta1), float(beta2),
+                       self._v[name].data_ptr(), n, float(self.lr), float(beta1), float(beta2),
                        float(self.eps), float(self.weight_decay), self._step, N.stream_ptr(dev))
             if not self.compact_params:
+                param = self._named[name]
                 flat = param.data.reshape(-1)
                 flat.scatter_(0, self._idx[name], target.to(param.dtype))
         if gated and self._count is not None:
             N.call("usaf_hip_count_step", N.ptr(finite), N.ptr(halt), self._count.data_ptr(),
                    N.stream_ptr(self._count.device))
             self._launched += 1
+
+    def _follows(self, prev, job) -> bool:
+        """Whether job's master, gradient, m and v start right where prev's end."""
+        (pn, pt, pg), (n, t, g) = prev, job
+        k = 4 * pt.numel()
+        return (t.device == pt.device and t.data_ptr() == pt.data_ptr() + k and g.data_ptr() == pg.data_ptr() + k
+                and self._m[n].data_ptr() == self._m[pn].data_ptr() + k
+                and self._v[n].data_ptr() == self._v[pn].data_ptr() + k)
 
     def refresh(self, model):
         """Re-bind current model Parameters by name (sparse_optim.py:136-150)."""
