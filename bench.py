@@ -186,7 +186,7 @@ def sync_overlays(L) -> None:
         ov.refresh(L["masters"][name].data)
 
 
-def _fwd_bwd_check(L, finite, overflow, slot: int = 0) -> dict:
+def _fwd_bwd_check(L, finite, overflow, slot: int = 0, reset: bool = True) -> dict:
     """Forward + backward with grad capture, then the reference's finite check
     (train.py:649-651) into finite[0].  overflow None buckets the experts
     exactly (one host read of the slot count); otherwise they go into
@@ -200,7 +200,8 @@ def _fwd_bwd_check(L, finite, overflow, slot: int = 0) -> dict:
     store.zero_()
     L["hs"].grad = None
     L["router_w"].grad = None
-    finite.fill_(1)
+    if reset:  # the check only ever clears the flag: a flag known to be 1 needs no reset
+        finite.fill_(1)
     out = G.moe_block(L["hs"], L["router_w"], L["k"], False, L["experts"], capture=(store, L["prefix"]),
                       overflow=overflow)
     out.backward(L["dy"])
@@ -261,13 +262,17 @@ class LaggedSteps:
         self.host = [torch.zeros(2, dtype=torch.int32).pin_memory() for _ in range(2)]
         self.events = [torch.cuda.Event() for _ in range(2)]
         self.cg = [None, None]
+        # each slot's finite flag as last read on the host (None: launched since, not read):
+        # a slot is read before it is launched again, and only a 0 or an unread flag needs a reset
+        self.known = [1, 1]
         self.pending = None
         self.slot = 0
         self.applied = self.skipped = self.recomputed = 0
 
     def _launch(self, i: int) -> None:
         f = self.finite[i]
-        self.cg[i] = _fwd_bwd_check(self.L, f, self.halt, slot=i)
+        self.cg[i] = _fwd_bwd_check(self.L, f, self.halt, slot=i, reset=self.known[i] != 1)
+        self.known[i] = None
         self.host[i].copy_(self.pair[i], non_blocking=True)
         self.events[i].record()
         self.L["sgd"].step(finite=f, halt=self.halt)
@@ -278,14 +283,16 @@ class LaggedSteps:
         self.events[j].synchronize()
         a, b = self.host[j].tolist()
         finite, halted = (a, b) if j == 0 else (b, a)
+        self.known[j] = finite
         if halted:
             # step j overflowed its static slots: no gated update ran since
             torch.cuda.synchronize()
             self.halt.zero_()
             self.recomputed += 1
             f = self.finite[j]
-            self.cg[j] = _fwd_bwd_check(self.L, f, None, slot=j)
+            self.cg[j] = _fwd_bwd_check(self.L, f, None, slot=j, reset=self.known[j] != 1)
             finite = f.tolist()[0]
+            self.known[j] = finite
             if finite:
                 self.L["sgd"].step()
                 self.L["opt"].step(compact_grads=self.cg[j])
