@@ -132,10 +132,15 @@ def moe_step_flops(T, H, I, E, k, n_active_gu, n_active_dn):
     return dict(fwd=fwd, dx=dx, sddmm=sddmm, router=router, total=fwd + dx + sddmm + router)
 
 
-def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfloat16):
+LOSS_SCALE_INIT, SCALE_UP_EVERY = 4096.0, 200  # train.py:31
+LOSS_SCALE_MIN, LOSS_SCALE_MAX = 64.0, 65536.0   # train.py:674, 676
+
+
+def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfloat16,
+              scale_up_every=SCALE_UP_EVERY):
     from usaf_amd import moe as G
     from usaf_amd.moe_loader import SparseGradStore
-    from usaf_amd.sparse_optim import MomentumSGD, SparseAdam
+    from usaf_amd.sparse_optim import DeviceLossScale, MomentumSGD, SparseAdam
     gen = torch.Generator(device=dev).manual_seed(seed)
     q = {}
     for name, shp in (("gate_up_proj", (E, 2 * I, H)), ("down_proj", (E, H, I))):
@@ -175,8 +180,13 @@ def build_moe(dev, T=4096, H=2048, I=768, E=128, k=8, seed=1234, dtype=torch.bfl
     sgd = MomentumSGD([router_w], lr=2e-4, momentum=0.9, weight_decay=0.005)
     dy = torch.randn(T, H, device=dev, generator=gen).to(dtype)
     n_act = {n.rsplit(".", 1)[1]: int(i.numel()) for n, i in active.items()}
+    # the trainer's dynamic loss scale (train.py:31, 351-353, 661-677): on the device
+    # for the lagged loop, as the reference's host variables for the synchronous one
+    scaler = DeviceLossScale(LOSS_SCALE_INIT, scale_up_every, LOSS_SCALE_MIN, LOSS_SCALE_MAX, accum=1, device=dev)
+    host_scale = dict(loss_scale=LOSS_SCALE_INIT, good_streak=0, n_skipped=0, every=scale_up_every, accum=1)
     return dict(experts=experts, store=store, opt=opt, hs=hs, router_w=router_w, sgd=sgd, dy=dy, k=k,
-                prefix=prefix, T=T, H=H, I=I, E=E, n_act=n_act, active=active, masters=masters, overlays=overlays)
+                prefix=prefix, T=T, H=H, I=I, E=E, n_act=n_act, active=active, masters=masters, overlays=overlays,
+                scaler=scaler, host_scale=host_scale)
 
 
 def sync_overlays(L) -> None:
@@ -186,14 +196,16 @@ def sync_overlays(L) -> None:
         ov.refresh(L["masters"][name].data)
 
 
-def _fwd_bwd_check(L, finite, overflow, slot: int = 0, reset: bool = True) -> dict:
-    """Forward + backward with grad capture, then the reference's finite check
-    (train.py:649-651) into finite[0].  overflow None buckets the experts
-    exactly (one host read of the slot count); otherwise they go into
-    T * (top_k + 1) static slots without a host read and the int32 GPU flag
-    overflow[0] is set to 1 if that overflowed (it is never cleared here).
-    The compact gradients go to the buffers of `slot` (two slots, so that a
-    step's gradients survive the next step's check until its update reads them)."""
+def _fwd_bwd_check(L, finite, overflow, slot: int = 0, reset: bool = True, host_scale: bool = False) -> dict:
+    """Forward + backward with grad capture on the loss-scaled gradient, then the
+    reference's unscale and finite check (train.py:351-353, 649-663) into
+    finite[0].  overflow None buckets the experts exactly (one host read of the
+    slot count); otherwise they go into T * (top_k + 1) static slots without a
+    host read and the int32 GPU flag overflow[0] is set to 1 if that
+    overflowed (it is never cleared here).  The compact gradients go to the
+    buffers of `slot` (two slots, so that a step's gradients survive the next
+    step's check until its update reads them).  host_scale: the loss scale is
+    the reference's host float (L["host_scale"]) instead of the device state."""
     from usaf_amd import _native as N
     from usaf_amd import moe as G
     store = L["store"]
@@ -204,33 +216,53 @@ def _fwd_bwd_check(L, finite, overflow, slot: int = 0, reset: bool = True) -> di
         finite.fill_(1)
     out = G.moe_block(L["hs"], L["router_w"], L["k"], False, L["experts"], capture=(store, L["prefix"]),
                       overflow=overflow)
-    out.backward(L["dy"])
+    hsc = L["host_scale"]
+    if host_scale:
+        dy = L["dy"] * hsc["loss_scale"]  # the gradient of loss * loss_scale (train.py:351-353)
+    else:
+        dy = L["scaler"].scale_grad(L["dy"], out=L.setdefault("dy_scaled", torch.empty_like(L["dy"])))
+    out.backward(dy)
+    if L.get("keep_out"):  # parity tests read the step's output
+        L["out"] = out.detach()
     dev = L["hs"].device
     flat = store.flat  # every compact gradient, one buffer: one check-and-copy launch
     o = L.setdefault(f"cg{slot}", torch.empty_like(flat))
-    N.call("usaf_hip_scale_check", flat.data_ptr(), o.data_ptr(), flat.numel(), 1.0, finite.data_ptr(),
-           N.stream_ptr(dev))
+    if host_scale:
+        N.call("usaf_hip_scale_check", flat.data_ptr(), o.data_ptr(), flat.numel(),
+               hsc["loss_scale"] * hsc["accum"], finite.data_ptr(), N.stream_ptr(dev))
+    else:
+        L["scaler"].unscale_check(flat, o, finite)
     return {name: o[start:start + n] for name, (start, n) in store.spans.items()}
 
 
 def moe_train_step_sync(L) -> bool:
-    """One step in the reference loop's order (train.py:649-672): the host reads
-    the finite flag, then applies the router's SGD step and SparseAdam if it is
-    set.  The slot count stays on the GPU unless the routing overflowed
-    T * (top_k + 1) slots; the step is then recomputed with exact bucketing."""
+    """One step in the reference loop's order (train.py:649-677): the host reads
+    the finite flag, then applies SparseAdam and the router's SGD step (on the
+    gradient divided by loss_scale * ACCUM) if it is set, and moves the loss
+    scale by the reference's host schedule.  The slot count stays on the GPU
+    unless the routing overflowed T * (top_k + 1) slots; the step is then
+    recomputed with exact bucketing."""
     dev = L["hs"].device
+    hsc = L["host_scale"]
     flag = L.setdefault("flag_sync", torch.ones(2, dtype=torch.int32, device=dev))
     flag[1:].fill_(0)
-    cg = _fwd_bwd_check(L, flag[:1], flag[1:])
+    cg = _fwd_bwd_check(L, flag[:1], flag[1:], host_scale=True)
     finite, overflow = flag.tolist()
     if overflow:
         L["recomputed"] = L.get("recomputed", 0) + 1
-        cg = _fwd_bwd_check(L, flag[:1], None)
+        cg = _fwd_bwd_check(L, flag[:1], None, host_scale=True)
         finite = flag.tolist()[0]
     if finite:
-        L["sgd"].step()
         L["opt"].step(compact_grads=cg)
         sync_overlays(L)
+        L["router_w"].grad.data.div_(hsc["loss_scale"] * hsc["accum"])
+        L["sgd"].step()
+        hsc["good_streak"] += 1
+        if hsc["good_streak"] % hsc["every"] == 0:
+            hsc["loss_scale"] = min(hsc["loss_scale"] * 2, LOSS_SCALE_MAX)
+    else:
+        hsc["n_skipped"] += 1
+        hsc["loss_scale"] = max(hsc["loss_scale"] / 2, LOSS_SCALE_MIN)
     return bool(finite)
 
 
@@ -238,13 +270,14 @@ class LaggedSteps:
     """The bench's training loop: step n + 1 is launched before the host reads
     step n's finite flag, so the GPU never idles on that read.
 
-    Each step launches forward + backward + finite check into its own flag slot
-    (two slots, alternating), then the router's SGD step and SparseAdam, both
-    gated on the device by that flag and by a sticky halt flag (capacity-mode
-    bucketing sets it on overflow), the refresh of the overlay tables from the
-    masters (the next forward reads them), and an async copy of both flags to
-    pinned host memory.  After launching step n + 1 the host reads step n's
-    flags to count it.
+    Each step launches forward + backward on the loss-scaled gradient + unscale
+    and finite check into its own flag slot (two slots, alternating), then the
+    router's SGD step and SparseAdam, both gated on the device by that flag and
+    by a sticky halt flag (capacity-mode bucketing sets it on overflow), the
+    refresh of the overlay tables from the masters (the next forward reads
+    them), the loss-scale schedule (DeviceLossScale.update, under the same
+    gate), and an async copy of both flags to pinned host memory.  After
+    launching step n + 1 the host reads step n's flags to count it.
     An overflow halts every gated update from that step on; the host recomputes
     the step with exact bucketing, applies it and relaunches the step after it.
     The updates applied, and their order, are those of moe_train_step_sync."""
@@ -275,9 +308,10 @@ class LaggedSteps:
         self.known[i] = None
         self.host[i].copy_(self.pair[i], non_blocking=True)
         self.events[i].record()
-        self.L["sgd"].step(finite=f, halt=self.halt)
+        self.L["sgd"].step(finite=f, halt=self.halt, loss_scale=self.L["scaler"])
         self.L["opt"].step(compact_grads=self.cg[i], finite=f, halt=self.halt)
         sync_overlays(self.L)
+        self.L["scaler"].update(f, self.halt)  # after the updates that read the step's scale
 
     def _resolve(self, j: int, relaunch=None) -> None:
         self.events[j].synchronize()
@@ -290,13 +324,14 @@ class LaggedSteps:
             self.halt.zero_()
             self.recomputed += 1
             f = self.finite[j]
+            # the halted updates and scale change never ran: the scale is still step j's
             self.cg[j] = _fwd_bwd_check(self.L, f, None, slot=j, reset=self.known[j] != 1)
+            self.L["sgd"].step(finite=f, loss_scale=self.L["scaler"])
+            self.L["opt"].step(compact_grads=self.cg[j], finite=f)
+            sync_overlays(self.L)
+            self.L["scaler"].update(f)
             finite = f.tolist()[0]
             self.known[j] = finite
-            if finite:
-                self.L["sgd"].step()
-                self.L["opt"].step(compact_grads=self.cg[j])
-                sync_overlays(self.L)
             if relaunch is not None:
                 self._launch(relaunch)  # the step after j, on the updated weights
         if finite:

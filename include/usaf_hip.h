@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define USAF_HIP_ABI_VERSION 1
+#define USAF_HIP_ABI_VERSION 2
 
 /* status codes */
 #define USAF_OK 0
@@ -464,14 +464,42 @@ int usaf_hip_count_step(const int32_t* finite, const int32_t* halt, int32_t* ste
  * Optional device gate (either pointer may be NULL): the step is skipped on the
  * device when *finite == 0 or *halt != 0, so a training loop can launch it
  * before it reads the step's finite flag on the host (train.py:649-672 decides
- * on the host).  A gated call cannot be the first step (first_step != 0). */
+ * on the host).  A gated call cannot be the first step (first_step != 0).
+ * Optional loss scale (scale_state, NULL = none): the gradient is first divided
+ * by loss_scale * accum read from the device state of usaf_hip_loss_scale_update
+ * and rounded to the dtype, as train.py:669-670 `p.grad.data.div_(loss_scale *
+ * ACCUM)` does before the router step; the grad buffer itself is left unchanged. */
 int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momentum_buf, int64_t n, int32_t dtype, double lr,
                                double momentum, double weight_decay, int32_t first_step, const int32_t* finite,
-                               const int32_t* halt, void* stream);
+                               const int32_t* halt, const int32_t* scale_state, double accum, void* stream);
 
 /* out = in / denom (fp32) and *finite_flag = 0 if any result is inf/NaN (train.py:661-663);
  * the caller sets *finite_flag = 1 beforehand. */
 int usaf_hip_scale_check(const float* in, float* out, int64_t n, float denom, int32_t* finite_flag, void* stream);
+
+/*
+ * Dynamic loss scale with its state on the device, for training loops that
+ * launch step n + 1 before the host reads step n's finite flag.  Replaces the
+ * host variables of train.py:31 (LOSS_SCALE_INIT = 4096, SCALE_UP_EVERY = 200),
+ * :351-353 (`(loss * loss_scale).backward()`) and :661-677 (denom = loss_scale *
+ * ACCUM; on a finite step good_streak += 1 and every SCALE_UP_EVERY-th good step
+ * loss_scale = min(2 loss_scale, 65536); on a skipped step n_skipped += 1 and
+ * loss_scale = max(loss_scale / 2, 64)).  scale_state is int32[4]: [0] the scale
+ * as fp32 bits, [1] good steps (never reset, as good_streak), [2] skipped steps.
+ *
+ * usaf_hip_loss_scale_apply: out = dtype(x * scale) for fp16/bf16 x (the gradient
+ * seed of the scaled loss; out may alias x).
+ * usaf_hip_scale_check_state: usaf_hip_scale_check with denom = scale * accum.
+ * usaf_hip_loss_scale_update: the schedule above for the step whose finite flag
+ * is *finite (NULL = finite); nothing changes when *halt != 0.  Launch it after
+ * the step's gated updates, which read the scale it replaces.
+ */
+int usaf_hip_loss_scale_apply(const void* x, void* out, int64_t n, int32_t dtype, const int32_t* scale_state,
+                              void* stream);
+int usaf_hip_scale_check_state(const float* in, float* out, int64_t n, const int32_t* scale_state, double accum,
+                               int32_t* finite_flag, void* stream);
+int usaf_hip_loss_scale_update(int32_t* scale_state, const int32_t* finite, const int32_t* halt,
+                               int32_t scale_up_every, double min_scale, double max_scale, void* stream);
 
 /* base.flat[idx[j]] = dtype(vals[j]) (usaf/moe_loader.py:218-221, 411-443); out-of-range
  * indices are skipped and set *bad_flag = 1. */

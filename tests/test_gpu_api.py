@@ -238,6 +238,162 @@ def test_quantized_streaming_fused_sync_resident(gpu_device):
     assert len(cache.fused_overlays) == 2
 
 
+def _streaming_model(seed, dt=torch.bfloat16):
+    from usaf_amd.qwen3moe_dml import patch_qwen3moe_for_dml
+    patch_qwen3moe_for_dml()
+    block = _tiny_qwen3_moe(seed=seed)
+    layer = nn.Module()
+    layer.mlp = block
+    model = nn.Module()
+    model.model = nn.Module()
+    model.model.layers = nn.ModuleList([layer])
+    model = model.to(dt)
+    experts_sd = {k: v.detach().half() for k, v in model.state_dict().items() if ".mlp.experts." in k}
+    return model, block, experts_sd
+
+
+def _scattered(base16, positions, values):
+    """The reference's fp16 weight after its scatter of the masters (moe_loader.py:218-221)."""
+    w = base16.clone()
+    w.reshape(-1)[positions.cpu().long()] = values.detach().cpu().half()
+    return w
+
+
+@pytest.mark.parametrize("resident", [False, True])
+def test_fused_overlays_follow_reselect(gpu_device, resident):
+    """train.py's overlay life cycle on the fused streaming path: cache.overlays
+    set at start-up reach the first forward (train.py:467); a RigL reselect keeps
+    the count (kept + grown = old size, train.py:560-565) and installs new
+    overlays (:603-608) followed by sync_resident: the fused view is rebuilt on
+    the new positions.  Dropped positions read the 4-bit base for a streamed
+    tensor (dequant + overlays, moe_loader.py:183-224) and keep their last
+    trained value for a resident one (in-place scatter, moe_loader.py:411-443)."""
+    _say(f"fused overlays through start-up, sync and a same-size reselect, resident={resident}")
+    from parity import check
+    from usaf_amd.importance import reselect_active
+    dt = torch.bfloat16
+    model, block, experts_sd = _streaming_model(seed=21)
+    qd = quantize_state_dict(experts_sd, device=gpu_device)
+    setup_quantized_streaming(model, qd, gpu_device, verbose=False)
+    cache = get_quantized_cache(model)
+    g = torch.Generator().manual_seed(22)
+    names = [f"model.layers.0.mlp.experts.{l}" for l in ("gate_up_proj", "down_proj")]
+    base = {n: _oracle_dequant(qd[n]) for n in names}
+    active, masters = {}, {}
+    for n in names:
+        numel = base[n].numel()
+        idx = torch.randperm(numel, generator=g)[: numel // 200].sort().values
+        active[n] = idx.to(gpu_device)
+        masters[n] = torch.nn.Parameter((base[n].reshape(-1)[idx].float()
+                                         + torch.randn(idx.numel(), generator=g) * 0.05).to(gpu_device),
+                                        requires_grad=False)
+        cache.overlays[n] = (active[n], masters[n])  # train.py:467
+    if resident:
+        cache.make_resident([0])
+        cache.apply_resident_overlays(active, masters)
+    hs = torch.randn(1, 128, 256, generator=g).to(dt)
+    wr = block.gate.weight.detach().cpu()
+
+    def run_and_check(w_eff, what):
+        ref = _reference_block(hs, wr, w_eff[names[0]].to(dt), w_eff[names[1]].to(dt), 2, True)
+        out = model.model.layers[0].mlp(hs.to(gpu_device))
+        torch.cuda.synchronize()
+        check(what, out, ref, dt)
+
+    # start-up: no sync_resident yet, the overlays alone carry the masters
+    run_and_check({n: _scattered(base[n], active[n], masters[n]) for n in names}, "start-up")
+    # an optimizer step and its sync
+    for n in names:
+        masters[n].data.add_(0.01)
+    cache.sync_resident(active, masters)
+    w_prev = {n: _scattered(base[n], active[n], masters[n]) for n in names}
+    run_and_check(w_prev, "after sync")
+    # reselect: a new selection of the same size overlapping half of the old one
+    new_active, new_masters = {}, {}
+    for n in names:
+        numel = base[n].numel()
+        old = active[n].cpu()
+        keep = old[torch.randperm(old.numel(), generator=g)[: old.numel() // 2]]
+        fresh = torch.randperm(numel, generator=g)[: old.numel()]
+        sel = torch.unique(torch.cat([keep, fresh]))[: old.numel() + old.numel() // 4]
+        final, vals, counts = reselect_active(active[n], masters[n], sel.to(gpu_device), qd[n])
+        assert final.numel() == old.numel() and counts["grown"] > 0 and counts["dropped"] > 0
+        new_active[n] = final
+        new_masters[n] = torch.nn.Parameter(vals + 0.02, requires_grad=False)  # one step after the reselect
+    cache.overlays.clear()
+    for n in names:
+        cache.overlays[n] = (new_active[n].reshape(-1).long(), new_masters[n])  # train.py:603-608
+    if resident:
+        cache.apply_resident_overlays(new_active, new_masters)
+    cache.sync_resident(new_active, new_masters)
+    if resident:
+        w_new = {n: _scattered(w_prev[n], new_active[n], new_masters[n]) for n in names}
+    else:
+        w_new = {n: _scattered(base[n], new_active[n], new_masters[n]) for n in names}
+    run_and_check(w_new, "after reselect")
+    for n in names:
+        assert cache.fused_overlays[n].ov is not None
+        if resident:
+            # the resident copy the reference would multiply holds the same weights
+            res = cache._resident["model.layers.0.mlp.experts"][n.rsplit(".", 1)[1]]
+            assert torch.equal(_bits(res), _bits(w_new[n]))
+
+
+def test_fused_overlay_dense_fallback_for_clustered_masks(gpu_device):
+    """Importance-selected positions concentrate on a few hidden channels (the
+    gradients are low-rank outer products): whole columns of 32 gate/up rows
+    are selected, more than the overlay tables hold per 32 x 16 block.  The
+    fused view then falls back to a dense copy of the trained weights for that
+    tensor, and the block still matches the oracle on the scattered weights."""
+    _say("TopKImportanceStore on column-clustered gradients -> over-dense overlay -> dense fallback")
+    from parity import check
+    from usaf_amd.importance import TopKImportanceStore
+    dt = torch.bfloat16
+    model, block, experts_sd = _streaming_model(seed=23)
+    qd = quantize_state_dict(experts_sd, device=gpu_device)
+    setup_quantized_streaming(model, qd, gpu_device, verbose=False)
+    cache = get_quantized_cache(model)
+    g = torch.Generator().manual_seed(24)
+    names = [f"model.layers.0.mlp.experts.{l}" for l in ("gate_up_proj", "down_proj")]
+    shapes = {n: tuple(qd[n]["shape"]) for n in names}
+    store = TopKImportanceStore(shapes, frac=0.005)
+    for n in names:
+        E, R, C = shapes[n]
+        hot = torch.zeros(C)
+        hot[torch.randperm(C, generator=g)[:3]] = 50.0  # three outlier input channels
+        for e in range(E):
+            u = torch.randn(R, generator=g)
+            v = torch.randn(C, generator=g) * 0.1 + hot
+            store.add(n, e, torch.outer(u, v).to(gpu_device))
+    active = store.select()
+    base = {n: _oracle_dequant(qd[n]) for n in names}
+    masters = {n: torch.nn.Parameter((base[n].reshape(-1)[active[n].cpu()].float() + 0.05).to(gpu_device),
+                                     requires_grad=False) for n in names}
+    for n in names:
+        cache.overlays[n] = (active[n], masters[n])
+    cache.sync_resident(active, masters)
+    assert cache.fused_overlays[names[0]].dense is not None, "expected the clustered gate_up mask to be over-dense"
+    hs = torch.randn(1, 128, 256, generator=g).to(dt)
+    wr = block.gate.weight.detach().cpu()
+    w_eff = {n: _scattered(base[n], active[n], masters[n]) for n in names}
+    ref = _reference_block(hs, wr, w_eff[names[0]].to(dt), w_eff[names[1]].to(dt), 2, True)
+    x = hs.to(gpu_device).requires_grad_(True)
+    out = model.model.layers[0].mlp(x)
+    out.float().square().sum().backward()
+    torch.cuda.synchronize()
+    check("clustered mask forward", out, ref, dt)
+    assert torch.isfinite(x.grad).all()
+    # the dense copy holds dtype(fp16(master)) at the active positions, bit for bit
+    dense = cache.fused_overlays[names[0]].dense
+    assert torch.equal(_bits(dense), _bits(w_eff[names[0]].to(dt)))
+    # a refresh rewrites the trained values in the dense copy
+    for n in names:
+        masters[n].data.mul_(0.5)
+    cache.sync_resident(active, masters)
+    assert torch.equal(_bits(cache.fused_overlays[names[0]].dense),
+                       _bits(_scattered(base[names[0]], active[names[0]], masters[names[0]]).to(dt)))
+
+
 def _tiny_olmoe(E=8, H=256, I=128, k=2, seed=0, norm=False):
     from transformers import OlmoeConfig
     from transformers.models.olmoe.modeling_olmoe import OlmoeSparseMoeBlock

@@ -4,8 +4,11 @@ finite flag (LaggedSteps), against the same steps in the reference loop's order
 identical parameters, optimizer state and step counts, through a non-finite
 step (skipped) and a routing that overflows the static slot capacity
 (recomputed with exact bucketing).  The lagged loop gates SparseAdam on the
-device (step count and bias corrections on the GPU); the synchronous loop
-steps it from the host.  Both refresh the overlay tables of the fused GEMMs
+device (step count and bias corrections on the GPU) and keeps the dynamic loss
+scale on the device (DeviceLossScale); the synchronous loop steps SparseAdam
+from the host and moves the loss scale by the reference's host schedule
+(train.py:661-677: halve on a skipped step, double every SCALE_UP_EVERY good
+steps, here 2 so that 6 steps double it twice).  Both refresh the overlay tables of the fused GEMMs
 from the masters after each applied step, so every forward after the first
 multiplies trained weights."""
 import pytest
@@ -21,7 +24,7 @@ def _say(msg):
 
 
 def _build(dev, zero_router):
-    L = bench.build_moe(dev, T=96, H=256, I=128, E=8, k=2, seed=5)
+    L = bench.build_moe(dev, T=96, H=256, I=128, E=8, k=2, seed=5, scale_up_every=2)
     if zero_router:
         # every expert ties for every token: 96 * 8 pairs against 96 * 3 static slots
         with torch.no_grad():
@@ -73,6 +76,11 @@ def test_lagged_loop_matches_sync_loop(gpu_device, zero_router, nan_step):
     assert loop.recomputed == A.get("recomputed", 0)
     assert (loop.recomputed >= 1) == zero_router
     assert got["adam_step"] == want["adam_step"] == steps - 1
+    hsc = A["host_scale"]
+    # 5 good steps at every 2: doubled twice, halved once -> 8192
+    assert (hsc["loss_scale"], hsc["good_streak"], hsc["n_skipped"]) == (8192.0, steps - 1, 1)
+    assert B["scaler"].state_dict() == {"loss_scale": hsc["loss_scale"], "good_streak": hsc["good_streak"],
+                                        "n_skipped": hsc["n_skipped"]}
     for key in want:
         if key == "adam_step":
             continue

@@ -44,3 +44,29 @@ def test_export_merged_weights_bit_exact(gpu_device, tmp_path):
             assert tuple(got[k]["shape"]) == tuple(entry["shape"])
         else:
             assert torch.equal(got[k].view(torch.int16), entry.view(torch.int16))
+
+
+def test_merge_masters_one_tensor_at_a_time(gpu_device):
+    """merge_masters re-quantizes each tensor before it dequantizes the next: the
+    HBM peak is one fp16 tensor and its 4-bit codes, not the whole model in fp16."""
+    print("[gpu-case] merge_masters HBM peak (4 tensors of 8 Mi elements)", flush=True)
+    from usaf_amd.checkpoint import merge_masters
+    g = torch.Generator().manual_seed(32)
+    n = 8 * 2 ** 20
+    sd = {f"model.layers.{i}.mlp.experts.gate_up_proj": (torch.randn(8, 1024, 1024, generator=g) * 0.02).half()
+          for i in range(4)}
+    q = quantize_state_dict(sd, device=gpu_device)
+    q = {k: {kk: (vv.cpu() if isinstance(vv, torch.Tensor) else vv) for kk, vv in v.items()} for k, v in q.items()}
+    masters = {k: torch.randn(n // 200, generator=g) * 0.05 for k in q}
+    active = {k: torch.randperm(n, generator=g)[: n // 200] for k in q}
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(gpu_device)
+    torch.cuda.reset_peak_memory_stats(gpu_device)
+    out = merge_masters(q, masters, active, device=gpu_device)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(gpu_device) - base
+    fp16_one = 2 * n
+    assert set(out) == set(q)
+    # one fp16 tensor + its codes, scales, zeros, the CPU entry's device copies and the
+    # master/index copies: well under two fp16 tensors (all four would be 64 MiB)
+    assert peak < 2 * fp16_one, f"merge peak {peak / 2 ** 20:.1f} MiB for {fp16_one / 2 ** 20:.0f} MiB tensors"

@@ -57,3 +57,57 @@ def test_hbm_resident_store(gpu_device, tmp_path):
     t = get_hidden(store, 9, gpu_device)
     assert t.shape == (1,) + arr.shape[1:]
     assert np.array_equal(t[0].cpu().numpy().view(np.uint16), np.asarray(arr[9]).view(np.uint16))
+
+
+class _ToyDecoderLayer(torch.nn.Module):
+    """A block whose class name the activation cache hooks (…DecoderLayer); it
+    returns a tuple, as transformers' decoder layers do."""
+
+    def __init__(self, h):
+        super().__init__()
+        self.lin = torch.nn.Linear(h, h)
+
+    def forward(self, x):
+        return (torch.tanh(self.lin(x)) * 3.0 + x,)
+
+
+@pytest.mark.parametrize("cache_on", ["cpu", "cuda"])
+def test_activation_cache_on_gpu_model(gpu_device, cache_on):
+    _say(f"ActivationCache of a GPU model, cache on {cache_on}: values read right after each forward")
+    from usaf_amd.cache import ActivationCache
+    torch.manual_seed(3)
+    h = 1024
+    model = torch.nn.Sequential(_ToyDecoderLayer(h), _ToyDecoderLayer(h)).to(gpu_device)
+    blocks = [model[0], model[1]]
+
+    def run(x):
+        for b in blocks:
+            x = b(x)[0]
+        return x
+
+    dev = gpu_device if cache_on == "cuda" else torch.device("cpu")
+    cache = ActivationCache(dev)
+    cache.register_hooks(model)
+    assert cache.cached_modules == {"0", "1"}
+    for step in range(3):
+        x = torch.randn(64, 512, h, device=gpu_device)  # 128 MiB per block output
+        with torch.no_grad():
+            y0 = blocks[0](x)[0]
+            # the cached copy is read before any synchronisation of the GPU model's
+            # stream (a host-side clone of a CPU copy does not wait for the GPU)
+            got = cache.get_cached("0", step)[0]
+            assert got.device.type == dev.type
+            snap = got.clone()
+            assert torch.equal(snap.cpu(), y0.cpu()), f"step {step}: cached block output differs"
+            y1 = blocks[1](y0)[0]
+            assert torch.equal(cache.get_cached("1", step)[0].cpu(), y1.cpu())
+        cache.advance_step()
+    assert cache.get_cached("0", 3) is None
+    assert cache.memory_estimate_mb() == pytest.approx(3 * 2 * 64 * 512 * h * 4 / 2 ** 20)
+    cache.invalidate({"1"})
+    with torch.no_grad():
+        blocks[1](y0)
+    assert "1" not in cache.cached_modules and cache.get_cached("1", 0) is None
+    cache.remove_hooks()
+    cache.reset()
+    assert not cache.cached_modules

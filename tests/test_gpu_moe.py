@@ -16,6 +16,8 @@ from usaf_amd import moe as G
 from usaf_amd.moe_loader import SparseGradStore, overlay_scatter
 from usaf_amd.sparse_optim import SparseAdam
 
+from parity import check
+
 pytestmark = pytest.mark.gpu
 TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
 
@@ -244,7 +246,7 @@ def test_experts_forward_cfg1(gpu_device):
     torch.cuda.synchronize()
     torch.set_num_threads(16)
     ref = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"])
-    assert rel_err(out, ref) <= TOL[dt]
+    check("cfg1 out", out, ref, dt, say=_say)
 
 
 def test_experts_forward_mixtral_shape(gpu_device):
@@ -255,7 +257,7 @@ def test_experts_forward_mixtral_shape(gpu_device):
     torch.cuda.synchronize()
     torch.set_num_threads(16)
     ref = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"])
-    assert rel_err(out, ref) <= TOL[dt]
+    check("mixtral out", out, ref, dt, say=_say)
 
 
 # ---- backward -----------------------------------------------------------------------
@@ -515,6 +517,100 @@ def test_scale_check(gpu_device):
     N.call("usaf_hip_scale_check", x.data_ptr(), out.data_ptr(), x.numel(), 4096.0, flag.data_ptr(),
            N.stream_ptr(gpu_device))
     assert int(flag.item()) == 0
+
+
+def _host_schedule(seq, init, every, lo=64.0, hi=65536.0):
+    """train.py:673-677 as the reference's host code runs it, over a sequence of
+    (finite, halted) steps; a halted step is not a step of the reference loop."""
+    scale, good, skipped, out = init, 0, 0, []
+    for finite, halted in seq:
+        if not halted:
+            if finite:
+                good += 1
+                if good % every == 0:
+                    scale = min(scale * 2, hi)
+            else:
+                skipped += 1
+                scale = max(scale / 2, lo)
+        out.append((scale, good, skipped))
+    return out
+
+
+def test_loss_scale_schedule_on_device(gpu_device):
+    _say("DeviceLossScale.update against the reference's host schedule (halve floor 64, double every 3 cap 65536)")
+    from usaf_amd.sparse_optim import DeviceLossScale
+    g = torch.Generator().manual_seed(5)
+    # long enough to hit both the cap (from 16384 with doublings) and the floor (runs of skips)
+    seq = [(bool(f), bool(h)) for f, h in zip((torch.rand(400, generator=g) < 0.8).tolist(),
+                                                (torch.rand(400, generator=g) < 0.05).tolist())]
+    seq[40:55] = [(False, False)] * 15  # 15 skips in a row: down to the floor
+    ls = DeviceLossScale(16384.0, 3, device=gpu_device)
+    one = torch.ones(1, dtype=torch.int32, device=gpu_device)
+    zero = torch.zeros(1, dtype=torch.int32, device=gpu_device)
+    got = []
+    for finite, halted in seq:
+        ls.update(one if finite else zero, one if halted else zero)
+        got.append(tuple(ls.state_dict().values()))
+    want = _host_schedule(seq, 16384.0, 3)
+    assert got == want
+    scales = [w[0] for w in want]
+    assert 64.0 in scales and 65536.0 in scales
+    ls.update()  # no flags: a finite step
+    assert ls.good_streak == want[-1][1] + 1
+
+
+@pytest.mark.parametrize("dtype,n", [(torch.bfloat16, 4096 * 2048), (torch.float16, 4096), (torch.float16, 1003),
+                                     (torch.bfloat16, 13)])
+def test_loss_scale_apply_and_unscale(gpu_device, dtype, n):
+    _say(f"loss_scale_apply / scale_check_state {dtype} n={n}")
+    from usaf_amd.sparse_optim import DeviceLossScale
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, generator=g).to(dtype).to(gpu_device)
+    x[:5] = torch.tensor([0.0, -0.0, 1e-30, 3.0e38, float("nan")]).to(dtype)
+    ls = DeviceLossScale(4096.0, device=gpu_device)
+    y = ls.scale_grad(x)
+    ref = x * 4096.0  # torch's tensor * Python float in the dtype
+    assert torch.equal(torch.isnan(y), torch.isnan(ref))
+    m = ~torch.isnan(ref)
+    assert torch.equal(y[m].view(torch.int16), ref[m].view(torch.int16))
+    ls.scale_grad(y, out=y)  # in place
+    assert torch.equal(y[m].view(torch.int16), (ref * 4096.0)[m].view(torch.int16))
+    ls2 = DeviceLossScale(128.0, accum=4, device=gpu_device)
+    c = torch.randn(10007, generator=g).to(gpu_device)
+    out = torch.empty_like(c)
+    flag = torch.ones(1, dtype=torch.int32, device=gpu_device)
+    ls2.unscale_check(c, out, flag)
+    assert int(flag.item()) == 1 and torch.equal(out, c / (128.0 * 4))
+    c[77] = float("-inf")
+    ls2.unscale_check(c, out, flag)
+    assert int(flag.item()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_momentum_sgd_loss_scaled(gpu_device, dtype):
+    _say(f"MomentumSGD with the device loss scale: grad.div_(scale * ACCUM) then torch's SGD step, {dtype}")
+    from usaf_amd.sparse_optim import DeviceLossScale, MomentumSGD
+    g = torch.Generator().manual_seed(79)
+    p0 = (torch.randn(128, 2048, generator=g) * 0.05).to(dtype).to(gpu_device)
+    a = p0.clone().requires_grad_(True)
+    b = p0.clone().requires_grad_(True)
+    ls = DeviceLossScale(1024.0, accum=2, device=gpu_device)
+    ours = MomentumSGD([a], lr=2e-4, momentum=0.9, weight_decay=0.005)
+    plain = MomentumSGD([b], lr=2e-4, momentum=0.9, weight_decay=0.005)
+    one = torch.ones(1, dtype=torch.int32, device=gpu_device)
+    for step in range(3):
+        grad = (torch.randn(128, 2048, generator=g) * 2048.0).to(dtype).to(gpu_device)
+        a.grad = grad.clone()
+        b.grad = grad.clone()
+        if step == 0:
+            ours.step(loss_scale=ls)
+        else:
+            ours.step(finite=one, loss_scale=ls)
+        b.grad.div_(1024.0 * 2)  # train.py:669-670, on the host's float
+        plain.step()
+        torch.cuda.synchronize()
+        assert torch.equal(a.grad, grad), "the gradient buffer is left unchanged"
+        assert torch.equal(a.detach(), b.detach()) and torch.equal(ours._buf[0], plain._buf[0])
 
 
 # ---- slot-major operands and the sampled gradient ------------------------------------

@@ -23,6 +23,8 @@ from usaf_amd import _native as N
 from usaf_amd import moe as G
 from usaf_amd.moe_loader import SparseGradStore
 
+from parity import check
+
 pytestmark = pytest.mark.gpu
 TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3}
 
@@ -179,11 +181,7 @@ def test_overlay_routed_layer_vs_oracle(gpu_device, dtype):
                            ("dweights", w.grad.cpu()[routed], dw_r[routed]),
                            ("sampled dW gate_up", store.compact["L.gate_up_proj"], comp["gate_up_proj"]),
                            ("sampled dW down", store.compact["L.down_proj"], comp["down_proj"])):
-        got = got.detach().float().cpu()
-        ref = ref.detach().float().cpu()
-        rel = float((got - ref).abs().max() / ref.abs().max())
-        _say(f"  {name}: rel {rel:.2e} (bar {TOL[dtype]:.0e})")
-        assert rel <= TOL[dtype], name
+        check(name, got, ref, dtype, say=_say)
     sep = float((out_plain.float() - out_r.float()).abs().max() / out_r.float().abs().max())
     _say(f"  without the overlay the output would be off by rel {sep:.2e}")
     assert sep > 4 * TOL[dtype]

@@ -69,7 +69,11 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_gather_transpose_blocked": [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p],
     "usaf_hip_sddmm_blocked": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_i32,
                                _c_p],
-    "usaf_hip_sgd_momentum_step": [_c_p, _c_p, _c_p, _c_i64, _c_i32, _c_d, _c_d, _c_d, _c_i32, _c_p, _c_p, _c_p],
+    "usaf_hip_sgd_momentum_step": [_c_p, _c_p, _c_p, _c_i64, _c_i32, _c_d, _c_d, _c_d, _c_i32, _c_p, _c_p, _c_p,
+                                   _c_d, _c_p],
+    "usaf_hip_loss_scale_apply": [_c_p, _c_p, _c_i64, _c_i32, _c_p, _c_p],
+    "usaf_hip_scale_check_state": [_c_p, _c_p, _c_i64, _c_p, _c_d, _c_p, _c_p],
+    "usaf_hip_loss_scale_update": [_c_p, _c_p, _c_p, _c_i32, _c_d, _c_d, _c_p],
     "usaf_hip_router_fwd": [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32, _c_p, _c_p, _c_i32, _c_p,
                             _c_p],
     "usaf_hip_router_dw": [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p],

@@ -3,6 +3,12 @@
 Same interface as the reference's ``ActivationCache``: forward hooks on every
 module whose class name marks a transformer block record its (detached)
 outputs per forward call, on ``device`` -- pass the GPU to keep them in HBM.
+As in the reference (cache.py:34-49), a copy to another device is a blocking
+``.to(device)``: a GPU output cached on the CPU has landed when the hook
+returns, so ``get_cached`` right after the forward reads finished data; an
+output already on ``device`` is kept as a detached alias, not copied.
+``memory_estimate_mb`` also counts the tensors inside tuple outputs (the
+reference counts bare tensors only).
 """
 from __future__ import annotations
 
@@ -16,7 +22,7 @@ _BLOCK_NAMES = ("DecoderLayer", "TransformerBlock", "GemmaDecoderLayer", "Gemma4
 
 def _detach_to(x: Any, device: torch.device) -> Any:
     if isinstance(x, torch.Tensor):
-        return x.detach().to(device, non_blocking=True)
+        return x.detach().to(device)
     if isinstance(x, tuple):
         return tuple(_detach_to(t, device) for t in x)
     return x

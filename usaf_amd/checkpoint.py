@@ -25,7 +25,7 @@ def merge_masters(q_dict: Dict[str, Any], masters: Dict[str, torch.Tensor], acti
                   group_size: int = 128, device=None) -> Dict[str, Any]:
     """The merged, re-quantized state dict (CPU tensors) without touching disk."""
     dev = torch.device(device) if device is not None else N.default_device()
-    merged: Dict[str, Any] = {}
+    out: Dict[str, Any] = {}
     for name, entry in q_dict.items():
         if isinstance(entry, dict) and "q" in entry:
             t = dequantize_4bit(entry["q"], entry["s"], entry["z"], entry["shape"],
@@ -38,13 +38,13 @@ def merge_masters(q_dict: Dict[str, Any], masters: Dict[str, torch.Tensor], acti
         if name in masters and name in active_idx:
             t = t.contiguous()
             overlay_scatter(t, active_idx[name], masters[name])
-        merged[name] = t
-    out: Dict[str, Any] = {}
-    for name, t in merged.items():
+        # re-quantized and moved to the host before the next tensor is dequantized:
+        # the HBM peak is one fp16 tensor and its codes
         q = quantize_state_dict({name: t}, group_size=group_size, device=dev)[name]
+        del t
         out[name] = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in q.items()} \
             if isinstance(q, dict) else q.cpu()
-        merged[name] = None  # release the fp16 copy before the next tensor
+        del q
     return out
 
 

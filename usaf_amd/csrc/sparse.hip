@@ -558,18 +558,28 @@ __global__ __launch_bounds__(256) void sgd_momentum_kernel(void* __restrict__ p,
                                                            void* __restrict__ buf, int64_t n, float lr,
                                                            float momentum, float wd, int first,
                                                            const int32_t* __restrict__ finite,
-                                                           const int32_t* __restrict__ halt) {
+                                                           const int32_t* __restrict__ halt,
+                                                           const int32_t* __restrict__ scale_state, float accum) {
 #pragma clang fp contract(off)
   // the step's gate, read on the device (no host read): skipped unless the
   // finite flag is set and the halt flag is clear
   if ((finite && *finite == 0) || (halt && *halt != 0)) return;
+  // the loss-scaled gradient is first divided by loss_scale * ACCUM and rounded
+  // to the dtype (train.py:669-670 grad.div_); the gradient buffer is not written
+  const float denom = scale_state ? __int_as_float(scale_state[0]) * accum : 1.f;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   // Each fp32 result is pinned (asm) before its conversion: otherwise the
   // compiler folds product-then-fp16 into v_fma_mix, which rounds once from the
   // exact product instead of rounding to fp32 first as torch's kernels do.
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     const float pf = load_as_f32<DT>(p, i);
-    float d32 = __builtin_fmaf(wd, pf, load_as_f32<DT>(grad, i));
+    float g = load_as_f32<DT>(grad, i);
+    if (scale_state) {
+      float gs = g / denom;
+      asm volatile("" : "+v"(gs));
+      g = round_to<DT>(gs);
+    }
+    float d32 = __builtin_fmaf(wd, pf, g);
     asm volatile("" : "+v"(d32));
     const float d = round_to<DT>(d32);
     float b;
@@ -599,6 +609,76 @@ __global__ __launch_bounds__(256) void scale_check_kernel(const float* __restric
     ok = ok && isfinite(v);
   }
   if (!ok) finite[0] = 0;  // benign race: every writer stores the same value
+}
+
+// ---- dynamic loss scale with its state on the device ------------------------------
+// The trainer's loss scaling (train.py:31, 351-353, 661-677) for loops that launch
+// step n + 1 before the host has read step n's finite flag.  State, int32[4]:
+//   [0] the loss scale (fp32 bits), [1] good steps (train.py's good_streak, never
+//   reset by a skipped step), [2] skipped steps, [3] unused.
+__device__ __forceinline__ float loss_scale_of(const int32_t* state) { return __int_as_float(state[0]); }
+
+// out = DT(x * scale): the gradient seed of the scaled loss.  VEC: 8 elements per
+// 16-byte vector (n % 8 == 0, both bases 16-byte aligned).
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void loss_scale_mul_kernel(const uint16_t* __restrict__ x,
+                                                             uint16_t* __restrict__ out, int64_t n,
+                                                             const int32_t* __restrict__ state) {
+  const float sc = loss_scale_of(state);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if constexpr (VEC) {
+    const int64_t nv = n / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride) {
+      const uint4 a = reinterpret_cast<const uint4*>(x)[i];
+      const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x2 v = unpack2<DT>(w[q]);
+        o[q] = pack2<DT>(v.x * sc, v.y * sc);
+      }
+      reinterpret_cast<uint4*>(out)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+      store_from_f32<DT>(out, i, load_as_f32<DT>(x, i) * sc);
+  }
+}
+
+// out = in / (scale * accum) and finite[0] = 0 if any result is inf/NaN
+// (train.py:661-663 with denom = loss_scale * ACCUM read from the state).
+__global__ __launch_bounds__(256) void scale_check_state_kernel(const float* __restrict__ in,
+                                                                float* __restrict__ out, int64_t n,
+                                                                const int32_t* __restrict__ state, float accum,
+                                                                int32_t* __restrict__ finite) {
+  const float denom = loss_scale_of(state) * accum;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  bool ok = true;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float v = in[i] / denom;
+    out[i] = v;
+    ok = ok && isfinite(v);
+  }
+  if (!ok) finite[0] = 0;  // benign race: every writer stores the same value
+}
+
+// The schedule of train.py:673-677, one thread, after the step's gated updates:
+// a finite step counts as good and doubles the scale on every `every`-th good
+// step (capped at hi); a non-finite one counts as skipped and halves it (floored
+// at lo).  A halted step (halt[0] != 0) changes nothing.
+__global__ void loss_scale_update_kernel(int32_t* __restrict__ state, const int32_t* __restrict__ finite,
+                                         const int32_t* __restrict__ halt, int32_t every, float lo, float hi) {
+  if (halt && *halt != 0) return;
+  float sc = loss_scale_of(state);
+  if (!finite || *finite != 0) {
+    const int32_t good = state[1] + 1;
+    state[1] = good;
+    if (good % every == 0) sc = fminf(sc * 2.f, hi);
+  } else {
+    state[2] = state[2] + 1;
+    sc = fmaxf(sc * 0.5f, lo);
+  }
+  state[0] = __float_as_int(sc);
 }
 
 template <int DT>
@@ -883,10 +963,12 @@ extern "C" int usaf_hip_count_step(const int32_t* finite, const int32_t* halt, i
 
 extern "C" int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momentum_buf, int64_t n, int32_t dtype,
                                           double lr, double momentum, double weight_decay, int32_t first_step,
-                                          const int32_t* finite, const int32_t* halt, void* stream) {
+                                          const int32_t* finite, const int32_t* halt, const int32_t* scale_state,
+                                          double accum, void* stream) {
   if (n < 0) return set_error(USAF_ERR_INVALID, "sgd_momentum_step: negative n");
   if (first_step && (finite || halt))
     return set_error(USAF_ERR_INVALID, "sgd_momentum_step: the first step (momentum buffer = d) cannot be gated");
+  if (scale_state && !(accum >= 1.0)) return set_error(USAF_ERR_INVALID, "sgd_momentum_step: accum must be >= 1");
   if (n == 0) return clear_error();
   if (!p || !grad || !momentum_buf) return set_error(USAF_ERR_INVALID, "sgd_momentum_step: null pointer");
   hipStream_t st = as_stream(stream);
@@ -895,15 +977,18 @@ extern "C" int usaf_hip_sgd_momentum_step(void* p, const void* grad, void* momen
   switch (dtype) {
     case USAF_F32:
       sgd_momentum_kernel<USAF_F32><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first,
-                                                                                  finite, halt);
+                                                                                  finite, halt, scale_state,
+                                                                                  (float)accum);
       break;
     case USAF_F16:
       sgd_momentum_kernel<USAF_F16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first,
-                                                                                  finite, halt);
+                                                                                  finite, halt, scale_state,
+                                                                                  (float)accum);
       break;
     case USAF_BF16:
       sgd_momentum_kernel<USAF_BF16><<<grid_for(n), 256, 0, st>>>(p, grad, momentum_buf, n, lr_f, m_f, wd_f, first,
-                                                                                  finite, halt);
+                                                                                  finite, halt, scale_state,
+                                                                                  (float)accum);
       break;
     default:
       return set_error(USAF_ERR_INVALID, "sgd_momentum_step: dtype must be fp32, fp16 or bf16");
@@ -918,6 +1003,49 @@ extern "C" int usaf_hip_scale_check(const float* in, float* out, int64_t n, floa
   if (!in || !out || !finite_flag) return set_error(USAF_ERR_INVALID, "scale_check: null pointer");
   scale_check_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(in, out, n, denom, finite_flag);
   return check_launch("scale_check");
+}
+
+extern "C" int usaf_hip_loss_scale_apply(const void* x, void* out, int64_t n, int32_t dtype,
+                                         const int32_t* scale_state, void* stream) {
+  if (n < 0) return set_error(USAF_ERR_INVALID, "loss_scale_apply: negative n");
+  if (dtype != USAF_F16 && dtype != USAF_BF16)
+    return set_error(USAF_ERR_INVALID, "loss_scale_apply: dtype must be fp16 or bf16");
+  if (n == 0) return clear_error();
+  if (!x || !out || !scale_state) return set_error(USAF_ERR_INVALID, "loss_scale_apply: null pointer");
+  hipStream_t st = as_stream(stream);
+  const bool vec = n % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0;
+  const uint16_t* xi = static_cast<const uint16_t*>(x);
+  uint16_t* oi = static_cast<uint16_t*>(out);
+  if (dtype == USAF_BF16) {
+    if (vec) loss_scale_mul_kernel<USAF_BF16, true><<<grid_for(n / 8), 256, 0, st>>>(xi, oi, n, scale_state);
+    else loss_scale_mul_kernel<USAF_BF16, false><<<grid_for(n), 256, 0, st>>>(xi, oi, n, scale_state);
+  } else {
+    if (vec) loss_scale_mul_kernel<USAF_F16, true><<<grid_for(n / 8), 256, 0, st>>>(xi, oi, n, scale_state);
+    else loss_scale_mul_kernel<USAF_F16, false><<<grid_for(n), 256, 0, st>>>(xi, oi, n, scale_state);
+  }
+  return check_launch("loss_scale_apply");
+}
+
+extern "C" int usaf_hip_scale_check_state(const float* in, float* out, int64_t n, const int32_t* scale_state,
+                                          double accum, int32_t* finite_flag, void* stream) {
+  if (n < 0) return set_error(USAF_ERR_INVALID, "scale_check_state: negative n");
+  if (!(accum >= 1.0)) return set_error(USAF_ERR_INVALID, "scale_check_state: accum must be >= 1");
+  if (n == 0) return clear_error();
+  if (!in || !out || !scale_state || !finite_flag)
+    return set_error(USAF_ERR_INVALID, "scale_check_state: null pointer");
+  scale_check_state_kernel<<<grid_for(n), 256, 0, as_stream(stream)>>>(in, out, n, scale_state, (float)accum,
+                                                                       finite_flag);
+  return check_launch("scale_check_state");
+}
+
+extern "C" int usaf_hip_loss_scale_update(int32_t* scale_state, const int32_t* finite, const int32_t* halt,
+                                          int32_t scale_up_every, double min_scale, double max_scale, void* stream) {
+  if (!scale_state) return set_error(USAF_ERR_INVALID, "loss_scale_update: null pointer");
+  if (scale_up_every < 1 || !(min_scale > 0.0) || !(max_scale >= min_scale))
+    return set_error(USAF_ERR_INVALID, "loss_scale_update: need scale_up_every >= 1 and 0 < min_scale <= max_scale");
+  loss_scale_update_kernel<<<1, 1, 0, as_stream(stream)>>>(scale_state, finite, halt, scale_up_every,
+                                                           (float)min_scale, (float)max_scale);
+  return check_launch("loss_scale_update");
 }
 
 extern "C" int usaf_hip_overlay_refresh(const float* p, int64_t n, const int32_t* words_a, const int32_t* index_a,

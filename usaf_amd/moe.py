@@ -127,6 +127,11 @@ _OVL_CAP = 16  # entries per (wave, k-step, fragment register): one 16-bit LDS s
 _OVL_WAVES, _OVL_WORDS = 8, 64  # waves per n-tile, entry words per wave and k-step
 
 
+class OverlayTooDense(ValueError):
+    """A set of trained positions puts more than 16 into one fragment register's
+    32 x 16 weight block of a fused GEMM: the overlay tables cannot hold it."""
+
+
 def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     """Where each flat position ``idx`` of an expert tensor ``shape`` = [E, R, C]
     sits in the fused GEMM ``kind``'s weight fragments, as the entry tables of
@@ -146,7 +151,7 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     The entries of one (u, k-step, j) are ranked in position order; rank r goes
     to word (u * nk + ks) * 64 + 16 j + r (lane 16 j + r stores it).  More than
     16 positions in one register's 32 x 16 block of a wave (3 % local density)
-    raise ValueError."""
+    raise OverlayTooDense (a ValueError)."""
     E, R, C = (int(d) for d in shape)
     idx = idx.reshape(-1).to(torch.int64)
     e = torch.div(idx, R * C, rounding_mode="floor")
@@ -189,8 +194,8 @@ def overlay_entries(kind: str, idx: torch.Tensor, shape, inter: int):
     rank = torch.empty_like(rank_sorted)
     rank[order] = rank_sorted
     if rank.numel() and int(rank.max()) >= _OVL_CAP:
-        raise ValueError(f"overlay ({kind}): more than {_OVL_CAP} trained positions in one 32 x 16 weight block; "
-                         f"use dense expert weights with overlay_scatter for such masks")
+        raise OverlayTooDense(f"overlay ({kind}): more than {_OVL_CAP} trained positions in one 32 x 16 weight "
+                              f"block; use dense expert weights with overlay_scatter for such masks")
     word = group * _OVL_WORDS + 16 * j + rank
     n_words = E * n_nt * _OVL_WAVES * nk * _OVL_WORDS
     return word.to(torch.int32), off.to(torch.int32), n_words

@@ -23,7 +23,7 @@ import torch.nn as nn
 
 from . import _native as N
 from .importance import TopKImportanceStore  # noqa: F401  (moe_loader.py:584-631, GPU selection)
-from .moe import Q4Overlay, Q4Tensor, timed_call
+from .moe import OverlayTooDense, Q4Overlay, Q4Tensor, timed_call
 from .olmoe_streaming import _record_grad, apply_captured_expert_grads  # noqa: F401  (moe_loader.py:778-802)
 from .quantization import dequantize_4bit
 
@@ -100,9 +100,10 @@ class QuantizedExpertCache:
         self._build_index()
         self._resident: Dict[str, Dict[str, torch.Tensor]] = {}
         self._resident_active = False
-        # fused path: trained values of 4-bit tensors as overlay tables the fused GEMMs
-        # read (Q4Overlay), refreshed by sync_resident; built for this activation dtype
-        self.fused_overlays: Dict[str, Any] = {}
+        # fused path: trained values of 4-bit tensors as the fused GEMMs read them
+        # (FusedOverlay: Q4Overlay tables, or a dense copy for over-dense masks),
+        # built from ``overlays`` / sync_resident for this activation dtype
+        self.fused_overlays: Dict[str, "FusedOverlay"] = {}
         self.fused_dtype: Optional[torch.dtype] = None
         self.hits = 0
         self.misses = 0
@@ -122,21 +123,29 @@ class QuantizedExpertCache:
     # ---- 4-bit access for the fused path --------------------------------------------
 
     def get_q4(self, expert_module_name: str) -> Dict[str, Any]:
-        """The HBM 4-bit tensors (Q4Tensor) or dense entries of a module, by local name."""
+        """The weights the fused GEMMs read for a module, by local name: the HBM
+        4-bit tensor (Q4Tensor), or the dense copy of a tensor whose trained
+        positions are too dense for overlay tables, or a dense entry."""
+        self._fused_from_overlays(expert_module_name)
         out = {}
         for full_name, local in self._expert_to_params.get(expert_module_name, []):
+            fo = self.fused_overlays.get(full_name)
+            if fo is not None and fo.dense is not None:
+                out[local] = fo.dense
+                continue
             entry = self._q_dict.get(full_name)
             if entry is not None:
                 out[local] = entry
         return out
 
     def get_q4_overlays(self, expert_module_name: str) -> Dict[str, Any]:
-        """The fused overlays (Q4Overlay) of a module's 4-bit tensors, by local name."""
+        """The overlay tables (Q4Overlay) of a module's 4-bit tensors, by local name."""
+        self._fused_from_overlays(expert_module_name)
         out = {}
         for full_name, local in self._expert_to_params.get(expert_module_name, []):
-            ov = self.fused_overlays.get(full_name)
-            if ov is not None:
-                out[local] = ov
+            fo = self.fused_overlays.get(full_name)
+            if fo is not None and fo.ov is not None:
+                out[local] = fo.ov
         return out
 
     # ---- dequantized copies --------------------------------------------------------
@@ -250,7 +259,9 @@ class QuantizedExpertCache:
         return None
 
     def apply_resident_overlays(self, active_idx, masters) -> None:
-        """moe_loader.py:411-423: scatter master values into the resident copies."""
+        """moe_loader.py:411-423: scatter master values into the resident copies
+        (and into the fused GEMMs' view of the 4-bit tensors)."""
+        self._sync_fused(active_idx, masters)
         self._scatter_masters(active_idx, masters)
 
     def sync_resident(self, active_idx, masters) -> None:
@@ -262,26 +273,64 @@ class QuantizedExpertCache:
             return
         self._scatter_masters(active_idx, masters)
 
+    # ---- the fused GEMMs' view of the trained values -----------------------------------
+
+    def _fused_target(self, fname: str) -> Optional[Q4Tensor]:
+        entry = self._q_dict.get(fname)
+        local = fname.rsplit(".", 1)[-1]
+        if (self.fused_dtype is None or not isinstance(entry, Q4Tensor) or local not in ("gate_up_proj", "down_proj")
+                or not entry.fused_ok()):
+            return None
+        return entry
+
+    def _sticky(self, fname: str) -> bool:
+        """Whether a position dropped from the active set keeps its last trained
+        value: the reference scatters masters into its resident copies in place
+        (moe_loader.py:411-443), so a resident tensor keeps every value it was
+        ever given, while a streamed one is re-dequantized with the current
+        overlays only (moe_loader.py:183-224)."""
+        name, local = fname.rsplit(".", 1)
+        return self._resident_active and name in self._resident and local in self._resident[name]
+
+    def _sync_one(self, fname: str, aidx: torch.Tensor, vals, refresh: bool) -> None:
+        """Make the fused view of ``fname`` hold ``vals`` at ``aidx``: refresh the
+        values when the positions are the ones it was built for (``refresh``, or
+        when ``vals`` is another tensor than last time), otherwise rebuild it."""
+        entry = self._fused_target(fname)
+        if entry is None:
+            return
+        fo = self.fused_overlays.get(fname)
+        v = vals.data if isinstance(vals, torch.nn.Parameter) else vals
+        v = v.detach().reshape(-1).to(device=self._device, dtype=torch.float32).contiguous()
+        if fo is not None and fo.same_positions(aidx):
+            if refresh or fo.vals_src is not vals:
+                fo.refresh(v)
+                fo.vals_src = vals
+            return
+        retired = fo.retired_after(aidx) if (fo is not None and self._sticky(fname)) else None
+        local = fname.rsplit(".", 1)[-1]
+        self.fused_overlays[fname] = FusedOverlay(entry, local.replace("_proj", ""), aidx, v, self.fused_dtype,
+                                                  retired)
+        self.fused_overlays[fname].vals_src = vals
+
     def _sync_fused(self, active_idx, masters) -> None:
         if self.fused_dtype is None:
             return
         for fname, aidx in active_idx.items():
-            entry = self._q_dict.get(fname)
-            local = fname.rsplit(".", 1)[-1]
-            if not isinstance(entry, Q4Tensor) or local not in ("gate_up_proj", "down_proj") or not entry.fused_ok():
-                continue
-            vals = masters[fname]
-            vals = (vals.data if isinstance(vals, torch.nn.Parameter) else vals).reshape(-1)
-            vals = vals.to(device=self._device, dtype=torch.float32).contiguous()
-            ov = self.fused_overlays.get(fname)
-            if ov is None or ov.n != aidx.numel():
-                role = local.replace("_proj", "")
-                shape = entry.shape
-                inter = int(shape[1]) // 2 if role == "gate_up" else int(shape[2])
-                self.fused_overlays[fname] = Q4Overlay(role, aidx.to(self._device), shape, inter, self.fused_dtype,
-                                                       vals)
-            else:
-                ov.refresh(vals)
+            if fname in masters:
+                self._sync_one(fname, aidx, masters[fname], refresh=True)
+
+    def _fused_from_overlays(self, expert_module_name: str) -> None:
+        """Before a fused forward: the trained values set in ``overlays`` (the
+        trainer sets them at start-up, after a resume and after a reselect,
+        train.py:467, 607) reach the fused view of each 4-bit tensor; values
+        already synced (sync_resident) are not rewritten."""
+        if self.fused_dtype is None:
+            return
+        for full_name, _ in self._expert_to_params.get(expert_module_name, []):
+            ov = self.overlays.get(full_name)
+            if ov is not None:
+                self._sync_one(full_name, ov[0], ov[1], refresh=False)
 
     def _scatter_masters(self, active_idx, masters) -> None:
         for fname, aidx in active_idx.items():
@@ -341,6 +390,76 @@ class QuantizedExpertCache:
             elif isinstance(entry, torch.Tensor):
                 total += entry.numel() * entry.element_size()
         return total / (1024 * 1024)
+
+
+class FusedOverlay:
+    """Trained values over one HBM 4-bit expert tensor as the fused GEMMs read
+    them: its Q4Overlay tables (``ov``) or, when the positions are too dense
+    for the tables (OverlayTooDense), a dense copy of the weights in the
+    activation dtype (``dense``: dequant to fp16, the masters scattered as
+    fp16, converted -- the reference's fp16 weights after its scatter,
+    moe_loader.py:218-221, in the activation dtype).
+
+    ``idx`` / ``vals``: the active positions and their fp32 masters (aligned);
+    ``retired``: optional (positions, values) kept from an earlier set
+    (QuantizedExpertCache._sticky).  ``refresh(vals)`` writes new masters."""
+
+    def __init__(self, entry: Q4Tensor, role: str, idx: torch.Tensor, vals: torch.Tensor, dtype: torch.dtype,
+                 retired: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
+        dev = entry.device
+        # index tensors known to hold these positions, with their versions (the
+        # trainer passes the same positions as several tensor objects)
+        self._known = [(idx, idx._version)]
+        self.active = idx.reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
+        self.n_active = int(self.active.numel())
+        if vals.numel() != self.n_active:
+            raise ValueError(f"overlay has {self.n_active} positions and {vals.numel()} values")
+        if retired is not None and retired[0].numel():
+            self.positions = torch.cat([self.active, retired[0]])
+            self.values = torch.cat([vals, retired[1]])
+        else:
+            self.positions = self.active
+            self.values = vals.clone()
+        self.vals_src = None
+        shape = entry.shape
+        inter = int(shape[1]) // 2 if role == "gate_up" else int(shape[2])
+        self.ov: Optional[Q4Overlay] = None
+        self.dense: Optional[torch.Tensor] = None
+        try:
+            self.ov = Q4Overlay(role, self.positions, shape, inter, dtype, self.values)
+        except OverlayTooDense:
+            base = entry.dequantize(torch.float16)
+            overlay_scatter(base, self.positions, self.values)
+            self.dense = base if dtype == torch.float16 else base.to(dtype)
+
+    def same_positions(self, idx: torch.Tensor) -> bool:
+        """Whether ``idx`` names the active positions this view was built for (the
+        same tensor, unmodified, or equal values)."""
+        if any(idx is t and idx._version == v for t, v in self._known):
+            return True
+        if idx.numel() != self.n_active:
+            return False
+        same = bool(torch.equal(idx.reshape(-1).to(device=self.active.device, dtype=torch.int64), self.active))
+        if same:
+            self._known = [(t, v) for t, v in self._known if t._version == v][-3:] + [(idx, idx._version)]
+        return same
+
+    def retired_after(self, new_idx: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(positions, values) of this view that ``new_idx`` does not name."""
+        new = new_idx.reshape(-1).to(device=self.positions.device, dtype=torch.int64)
+        keep = ~torch.isin(self.positions, new)
+        return self.positions[keep], self.values[keep]
+
+    def refresh(self, vals: torch.Tensor) -> None:
+        """New fp32 masters of the active positions (aligned with ``idx``)."""
+        if vals.numel() != self.n_active:
+            raise ValueError(f"overlay refresh needs {self.n_active} values, got {vals.numel()}")
+        self.values[:self.n_active].copy_(vals.reshape(-1))
+        if self.ov is not None:
+            self.ov.refresh(self.values)
+        else:
+            # dtype(fp16(master)): the fp16 value is exact in fp32
+            overlay_scatter(self.dense, self.positions, self.values.half().float())
 
 
 def overlay_scatter(base: torch.Tensor, idx: torch.Tensor, vals: torch.Tensor) -> None:

@@ -246,12 +246,14 @@ class SparseAdam:
         if self._count is not None:
             self._count.fill_(self._step)
             self._launched = self._step
+        # copied into the existing moment slices, so that tensors packed into one
+        # buffer (_pack_moments) keep their one-launch step after a resume
         for n, t in sd["m"].items():
             if n in self._m and t.numel() == self._m[n].numel():
-                self._m[n] = t.detach().to(self._m[n].device, torch.float32).clone()
+                self._m[n].copy_(t.detach().reshape(-1).to(self._m[n].device, torch.float32))
         for n, t in sd["v"].items():
             if n in self._v and t.numel() == self._v[n].numel():
-                self._v[n] = t.detach().to(self._v[n].device, torch.float32).clone()
+                self._v[n].copy_(t.detach().reshape(-1).to(self._v[n].device, torch.float32))
 
     @property
     def num_active_params(self) -> int:
@@ -287,16 +289,21 @@ class MomentumSGD:
                 p.grad.zero_()
 
     @torch.no_grad()
-    def step(self, finite: torch.Tensor | None = None, halt: torch.Tensor | None = None) -> None:
+    def step(self, finite: torch.Tensor | None = None, halt: torch.Tensor | None = None,
+             loss_scale: "DeviceLossScale | None" = None) -> None:
         """One step.  ``finite`` / ``halt``: optional int32 GPU flags read by the
         kernel, which skips the update unless finite[0] != 0 and halt[0] == 0 --
         the trainer's finite gate (train.py:649-672) decided on the device, so
         the step can be launched before the host has read the flag.  A tensor's
         first step (which creates its momentum buffer, as torch does) reads the
-        gate on the host instead."""
+        gate on the host instead.  ``loss_scale``: the gradients carry that
+        device loss scale and are divided by loss_scale * ACCUM (rounded to the
+        dtype) before the update, as train.py:669-670 does on the host."""
         for t, what in ((finite, "finite"), (halt, "halt")):
             if t is not None and (not t.is_cuda or t.dtype != torch.int32 or t.numel() < 1):
                 raise TypeError(f"MomentumSGD: {what} must be an int32 GPU tensor")
+        scale_ptr = None if loss_scale is None else loss_scale.state.data_ptr()
+        accum = 1.0 if loss_scale is None else float(loss_scale.accum)
         for i, p in enumerate(self.params):
             g = p.grad
             if g is None:
@@ -318,4 +325,90 @@ class MomentumSGD:
                 gate_h = halt.data_ptr() if halt is not None else None
             N.call("usaf_hip_sgd_momentum_step", p.data_ptr(), g.data_ptr(), buf.data_ptr(), p.numel(),
                    N.dtype_code(p.dtype), self.lr, self.momentum, self.weight_decay, 1 if first else 0,
-                   gate_f, gate_h, N.stream_ptr(p.device))
+                   gate_f, gate_h, scale_ptr, accum, N.stream_ptr(p.device))
+
+
+class DeviceLossScale:
+    """The trainer's dynamic loss scale with its state on the GPU.
+
+    train.py keeps ``loss_scale`` (LOSS_SCALE_INIT = 4096, :31), ``good_streak``
+    and ``n_skipped`` as host variables: the backward runs on ``loss *
+    loss_scale`` (:351-353); the compact gradients and the router gradient are
+    divided by ``loss_scale * ACCUM`` (:661, :669-670); a finite step counts as
+    good and every SCALE_UP_EVERY-th (200) good step doubles the scale, capped at
+    65536 (:673-674); a skipped step halves it, floored at 64 (:676).  Here the
+    three live in one int32[4] device buffer (``state``: scale as fp32 bits,
+    good steps, skipped steps), so a loop that launches step n + 1 before it
+    reads step n's finite flag keeps the same schedule:
+
+    * ``scale_grad(g)``: g * loss_scale in g's dtype (the scaled loss's gradient
+      seed, usaf_hip_loss_scale_apply);
+    * ``unscale_check(flat, out, finite)``: out = flat / (loss_scale * ACCUM) and
+      finite[0] = 0 if any result is not finite (usaf_hip_scale_check_state);
+    * ``MomentumSGD.step(..., loss_scale=self)``: the router gradient divided the same way;
+    * ``update(finite, halt)``: the schedule for that step, launched after the
+      step's gated updates (usaf_hip_loss_scale_update).
+    """
+
+    def __init__(self, init_scale: float = 4096.0, scale_up_every: int = 200, min_scale: float = 64.0,
+                 max_scale: float = 65536.0, accum: int = 1, device=None):
+        dev = torch.device(device) if device is not None else N.default_device()
+        if scale_up_every < 1 or not (0 < min_scale <= max_scale) or accum < 1:
+            raise ValueError("DeviceLossScale: need scale_up_every >= 1, 0 < min_scale <= max_scale, accum >= 1")
+        self.scale_up_every, self.min_scale, self.max_scale = int(scale_up_every), float(min_scale), float(max_scale)
+        self.accum = int(accum)
+        self.state = torch.zeros(4, dtype=torch.int32, device=dev)
+        self.state[:1].view(torch.float32).fill_(float(init_scale))
+
+    @property
+    def device(self) -> torch.device:
+        return self.state.device
+
+    def scale_grad(self, g: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """g * loss_scale in g's dtype (fp16 / bf16); ``out`` may be g itself."""
+        if g.dtype not in (torch.float16, torch.bfloat16) or not g.is_contiguous() or g.device != self.device:
+            raise TypeError("DeviceLossScale.scale_grad: contiguous fp16/bf16 tensor on the scale's device")
+        out = torch.empty_like(g) if out is None else out
+        if out.shape != g.shape or out.dtype != g.dtype or not out.is_contiguous():
+            raise ValueError("DeviceLossScale.scale_grad: out must match g")
+        N.call("usaf_hip_loss_scale_apply", g.data_ptr(), out.data_ptr(), g.numel(), N.dtype_code(g.dtype),
+               self.state.data_ptr(), N.stream_ptr(self.device))
+        return out
+
+    def unscale_check(self, flat: torch.Tensor, out: torch.Tensor, finite: torch.Tensor) -> None:
+        """out = flat / (loss_scale * ACCUM); finite[0] = 0 if any result is inf/NaN
+        (the caller sets finite[0] = 1 beforehand)."""
+        for t in (flat, out):
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.device != self.device:
+                raise TypeError("DeviceLossScale.unscale_check: contiguous fp32 tensors on the scale's device")
+        if out.numel() != flat.numel() or finite.dtype != torch.int32 or not finite.is_cuda:
+            raise ValueError("DeviceLossScale.unscale_check: out must match flat; finite is an int32 GPU flag")
+        N.call("usaf_hip_scale_check_state", flat.data_ptr(), out.data_ptr(), flat.numel(), self.state.data_ptr(),
+               float(self.accum), finite.data_ptr(), N.stream_ptr(self.device))
+
+    def update(self, finite: torch.Tensor | None = None, halt: torch.Tensor | None = None) -> None:
+        """The schedule for the step whose flag is finite[0] (None = finite); a
+        halted step (halt[0] != 0) leaves the state unchanged."""
+        N.call("usaf_hip_loss_scale_update", self.state.data_ptr(), N.ptr(finite), N.ptr(halt),
+               self.scale_up_every, self.min_scale, self.max_scale, N.stream_ptr(self.device))
+
+    @property
+    def loss_scale(self) -> float:
+        """The current scale (a host read)."""
+        return float(self.state[:1].view(torch.float32).item())
+
+    @property
+    def good_streak(self) -> int:
+        return int(self.state[1].item())
+
+    @property
+    def n_skipped(self) -> int:
+        return int(self.state[2].item())
+
+    def state_dict(self) -> dict:
+        return {"loss_scale": self.loss_scale, "good_streak": self.good_streak, "n_skipped": self.n_skipped}
+
+    def load_state_dict(self, sd: dict) -> None:
+        host = torch.tensor([0, int(sd["good_streak"]), int(sd["n_skipped"]), 0], dtype=torch.int32)
+        host[:1].view(torch.float32).fill_(float(sd["loss_scale"]))
+        self.state.copy_(host)
