@@ -89,6 +89,25 @@ def bench_dequant(dev, steps: int, warmup: int, out_dtype=torch.bfloat16) -> dic
                 out_dtype=str(out_dtype).replace("torch.", ""))
 
 
+def host_cpu() -> dict:
+    """The host the CPU baselines ran on: CPU model (lscpu's "Model name", from
+    /proc/cpuinfo), logical CPUs (nproc) and the threads torch used."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count()
+    return {"cpu_model": model, "nproc": nproc, "torch_threads": torch.get_num_threads()}
+
+
 def cpu_baseline_dequant(max_seconds: float = 20.0) -> dict:
     """The reference's CPU dequant op sequence (oracle/codec_torch.py, torch CPU,
     all host cores) on a bounded sample: 16 of 128 experts of the layer."""
@@ -113,7 +132,7 @@ def cpu_baseline_dequant(max_seconds: float = 20.0) -> dict:
         if dt > max_seconds or reps >= 50:
             break
     gbs = reps * elems * DEQUANT_BYTES_PER_ELEM / dt / 1e9
-    return dict(value=round(gbs, 3), unit="GB/s", cores=threads, kind="port",
+    return dict(value=round(gbs, 3), unit="GB/s", cores=threads, kind="port", host=host_cpu(),
                 sample=f"torch-CPU restatement of quantization.py:107-132 on 16 of 128 experts of one Qwen3 "
                        f"MoE layer ({elems:,} elements) x {reps} reps, {dt:.1f} s, fp16 output")
 
@@ -571,12 +590,13 @@ def cpu_baseline_mixtral(max_seconds: float = 15.0) -> dict:
         dt = time.perf_counter() - t0
         if dt > max_seconds or reps >= 10:
             break
-    return dict(value=round(reps * T / dt, 2), unit="tokens/s", cores=threads, kind="port",
+    return dict(value=round(reps * T / dt, 2), unit="tokens/s", cores=threads, kind="port", host=host_cpu(),
                 sample=f"routed per-expert loop (torch CPU bf16 autograd: fwd + grad-input + dense expert weight "
                        f"grads) at the Mixtral shape on {T} of the 8192 tokens, x{reps} reps in {dt:.1f} s")
 
 
-CFG4 = dict(L=48, E=128, H=2048, I=768, k=8, T=2048, cap_bytes=64 * 10 ** 9, zipf=1.1)
+CFG4 = dict(L=48, E=128, H=2048, I=768, k=8, T=2048, cap_bytes=64 * 10 ** 9, small_cap_bytes=32 * 10 ** 9,
+            zipf=1.1)
 
 
 def zipf_router_logits(T, E, rank_of, s, gen):
@@ -589,17 +609,21 @@ def zipf_router_logits(T, E, rank_of, s, gen):
 
 def bench_cache_stress(dev, microbatches: int = 6) -> dict:
     """48 Qwen3-MoE-shaped layers of 4-bit experts resident in HBM
-    (15.4 GB), a per-expert LRU of dequantized bf16 copies in a slot arena capped
-    at 64 GB, Zipf(1.1) expert popularity per layer, 2048-token microbatches
-    through the 48 layers (routing, cache lookup and fill, arena GEMMs,
-    combine, residual add).  The first microbatch starts from an empty cache
-    (cold fill: every expert dequantized once); the later ones hit only.  The
-    same microbatches also run through the fused 4-bit GEMMs, which need no
-    copies at all."""
+    (15.4 GB), a per-expert LRU of dequantized fp16 copies in a slot arena,
+    Zipf(1.1) expert popularity per layer, fp16 2048-token microbatches
+    through the 48 layers (routing, one host read of the per-expert counts,
+    on-demand fill of the selected experts that are missing, arena GEMMs,
+    combine, residual add).
+    * cap 64 GB (every expert of the model fits): the first microbatch starts
+      from an empty cache (cold fill), the later ones hit only;
+    * cap 32 GB (about half the working set): the LRU evicts, and an access
+      pattern that sweeps the layers in order refills what it evicted;
+    * the same microbatches on the fused 4-bit GEMMs, which need no copies."""
     from usaf_amd import moe as G
     from usaf_amd.expert_cache import ExpertSlotCache
     c = CFG4
     L, E, H, I, k, T = c["L"], c["E"], c["H"], c["I"], c["k"], c["T"]
+    dt = torch.float16
     gen = torch.Generator(device=dev).manual_seed(4848)
     layers, ranks = {}, {}
     for li in range(L):
@@ -612,16 +636,16 @@ def bench_cache_stress(dev, microbatches: int = 6) -> dict:
         layers[name] = G.ExpertWeights(*qs)
         ranks[name] = torch.randperm(E, device=dev, generator=gen) + 1
     q4_bytes = sum(ew.gate_up.nbytes() + ew.down.nbytes() for ew in layers.values())
-    cache = ExpertSlotCache(layers, dev, max_bytes=c["cap_bytes"], dtype=torch.bfloat16)
     names = list(layers)
     logits = [[zipf_router_logits(T, E, ranks[n], c["zipf"], gen) for n in names] for _ in range(microbatches)]
-    hs0 = torch.randn(T, H, device=dev, generator=gen).bfloat16()
+    hs0 = torch.randn(T, H, device=dev, generator=gen).to(dt)
+    flop_per_mb = 2 * T * k * (H * 2 * I + I * H) * L
 
-    def run(mb, fused):
+    def run(mb, cache=None):
         x = hs0
         for li, name in enumerate(names):
-            w, _ = G.route_topk(logits[mb][li], k, False, torch.bfloat16, with_probs=False)
-            if fused:
+            w, _ = G.route_topk(logits[mb][li], k, False, dt, with_probs=False)
+            if cache is None:
                 y = G.routed_experts(x, w, layers[name], slot_capacity=T * (k + 1),
                                      overflow=torch.zeros(1, dtype=torch.int32, device=dev))
             else:
@@ -629,44 +653,50 @@ def bench_cache_stress(dev, microbatches: int = 6) -> dict:
             x = x + y
         return x
 
-    cache.dequant_events = []
-    with _Timer() as t:
-        run(0, fused=False)
-    cold_ms = t.ms
-    fill_ms = sum(a.elapsed_time(b) for a, b, _ in cache.dequant_events)
-    filled = sum(n for _, _, n in cache.dequant_events)
-    fill_bytes = cache.dequant_bytes
-    cache.dequant_events = None
-    h0, m0 = cache.hits, cache.misses
+    def rate(ms):
+        return {"ms_per_microbatch": round(ms, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                "tflops": round(flop_per_mb / (ms * 1e-3) / 1e12, 1)}
+
+    out = dict(workload="48 stacked Qwen3-30B-A3B MoE layers (configs[4]): 4-bit experts resident in HBM, per-expert "
+                        "LRU of fp16 copies filled on demand, Zipf(1.1) expert popularity, 2048-token fp16 "
+                        "microbatches, forward",
+               layers=L, q4_resident_gb=round(q4_bytes / 1e9, 2), microbatches=microbatches, dtype="fp16")
+    for key, cap in (("cap_64gb", c["cap_bytes"]), ("cap_32gb", c["small_cap_bytes"])):
+        cache = ExpertSlotCache(layers, dev, max_bytes=cap, dtype=dt)
+        cache.dequant_events = []
+        with _Timer() as t:
+            run(0, cache)
+        cold_ms = t.ms
+        fill_ms = sum(a.elapsed_time(b) for a, b, _ in cache.dequant_events)
+        filled = sum(n for _, _, n in cache.dequant_events)
+        fill_bytes = cache.dequant_bytes
+        cache.dequant_events = None
+        h0, m0, e0 = cache.hits, cache.misses, cache.evictions
+        with _Timer() as t:
+            for mb in range(1, microbatches):
+                run(mb, cache)
+        steady_ms = t.ms / (microbatches - 1)
+        hits, misses, evictions = cache.hits - h0, cache.misses - m0, cache.evictions - e0
+        fill_gbs = fill_bytes / (fill_ms * 1e-3) / 1e9 if fill_ms > 0 else None
+        out[key] = {"arena_slots": cache.n_slots, "arena_gb": round(cache.nbytes() / 1e9, 2),
+                    "cold_fill": dict(rate(cold_ms), experts_filled=filled, dequant_ms=round(fill_ms, 3),
+                                      dequant_roofline={"bound": "hbm",
+                                                        "achieved": None if fill_gbs is None else round(fill_gbs, 1),
+                                                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                        "frac": None if fill_gbs is None
+                                                        else round(fill_gbs / HBM_PEAK_GBS, 4),
+                                                        "bytes": fill_bytes}),
+                    "steady": dict(rate(steady_ms), hit_rate=round(hits / max(1, hits + misses), 4),
+                                   misses_per_microbatch=round(misses / (microbatches - 1), 1),
+                                   evictions_per_microbatch=round(evictions / (microbatches - 1), 1))}
+        del cache
+        torch.cuda.empty_cache()
+    run(0)
     with _Timer() as t:
         for mb in range(1, microbatches):
-            run(mb, fused=False)
-    steady_ms = t.ms / (microbatches - 1)
-    steady_hits, steady_misses = cache.hits - h0, cache.misses - m0
-    run(0, fused=True)
-    with _Timer() as t:
-        for mb in range(1, microbatches):
-            run(mb, fused=True)
-    fused_ms = t.ms / (microbatches - 1)
-    fill_gbs = fill_bytes / (fill_ms * 1e-3) / 1e9 if fill_ms > 0 else None
-    flop_per_mb = 2 * T * k * (H * 2 * I + I * H) * L
-    return dict(
-        workload="48 stacked Qwen3-30B-A3B MoE layers (configs[4]): 4-bit experts resident in HBM, per-expert LRU "
-                 "of bf16 copies capped at 64 GB, Zipf(1.1) expert popularity, 2048-token microbatches, forward",
-        layers=L, q4_resident_gb=round(q4_bytes / 1e9, 2), arena_slots=cache.n_slots,
-        arena_gb=round(cache.nbytes() / 1e9, 2), microbatches=microbatches,
-        cold_fill={"ms_per_microbatch": round(cold_ms, 3), "tokens_per_s": round(T / (cold_ms * 1e-3), 1),
-                   "experts_filled": filled, "dequant_ms": round(fill_ms, 3),
-                   "dequant_roofline": {"bound": "hbm", "achieved": None if fill_gbs is None else round(fill_gbs, 1),
-                                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                        "frac": None if fill_gbs is None else round(fill_gbs / HBM_PEAK_GBS, 4),
-                                        "bytes": fill_bytes}},
-        steady={"ms_per_microbatch": round(steady_ms, 3), "tokens_per_s": round(T / (steady_ms * 1e-3), 1),
-                "hit_rate": round(steady_hits / max(1, steady_hits + steady_misses), 4),
-                "tflops": round(flop_per_mb / (steady_ms * 1e-3) / 1e12, 1)},
-        fused_q4_no_copies={"ms_per_microbatch": round(fused_ms, 3), "tokens_per_s": round(T / (fused_ms * 1e-3), 1),
-                            "tflops": round(flop_per_mb / (fused_ms * 1e-3) / 1e12, 1)},
-        hits=cache.hits, misses=cache.misses, evictions=cache.evictions)
+            run(mb)
+    out["fused_q4_no_copies"] = rate(t.ms / (microbatches - 1))
+    return out
 
 
 def cpu_baseline_moe(max_seconds: float = 20.0) -> dict:
@@ -689,7 +719,7 @@ def cpu_baseline_moe(max_seconds: float = 20.0) -> dict:
         dt = time.perf_counter() - t0
         if dt > max_seconds or reps >= 20:
             break
-    return dict(value=round(reps * T / dt, 2), unit="tokens/s", cores=threads, kind="port",
+    return dict(value=round(reps * T / dt, 2), unit="tokens/s", cores=threads, kind="port", host=host_cpu(),
                 sample=f"routed per-expert loop (benchmarks/kaggle_t4_bench.py:253-282 restated, torch CPU bf16 "
                        f"autograd: fwd + grad-input + dense expert weight grads) on {T} of the 4096 tokens, "
                        f"x{reps} reps in {dt:.1f} s; the dense-masked reference path does 16x this work")
@@ -797,12 +827,16 @@ def main() -> int:
          f"{mx['step_tflops']:.1f} TFLOP/s algorithmic")
     for name, kv in mx["kernels"].items():
         _log(f"  {name}: {kv['ms']:.3f} ms, {kv['tflops']:.1f} TFLOP/s ({100 * kv['frac']:.1f} % of peak)")
-    _log("cache stress: configs[4], 48 layers, 64 GB per-expert LRU, Zipf(1.1), 2048-token microbatches")
+    _log("cache stress: configs[4], 48 layers, per-expert LRU of fp16 copies (64 GB, 32 GB), Zipf(1.1), "
+         "2048-token microbatches")
     cs = bench_cache_stress(dev)
-    _log(f"cache stress: cold fill {cs['cold_fill']['ms_per_microbatch']:.2f} ms/microbatch "
-         f"({cs['cold_fill']['experts_filled']} experts, dequant {cs['cold_fill']['dequant_roofline']['achieved']} GB/s), "
-         f"steady {cs['steady']['ms_per_microbatch']:.2f} ms ({cs['steady']['tokens_per_s']:.0f} tokens/s, hit rate "
-         f"{cs['steady']['hit_rate']}), fused 4-bit {cs['fused_q4_no_copies']['ms_per_microbatch']:.2f} ms")
+    for key in ("cap_64gb", "cap_32gb"):
+        v = cs[key]
+        _log(f"cache stress {key}: cold fill {v['cold_fill']['ms_per_microbatch']:.2f} ms/microbatch "
+             f"({v['cold_fill']['experts_filled']} experts, dequant {v['cold_fill']['dequant_roofline']['achieved']} "
+             f"GB/s), steady {v['steady']['ms_per_microbatch']:.2f} ms ({v['steady']['tokens_per_s']:.0f} tokens/s, "
+             f"hit rate {v['steady']['hit_rate']}, {v['steady']['evictions_per_microbatch']} evictions/microbatch)")
+    _log(f"cache stress: fused 4-bit, no copies {cs['fused_q4_no_copies']['ms_per_microbatch']:.2f} ms/microbatch")
     cpu = cpu_dq = None
     if not args.no_cpu_baseline:
         _log("cpu baseline: routed expert layer fwd+bwd sample")

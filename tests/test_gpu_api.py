@@ -394,6 +394,66 @@ def test_fused_overlay_dense_fallback_for_clustered_masks(gpu_device):
                        _bits(_scattered(base[names[0]], active[names[0]], masters[names[0]]).to(dt)))
 
 
+def test_streaming_slot_cache_serves_no_grad_forwards(gpu_device):
+    """setup_quantized_streaming(expert_cache_bytes=...): forwards that need no
+    gradients run on per-expert dequantized copies made on demand (the
+    reference's dequant-on-access cache, usaf/moe_loader.py:130-181); a forward
+    with gradients, or of a module with trained values, runs on the fused 4-bit
+    GEMMs.  Every path matches the oracle."""
+    _say("streaming with a per-expert copy cache: no-grad forwards on copies, grad / trained on the fused path")
+    from parity import check
+    dt = torch.bfloat16
+    model, block, experts_sd = _streaming_model(seed=31)
+    qd = quantize_state_dict(experts_sd, device=gpu_device)
+    E, H, I = 8, 256, 128
+    setup_quantized_streaming(model, qd, gpu_device, verbose=False, expert_cache_bytes=E * (3 * H * I) * 2)
+    cache = get_quantized_cache(model)
+    sc = cache.slot_cache
+    assert sc is not None and sc.n_slots == E and sc.dtype == dt
+    names = [f"model.layers.0.mlp.experts.{l}" for l in ("gate_up_proj", "down_proj")]
+    base = {n: _oracle_dequant(qd[n]) for n in names}
+    g = torch.Generator().manual_seed(32)
+    hs = torch.randn(1, 96, H, generator=g).to(dt)
+    wr = block.gate.weight.detach().cpu()
+    ref = _reference_block(hs, wr, base[names[0]].to(dt), base[names[1]].to(dt), 2, True)
+    with torch.no_grad():
+        out = model.model.layers[0].mlp(hs.to(gpu_device))
+    torch.cuda.synchronize()
+    check("no-grad forward on the copies", out, ref, dt)
+    used = int(sc.misses)
+    assert used > 0 and sc.hits == 0
+    with torch.no_grad():
+        model.model.layers[0].mlp(hs.to(gpu_device))
+    assert sc.hits == used and sc.misses == used  # the same experts again: hits only
+    x = hs.to(gpu_device).requires_grad_(True)
+    out_g = model.model.layers[0].mlp(x)
+    torch.cuda.synchronize()
+    assert sc.hits == used and sc.misses == used, "a forward with gradients must not use the copies"
+    check("grad forward on the fused path", out_g, ref, dt)
+    # trained values: the module leaves the copies for the fused path with overlays
+    active, masters = {}, {}
+    for n in names:
+        numel = base[n].numel()
+        idx = torch.randperm(numel, generator=g)[: numel // 200].sort().values
+        active[n] = idx.to(gpu_device)
+        masters[n] = torch.nn.Parameter((base[n].reshape(-1)[idx].float() + 0.05).to(gpu_device),
+                                        requires_grad=False)
+        cache.overlays[n] = (active[n], masters[n])
+    w_eff = {}
+    for n in names:
+        w = base[n].clone()
+        w.reshape(-1)[active[n].cpu()] = masters[n].detach().cpu().half()
+        w_eff[n] = w.to(dt)
+    ref_t = _reference_block(hs, wr, w_eff[names[0]], w_eff[names[1]], 2, True)
+    with torch.no_grad():
+        out_t = model.model.layers[0].mlp(hs.to(gpu_device))
+    torch.cuda.synchronize()
+    assert sc.hits == used and sc.misses == used
+    check("no-grad forward with trained values (fused)", out_t, ref_t, dt)
+    cache.free_frozen(0)
+    assert not sc.layers and not sc.cached_keys
+
+
 def _tiny_olmoe(E=8, H=256, I=128, k=2, seed=0, norm=False):
     from transformers import OlmoeConfig
     from transformers.models.olmoe.modeling_olmoe import OlmoeSparseMoeBlock

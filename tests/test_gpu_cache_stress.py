@@ -5,7 +5,8 @@ usaf/moe_loader.py:130-181).
 
 Checks, after every layer forward of every microbatch:
 * the cached keys and their LRU order equal the reference policy's
-  (oracle/cache.py LRUModel) fed the same accesses;
+  (oracle/cache.py LRUModel) fed the same accesses: the experts the routing
+  selected, in ascending order (copies are made on demand);
 * sampled cached copies are bit-exact with the C oracle's dequant of that
   expert's 4-bit slices;
 * the layer's output from the arena GEMMs is within the bf16 bar of the
@@ -20,6 +21,8 @@ from oracle import moe as M
 from oracle.cache import LRUModel
 from usaf_amd import moe as G
 from usaf_amd.expert_cache import ExpertSlotCache
+
+from parity import check
 
 pytestmark = pytest.mark.gpu
 
@@ -68,13 +71,11 @@ def test_slot_cache_lru_copies_and_forward(gpu_device):
             w, _, _ = M.route(_zipf_logits(T, E, perms[name], 1.1, g), k, False, dt)
             out = cache.forward(name, x.to(gpu_device), w.to(gpu_device), k)
             torch.cuda.synchronize()
-            assert not cache.overflowed()
-            for e in range(E):
+            for e in (w != 0).any(0).nonzero().reshape(-1).tolist():
                 model.access((name, e))
             assert cache.cached_keys == model.keys(), f"LRU order differs after mb {mb} layer {li}"
             ref = M.experts_routed(x, w, deq[name][0], deq[name][1])
-            rel = float((out.float().cpu() - ref.float()).abs().max() / ref.float().abs().max())
-            assert rel <= 1e-2, f"mb {mb} layer {li}: rel {rel:.3e}"
+            check(f"mb {mb} layer {li} out", out, ref, dt, say=_say)
             # sampled copies, bit for bit
             keys = cache.cached_keys
             for j in torch.randint(0, len(keys), (3,), generator=g).tolist():
@@ -93,3 +94,51 @@ def test_slot_cache_refuses_arena_below_one_layer(gpu_device):
     d = G.Q4Tensor.quantize((torch.randn(E, H, I) * 0.02).half().to(gpu_device))
     with pytest.raises(ValueError):
         ExpertSlotCache({"l0": G.ExpertWeights(q, d)}, gpu_device, max_bytes=(2 * I * H + H * I) * 2 * (E - 1))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_slot_cache_qwen3_layer_shape(gpu_device, dt):
+    """configs[4] at the Qwen3-30B-A3B layer shape (E=128, H=2048, I=768): two
+    layers, an arena of 200 expert slots against a working set of up to 256,
+    Zipf(1.1) routing (T=512 tokens still select every expert of a layer), the
+    layers visited in an order with repeats -- hits and evictions -- with the
+    LRU order, sampled copies and each layer output checked."""
+    L, E, H, I, T, k = 2, 128, 2048, 768, 512, 8
+    _say(f"slot cache at the Qwen3 layer shape: {L} layers x {E} experts, 200 slots, T={T} k={k}, {dt}")
+    torch.set_num_threads(16)
+    from oracle.codec_torch import dequant_opseq
+    g = torch.Generator().manual_seed(4848)
+    layers, deq, perms = {}, {}, {}
+    for li in range(L):
+        name = f"model.layers.{li}.mlp.experts"
+        qs = [G.Q4Tensor.quantize((torch.randn(shp, generator=g) * 0.02).half().to(gpu_device))
+              for shp in ((E, 2 * I, H), (E, H, I))]
+        layers[name] = G.ExpertWeights(*qs)
+        # the reference's CPU dequant of the same codes (fp16), in the cache dtype
+        deq[name] = tuple(dequant_opseq(q.q.cpu(), q.s.cpu(), q.z.cpu(), q.shape).to(dt) for q in qs)
+        perms[name] = torch.randperm(E, generator=g)
+    slot_bytes = (2 * I * H + H * I) * 2
+    cache = ExpertSlotCache(layers, gpu_device, max_bytes=200 * slot_bytes, dtype=dt)
+    assert cache.n_slots == 200
+    model = LRUModel(200)
+    x = torch.randn(T, H, generator=g).to(dt)
+    for mb, li in enumerate((0, 0, 1, 0, 1, 1)):
+        if True:
+            name = f"model.layers.{li}.mlp.experts"
+            w, _, _ = M.route(_zipf_logits(T, E, perms[name], 1.1, g), k, False, dt)
+            out = cache.forward(name, x.to(gpu_device), w.to(gpu_device), k)
+            torch.cuda.synchronize()
+            used = (w != 0).any(0).nonzero().reshape(-1).tolist()
+            for e in used:
+                model.access((name, e))
+            assert cache.cached_keys == model.keys(), f"LRU order differs after mb {mb} layer {li}"
+            ref = M.experts_routed(x, w, deq[name][0], deq[name][1])
+            check(f"mb {mb} layer {li} out ({len(used)} experts used)", out, ref, dt, say=_say)
+            keys = cache.cached_keys
+            for j in torch.randint(0, len(keys), (4,), generator=g).tolist():
+                lname, e = keys[j]
+                s = cache.slot_of(lname, e)
+                assert torch.equal(cache.gu_arena[s].cpu().view(torch.int16), deq[lname][0][e].view(torch.int16))
+                assert torch.equal(cache.dn_arena[s].cpu().view(torch.int16), deq[lname][1][e].view(torch.int16))
+    assert cache.evictions > 0 and cache.hits > 0
+    _say(f"  hits {cache.hits}, misses {cache.misses}, evictions {cache.evictions}")

@@ -14,13 +14,20 @@ layers of Qwen3-30B-A3B) and the copies are per expert:
   recent end, a miss takes a free slot or evicts the least recently used key
   -- and fills every missed slot with one batched dequant launch per tensor
   (usaf_hip_dequant_q4_slices), reading the 4-bit slices from HBM;
+* ``forward`` buckets the tokens first and touches only the experts the
+  routing selected (one host read of the per-expert counts): a copy is made
+  on demand, when an expert is used and missing, as the reference dequantizes
+  a module when its forward asks for it (usaf/moe_loader.py:130-181);
 * the layer's slot table (int32 [E] on the device) then feeds the arena
   GEMMs (usaf_hip_moe_gate_up_fwd_slots / _down_fwd_slots), so no expert is
   ever copied into a contiguous [E, ...] tensor.
 
-A layer's experts must fit the arena together (n_slots >= E), so a touch never
-evicts a key it inserted itself.  Slot tables of layers that lost experts to
-eviction are refreshed by their next touch, which every forward starts with.
+Copies hold the reference's fp16 dequantized values (dtype fp16, the default,
+with fp16 activations) or their bf16 rounding (dtype bf16, for bf16
+activations: the MFMA operands of one product share a type).  A layer's
+experts must fit the arena together (n_slots >= E), so a touch never evicts a
+key it inserted itself.  Slot tables of layers that lost experts to eviction
+are refreshed by their next touch, which every forward starts with.
 """
 from __future__ import annotations
 
@@ -35,7 +42,7 @@ from .moe import ExpertWeights, Q4Tensor, bucket_by_expert, combine
 
 class ExpertSlotCache:
     def __init__(self, layers: Dict[str, ExpertWeights], device, max_bytes: int,
-                 dtype: torch.dtype = torch.bfloat16) -> None:
+                 dtype: torch.dtype = torch.float16) -> None:
         if not layers:
             raise ValueError("ExpertSlotCache needs at least one layer")
         self.device = torch.device(device)
@@ -81,6 +88,15 @@ class ExpertSlotCache:
 
     def nbytes(self) -> int:
         return self.n_slots * self.slot_bytes
+
+    def drop_layer(self, layer: str) -> None:
+        """Forget a layer (its 4-bit weights are being freed): its copies' slots
+        return to the free list."""
+        if layer not in self.layers:
+            return
+        for key in [k for k in self._lru if k[0] == layer]:
+            self._free.append(self._lru.pop(key))
+        del self.layers[layer], self._host_tables[layer], self._tables[layer]
 
     def touch(self, layer: str, experts: Optional[Iterable[int]] = None) -> torch.Tensor:
         """Mark ``experts`` (default: all of the layer's) used, in order; dequantize
@@ -138,15 +154,29 @@ class ExpertSlotCache:
 
     # ---- forward --------------------------------------------------------------------
 
-    def forward(self, layer: str, hs: torch.Tensor, weights: torch.Tensor, top_k: int) -> torch.Tensor:
+    def forward(self, layer: str, hs: torch.Tensor, weights: torch.Tensor,
+                top_k: Optional[int] = None) -> torch.Tensor:
         """The routed experts of ``layer`` (qwen3moe_dml.py:24-64, forward only) on
-        the cached copies: hs [T, H] and routing weights [T, E] in the cache dtype."""
+        the cached copies: hs [T, H] and routing weights [T, E] in the cache dtype.
+        Only the experts the routing selected are touched (and filled when
+        missing), in ascending expert order.  ``top_k`` sizes the slot buffers
+        for T * (top_k + 1) routed pairs without a host read of the slot count
+        (bucket_by_expert's capacity mode); a routing beyond that, or no
+        ``top_k``, buckets exactly."""
         if hs.dtype != self.dtype or weights.dtype != self.dtype:
             raise TypeError("activations and routing weights must be in the cache dtype")
         T = hs.shape[0]
-        table = self.touch(layer)
-        overflow = torch.zeros(1, dtype=torch.int32, device=self.device)
-        b = bucket_by_expert(weights, T * min(top_k + 1, self.E), overflow)
+        if top_k is not None:
+            cap = T * min(top_k + 1, self.E)
+            overflow = torch.zeros(1, dtype=torch.int32, device=self.device)
+            b = bucket_by_expert(weights, cap, overflow)
+            counts = b.counts.cpu()  # the one host read: which experts the routing selected
+            if int(counts.sum()) > cap:
+                b = bucket_by_expert(weights)
+        else:
+            b = bucket_by_expert(weights)
+            counts = b.counts.cpu()
+        table = self.touch(layer, counts.nonzero().reshape(-1).tolist())
         S = b.n_slots
         st = N.stream_ptr(self.device)
         code = N.dtype_code(self.dtype)
@@ -158,15 +188,7 @@ class ExpertSlotCache:
                code, gu.data_ptr(), act.data_ptr(), st)
         N.call("usaf_hip_moe_down_fwd_slots", act.data_ptr(), self.I, b.offsets.data_ptr(), S, self.E, self.H,
                self.dn_arena.data_ptr(), table.data_ptr(), self.n_slots, code, y.data_ptr(), st)
-        out = combine(y, weights, b.pair_slot, self.dtype)
-        self._overflow = overflow
-        return out
-
-    def overflowed(self) -> bool:
-        """Whether the last forward's routing exceeded its static slot capacity
-        (T * (top_k + 1) pairs; then its output is incomplete)."""
-        ov = getattr(self, "_overflow", None)
-        return bool(ov is not None and int(ov.item()))
+        return combine(y, weights, b.pair_slot, self.dtype)
 
 
 def q4_expert_slice(q: Q4Tensor, expert: int, dtype: torch.dtype) -> torch.Tensor:

@@ -23,7 +23,8 @@ import torch.nn as nn
 
 from . import _native as N
 from .importance import TopKImportanceStore  # noqa: F401  (moe_loader.py:584-631, GPU selection)
-from .moe import OverlayTooDense, Q4Overlay, Q4Tensor, timed_call
+from .expert_cache import ExpertSlotCache
+from .moe import ExpertWeights, OverlayTooDense, Q4Overlay, Q4Tensor, timed_call
 from .olmoe_streaming import _record_grad, apply_captured_expert_grads  # noqa: F401  (moe_loader.py:778-802)
 from .quantization import dequantize_4bit
 
@@ -105,6 +106,9 @@ class QuantizedExpertCache:
         # built from ``overlays`` / sync_resident for this activation dtype
         self.fused_overlays: Dict[str, "FusedOverlay"] = {}
         self.fused_dtype: Optional[torch.dtype] = None
+        # optional per-expert LRU of dequantized copies (make_slot_cache), used by
+        # forwards that need no gradients through layers without trained values
+        self.slot_cache: Optional[ExpertSlotCache] = None
         self.hits = 0
         self.misses = 0
 
@@ -228,6 +232,26 @@ class QuantizedExpertCache:
             name = f"model.layers.{li}.mlp.experts"
             self._expert_to_params.pop(name, None)
             self._prefetched.pop(name, None)
+            if self.slot_cache is not None:
+                self.slot_cache.drop_layer(name)
+
+    def make_slot_cache(self, max_bytes: int, dtype: Optional[torch.dtype] = None) -> ExpertSlotCache:
+        """A per-expert LRU of dequantized copies in one HBM arena of ``max_bytes``
+        (ExpertSlotCache) over every module whose gate_up/down are 4-bit: the
+        reference's dequant-on-demand cache at expert granularity, copies made
+        when the routing first selects a missing expert.  ``dtype``: of the
+        copies, the activation dtype of the forwards it serves (default the
+        fused path's, else fp16)."""
+        layers = {}
+        for name in self._expert_to_params:
+            gu, dn = self._q_dict.get(f"{name}.gate_up_proj"), self._q_dict.get(f"{name}.down_proj")
+            if isinstance(gu, Q4Tensor) and isinstance(dn, Q4Tensor) and gu.fused_ok() and dn.fused_ok():
+                layers[name] = ExpertWeights(gu, dn)
+        if not layers:
+            raise ValueError("make_slot_cache: no module holds 4-bit gate_up_proj and down_proj")
+        dt = dtype or self.fused_dtype or torch.float16
+        self.slot_cache = ExpertSlotCache(layers, self._device, max_bytes, dtype=dt)
+        return self.slot_cache
 
     def make_resident(self, train_layers, dequant_batch: int = 8, only_params=None) -> None:
         """moe_loader.py:263-299: dequantize trainable layers once into HBM fp16."""
@@ -615,14 +639,19 @@ class SparseGradStore:
 def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], device: torch.device, *,
                               max_cached_experts: int = 2, group_size: int = 128,
                               expert_pattern: str = "*.mlp.experts", verbose: bool = True,
-                              fused: bool = True) -> nn.Module:
+                              fused: bool = True, expert_cache_bytes: Optional[int] = None) -> nn.Module:
     """moe_loader.py:650-769.  The expert modules lose their Parameters (their
     weights live in the cache's HBM 4-bit store); everything else moves to the
     GPU in place.  Each expert module gets a pre-hook that attaches its HBM 4-bit
     tensors (``module._usaf_q4``, read by the fused forward) -- or, with
     ``fused=False``, dequantized fp16 Parameters from the LRU as the reference
     does, their gradients captured into ``model._expert_grads`` -- and a
-    post-hook that detaches them again."""
+    post-hook that detaches them again.  ``expert_cache_bytes`` (fused path):
+    also keep a per-expert LRU of dequantized copies of that size
+    (QuantizedExpertCache.make_slot_cache, attached as ``module._usaf_slots``);
+    the patched experts forward runs on the copies when it needs no gradients
+    and the module has no trained values, and on the fused 4-bit GEMMs
+    otherwise."""
     cache = QuantizedExpertCache(quantized_dict, device=device, max_cached=max_cached_experts,
                                  group_size=group_size)
     expert_names = [name for name, _ in model.named_modules() if fnmatch.fnmatch(name, expert_pattern)]
@@ -644,12 +673,20 @@ def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], 
         dtypes = {p.dtype for p in resident if p.is_floating_point()}
         act = torch.bfloat16 if torch.bfloat16 in dtypes else torch.float16
         cache.fused_dtype = act  # the overlay tables hold trained values in the activation dtype
+        if expert_cache_bytes:
+            cache.make_slot_cache(int(expert_cache_bytes), act)
 
     def attach(mod_name: str):
         def pre_hook(module: nn.Module, _args) -> None:
             if fused:
                 module._usaf_q4 = cache.get_q4(mod_name)
                 module._usaf_q4_overlays = cache.get_q4_overlays(mod_name)
+                # the copies hold the plain 4-bit values: modules with trained values
+                # (overlay tables or a dense fallback) stay on the fused path
+                sc = cache.slot_cache
+                trained = any(n in cache.fused_overlays for n, _ in cache._expert_to_params.get(mod_name, []))
+                module._usaf_slots = (sc, mod_name) if sc is not None and mod_name in sc.layers and not trained \
+                    else None
             else:
                 for pname, param in cache.get_expert_weights(mod_name).items():
                     module._parameters[pname] = param
@@ -663,6 +700,7 @@ def setup_quantized_streaming(model: nn.Module, quantized_dict: Dict[str, Any], 
         module._parameters.clear()
         module._usaf_q4 = None
         module._usaf_q4_overlays = None
+        module._usaf_slots = None
         state["resident"] -= 1
         return output
 

@@ -46,11 +46,29 @@ def _expert_weights(module) -> ExpertWeights:
     return ExpertWeights(gu.detach(), dn.detach())
 
 
+def _slot_cache_of(module, hidden_states: torch.Tensor, weights: torch.Tensor, capture):
+    """The per-expert copy cache for this forward, if it may serve it: no
+    gradient is wanted, the module carries no trained values (their masters
+    change every step; the fused GEMMs read them through overlay tables) and
+    the activations are in the copies' dtype."""
+    slots = getattr(module, "_usaf_slots", None)
+    if slots is None or capture is not None or getattr(module, "_usaf_q4_overlays", None):
+        return None
+    if torch.is_grad_enabled() and (hidden_states.requires_grad or weights.requires_grad):
+        return None
+    cache, name = slots
+    return slots if hidden_states.dtype == cache.dtype else None
+
+
 def dml_qwen3_experts_forward(self, hidden_states: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
     """qwen3moe_dml.py:24-64: [N, H] x routing weights [N, E] -> [N, H]."""
     capture = None
     if torch.is_grad_enabled() and getattr(self, "_grad_capture", None) is not None:
         capture = self._grad_capture
+    slots = _slot_cache_of(self, hidden_states, weights, capture)
+    if slots is not None:
+        cache, name = slots
+        return cache.forward(name, hidden_states.contiguous(), weights.to(cache.dtype).contiguous())
     return routed_experts(hidden_states, weights, _expert_weights(self), capture)
 
 
