@@ -249,6 +249,21 @@ def test_experts_forward_cfg1(gpu_device):
     check("cfg1 out", out, ref, dt, say=_say)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_experts_forward_dense_weights_cfg1(gpu_device, dt):
+    """Dense 16-bit expert weights (the copies of the per-expert cache, the dense
+    fallback of over-dense overlays) on the LDS-DMA kernel's dense-weight
+    variant, at the full Qwen3 layer shape against the oracle's routed loop on
+    the same weights."""
+    _say(f"experts fwd cfg1 with dense {dt} weights: T=4096 H=2048 I=768 E=128 k=8")
+    L = make_layer(gpu_device, 128, 2048, 768, 4096, 8, dt, seed=13, dense=True)
+    out = G.routed_experts(L["hs"].to(gpu_device), L["w"].to(gpu_device), L["ew"])
+    torch.cuda.synchronize()
+    torch.set_num_threads(16)
+    ref = M.experts_routed(L["hs"], L["w"], L["deq_g"], L["deq_d"])
+    check("cfg1 out, dense weights", out, ref, dt, say=_say)
+
+
 def test_experts_forward_mixtral_shape(gpu_device):
     _say("experts fwd cfg3 Mixtral shapes E=8 H=4096 I=14336 k=2 (T=192) bf16 q4")
     dt = torch.bfloat16

@@ -1230,7 +1230,20 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off), "s"(base) : "m0");
 }
+// dma4 for a base that may come straight out of readfirstlane: 5 wait states
+// between that VALU write of the SGPRs and the DMA reading them (s_mov + s_nop 3)
+__device__ __forceinline__ void dma4_vb(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 3\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off), "s"(base) : "m0");
+}
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// A wave-uniform 64-bit pointer in scalar registers: each 32-bit half passes
+// readfirstlane as an unsigned word and the halves are joined zero-extended.
+__device__ __forceinline__ const uint8_t* uni_ptr(const uint8_t* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return reinterpret_cast<const uint8_t*>((uintptr_t)(((uint64_t)hi << 32) | (uint64_t)lo));
+}
 
 constexpr int Q_MTE_CAP = 1024;  // m-tiles covered by the m-tile -> expert table
 
@@ -1253,8 +1266,17 @@ struct QTile {
 // SwiGLU forward: wave w holds gate rows n = 16 w + [0, 16) of the n-tile as
 // its rows 0-15 and the up rows I + n as rows 16-31, so accumulator registers
 // r and r + 8 of a lane are gate and up of the same column and slot.
-template <int EPI, int DT, bool BT, bool OVL>
+// DW: dense 16-bit weights of the activation dtype instead of codes (the
+// dequantized copies of the per-expert cache, expert e's [w_rows, w_cols]
+// matrix at block weight_block(e) of w16).  Each weight element feeds exactly
+// one lane, so the weights skip LDS: a lane loads its four fragment registers
+// of k-step gs + 1 straight from global memory during k-step gs (one 16-byte
+// load each), and the code stream's DMA slot instead touches the wave's
+// weight lines of k-step gs + 3 (4 bytes per lane into a scratch word), which
+// brings them into the cache hierarchy ahead of the register loads.
+template <int EPI, int DT, bool BT, bool OVL, bool DW = false>
 __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g) {
+  static_assert(!DW || (!BT && !OVL && EPI != EPI_SWIGLU_BWD), "dense weights: forward GEMMs without overlays");
   extern __shared__ __attribute__((aligned(16))) uint8_t qsm[];
   __shared__ __attribute__((aligned(16))) uint16_t q_ep[Q_WAVES * Q_EP_ELEMS];
   __shared__ uint8_t q_mte[Q_MTE_CAP];  // expert of m-tile mt (when the list fits)
@@ -1347,7 +1369,20 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   uint32_t o_off = 0;             // OVL: byte offset of this lane's entry word at k-step 0 of the code stream's tile
   const int a_lc = (tid & 7) ^ q_swz(tid >> 3);  // logical chunk of this thread's DMA slot
   const uint32_t lda_b = (uint32_t)g.lda * 2;
+  // DW: expert blocks of the dense weight; within one block the offsets are 32-bit
+  const uint64_t w_blk_bytes = (uint64_t)g.w_rows * (uint64_t)g.w_cols * 2u;
+  auto w_block_base = [&](const QTile& t) -> const uint8_t* {
+    const uint32_t blk = (uint32_t)uni((int)weight_block(g, t.e));  // clamped to [0, n_slots)
+    return reinterpret_cast<const uint8_t*>(g.w16) + (uint64_t)blk * w_blk_bytes;
+  };
+  const uint8_t* c_wbase = nullptr;  // DW: weight block of the code stream's tile
   auto c_setup = [&](const QTile& t) {
+    if constexpr (DW) {
+      // lane l touches row 32 wave + (l >> 1) of the wave, 64-byte half l & 1
+      c_wbase = w_block_base(t);
+      c_off = (uint32_t)(wrow(t, 32 * wave + (lane >> 1)) * g.K * 2) + 64u * (uint32_t)(lane & 1);
+      return;
+    }
     const int64_t base = (int64_t)t.e * g.w_rows;
     c_off = (uint32_t)((((base + wrow(t, tid >> 1)) * g.K) >> 1) + 16 * (tid & 1));
     if constexpr (OVL) {
@@ -1395,6 +1430,18 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     sa_stage = uni(sa_stage);
     const int c_kt_u = uni(c_kt), a_kt_u = uni(a_kt);
     const uint32_t sc = qsm_lds + sc_stage * Q_STAGE + Q_A_BYTES;
+    if constexpr (DW) {
+      // d = 0: the weight lines of the code stream's k-step, into the wave's
+      // scratch words in the (unused) code area; d = 1..: activation chunks
+      if (d == 0) {
+        dma4_vb(uni_ptr(c_wbase + c_kt_u * (BK * 2)), c_off, sc + wave * 256);
+      } else {
+        const int c = d - 1;
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(g.A) + a_kt_u * (BK * 2);
+        dma16(base, a_off[c], qsm_lds + sa_stage * Q_STAGE + (c * Q_THREADS + wave * 64) * 16);
+      }
+      return;
+    }
     if (OVL && d == Q_DMAS) {
       const uint8_t* base = reinterpret_cast<const uint8_t*>(g.ovl) + c_kt_u * (Q_OVL_WORDS * 4);
       dma4(base, o_off, sc + Q_C_BYTES + Q_Z_BYTES + wave * (Q_OVL_WORDS * 4));
@@ -1427,10 +1474,34 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       tok_fill(c_next, (c_ord + 1) & 1);
     }
   };
+  // DW register-load stream: the weight fragments of k-step r_kt of tile
+  // r_ord, one k-step ahead of the MFMAs (r_base: the tile's weight block;
+  // r_off: this lane's row and half within it)
+  int r_ord = 0, r_kt = 0;
+  const uint8_t* r_base = nullptr;
+  uint32_t r_off = 0;
+  auto r_setup = [&](const QTile& t) {
+    r_base = w_block_base(t);
+    r_off = (uint32_t)(wrow(t, 32 * wave + l32) * g.K * 2) + 64u * (uint32_t)half;
+  };
   // end of a k-step: advance both streams (past the last tile they repeat the
   // last k-step into a stage nobody reads).  The stream state goes through
   // readfirstlane: it is uniform, and the compiler then keeps it in scalar
   // registers and branches on it with scalar branches.
+  // DW: the r stream moves one k-step per k-step of the MFMAs (and once in the
+  // prologue, after k-step 0's load), independently of the DMA streams
+  auto r_advance = [&]() {
+    r_kt = uni(r_kt + 1);
+    if (r_kt == nk) {
+      if (r_ord + 1 < n_my) {
+        r_ord = uni(r_ord + 1);
+        r_kt = 0;
+        r_setup(decode(r_ord));
+      } else {
+        r_kt = nk - 1;
+      }
+    }
+  };
   auto advance = [&]() {
     c_kt = uni(c_kt + 1);
     if (c_kt == nk) {
@@ -1457,6 +1528,41 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // ---- weight fragments: wf[set][sub-step j]; lane half h holds
   //      k = 32h + 8j + [0, 8) of weight row 32 wave + l32 ----
   u32x4 wf[2][4];
+  // DW: the four fragment registers of the r stream's k-step into set BSX (one
+  // 16-byte global load each, issued as asm so that no compiler wait drains
+  // the DMAs in flight); the step's closing vmcnt wait covers them, and that
+  // wait takes the registers as operands, so no use can move above it.  The
+  // base comes out of readfirstlane (a VALU write of the SGPRs) and a VMEM
+  // instruction may read such an SGPR only 5 wait states later; the compiler
+  // does not look into the asm, so the asm supplies them (s_nop 4).
+#define USAF_WLOAD(X)                                                                          \
+  asm volatile("s_nop 4\n\t"                                                                    \
+               "global_load_dwordx4 %0, %4, %5\n\t"                                             \
+               "global_load_dwordx4 %1, %4, %5 offset:16\n\t"                                   \
+               "global_load_dwordx4 %2, %4, %5 offset:32\n\t"                                   \
+               "global_load_dwordx4 %3, %4, %5 offset:48"                                        \
+               : "=&v"(wf[X][0]), "=&v"(wf[X][1]), "=&v"(wf[X][2]), "=&v"(wf[X][3])              \
+               : "v"(woff), "s"(wbase))
+#define USAF_WWAIT(X, N)                                                                       \
+  asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_barrier"                                          \
+               : "+v"(wf[X][0]), "+v"(wf[X][1]), "+v"(wf[X][2]), "+v"(wf[X][3])::"memory")
+  auto wload = [&](int set) {
+    const uint8_t* wbase = uni_ptr(r_base + uni(r_kt) * (BK * 2));
+    const uint32_t woff = r_off;
+    if (set == 0) USAF_WLOAD(0);
+    else USAF_WLOAD(1);
+  };
+  // the step's closing wait (vmcnt(5): all but its 5 DMAs) and barrier, with set `set` as operands
+  auto wwait5 = [&](int set) {
+    if (set == 0) USAF_WWAIT(0, 5);
+    else USAF_WWAIT(1, 5);
+  };
+  auto wwait0 = [&](int set) {
+    if (set == 0) USAF_WWAIT(0, 0);
+    else USAF_WWAIT(1, 0);
+  };
+#undef USAF_WLOAD
+#undef USAF_WWAIT
   // per-lane LDS byte offsets within a stage (the stage offset is uniform):
   // activation fragment j of slot block i at fb_j + 4096 i (the swizzle of row
   // 32 i + l32 does not depend on i), the lane's codes, its scale|zero word
@@ -1546,7 +1652,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   //      set BS) with the dequant of k-step gs + 1 (codes in stage s1) into
   //      set BS ^ 1; the k-step's DMAs (codes of gs + 3 into stage s0,
   //      activations of gs + 2 into stage s2) are spread over its regions ----
-  constexpr int QD = Q_DMAS + (OVL ? 1 : 0);  // DMA instructions of a full step
+  constexpr int QD = DW ? 1 + Q_A_LOADS : Q_DMAS + (OVL ? 1 : 0);  // DMA instructions of a full step
   auto step = [&](auto bs_c, auto nrb_c, f32x16 (&acc)[decltype(nrb_c)::value], int s0, int s1, int s2) {
     constexpr int BS = decltype(bs_c)::value, NRB = decltype(nrb_c)::value;
     constexpr int NF = 4 * NRB;   // activation fragments = MFMAs, f = j * NRB + i
@@ -1559,9 +1665,11 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
     auto rp = [](int p) { return 1 + p * (R - 1) / NP; };
     auto rd = [](int d) { return d * R / QD; };
     pre_step();
+    // DW: next k-step's weight fragments, first of the step's memory operations
+    if constexpr (DW) wload(BS ^ 1);
     u32x4 cq, kz[8];
     uint32_t csz = 0;
-    codes_read(s1, cq, csz);
+    if constexpr (!DW) codes_read(s1, cq, csz);
     // BT: the words of register wd are read one region before its first pair
     if constexpr (BT) kz_read(s1, 0, kz);
     uint32_t oa = 0, od = 0;
@@ -1607,7 +1715,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
         for (int wd = 1; wd < 4; ++wd)
           if (rp(4 * wd) - 1 == r) kz_read(s1, wd, kz);
       }
-      if (r >= 1) {
+      if (!DW && r >= 1) {
         // this region's pairs p (half-word pair q = p & 3 of fragment register
         // wd = p >> 2), computed together (independent chains) and pinned here
         uint32_t v[NP];
@@ -1648,16 +1756,18 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       __builtin_amdgcn_sched_barrier(0);
     }
     advance();
+    if constexpr (DW) r_advance();
     // this step's QD DMAs may stay in flight; everything older (the stages the
     // next step reads, the token rows) has landed in this wave, and after the
     // barrier in all waves.  sched_barrier keeps the step's register work on
     // its side of the barrier.
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (OVL) asm volatile("s_waitcnt vmcnt(7)\n\ts_barrier" ::: "memory");
+    if constexpr (DW) wwait5(BS ^ 1);  // the weight loads were issued before the step's 5 DMAs
+    else if constexpr (OVL) asm volatile("s_waitcnt vmcnt(7)\n\ts_barrier" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
-  static_assert(QD == (OVL ? 7 : 6), "the step's vmcnt wait counts its DMAs");
+  static_assert(QD == (DW ? 5 : OVL ? 7 : 6), "the step's vmcnt wait counts its DMAs");
 
   // ---- epilogue: per 32-slot block, the wave's dtype results go through its
   //      own LDS tile ([32 slots][Q_EPW]) and out as 16-byte row stores ----
@@ -1847,12 +1957,13 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   {
     const QTile t0 = decode(0);
     c_setup(t0);
+    if constexpr (DW) r_setup(t0);
     tok_fill(t0, 0);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     a_refresh(0);
   }
-  dma_one(0, 0, 0);                            // codes 0: scale|zero
-  dma_one(1, 0, 0);                            // codes 0
+  dma_one(0, 0, 0);                            // codes 0: scale|zero (DW: the weight lines of k-step 0)
+  if constexpr (!DW) dma_one(1, 0, 0);         // codes 0
   if constexpr (OVL) dma_one(Q_DMAS, 0, 0);    // their entries
   if (nk == 2 && n_my > 1) {                   // the code stream enters tile 1 after codes 1
     c_next = decode(1);
@@ -1873,7 +1984,14 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   for (int d = 0; d < QD; ++d) dma_one(d, 2, 1);  // codes (and entries) 2, activations 1
   advance();
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  dequant_all(I0{}, 0);
+  if constexpr (DW) {
+    // k-step 0's weight fragments; the r stream then stands at k-step 1
+    wload(0);
+    wwait0(0);
+    r_advance();
+  } else {
+    dequant_all(I0{}, 0);
+  }
   if constexpr (OVL) {  // k-step 0: its entries are in stage 0
     const uint32_t e = ovl_entry(0);
     const uint32_t a = sEp_lds + (e & 0xFFFFu), d = e >> 16;
@@ -1939,11 +2057,19 @@ int launch_nk_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
   return USAF_OK;
 }
 
-template <int EPI, int DT, bool BT, bool OVL>
+template <int EPI, int DT, bool BT, bool OVL, bool DW = false>
 void q4_prepare() {
   static const bool done =
-      raise_lds_limit(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT, BT, OVL>), kQSmemBytes);
+      raise_lds_limit(reinterpret_cast<const void*>(&moe_gemm_q4_kernel<EPI, DT, BT, OVL, DW>), kQSmemBytes);
   (void)done;
+}
+
+// dense 16-bit weights on the LDS-DMA kernel (DW)
+template <int EPI, int DT>
+int launch_dw_one(const GemmArgs& g, unsigned blocks, hipStream_t st) {
+  q4_prepare<EPI, DT, false, false, true>();
+  moe_gemm_q4_kernel<EPI, DT, false, false, true><<<blocks, Q_THREADS, kQSmemBytes, st>>>(g);
+  return USAF_OK;
 }
 
 template <int EPI, int DT, bool BT = false>
@@ -2003,6 +2129,13 @@ bool q4_dma_ok(const GemmArgs& g, int64_t a_rows_total) {
          a_rows_total * g.lda * 2 < ((int64_t)1 << 32) && (int64_t)g.E * g.w_rows * g.w_cols / 2 < ((int64_t)1 << 32);
 }
 
+// dense weights (one expert's block below 4 GiB, 16-byte aligned) on the same kernel (DW)
+bool dw_dma_ok(const GemmArgs& g, int64_t a_rows_total) {
+  return g.w16 != nullptr && ((uintptr_t)g.w16 & 15) == 0 && ((uintptr_t)g.A & 15) == 0 && g.lda % 8 == 0 &&
+         g.K % 128 == 0 && g.E <= Q_MAX_E && a_rows_total * g.lda * 2 < ((int64_t)1 << 32) &&
+         g.w_rows * g.w_cols * 2 < ((int64_t)1 << 32) && g.w_cols == g.K;
+}
+
 template <int EPI>
 int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_total, hipStream_t st,
                    const char* what) {
@@ -2019,13 +2152,16 @@ int launch_gemm_nk(const GemmArgs& g, int dt, int64_t max_tiles, int64_t a_rows_
                      "%s: an overlay needs the 4-bit LDS-DMA kernel (4-bit weights, 16-byte aligned activation rows, "
                      "K %% 128 == 0, E <= %d, operands below 4 GiB)", what, Q_MAX_E);
   if (int rc = check_ovl(g, EPI, what)) return rc;
+  const bool dw = dense && dw_dma_ok(g, a_rows_total);
   int rc;
   if (dt == USAF_BF16)
-    rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
+    rc = dw ? launch_dw_one<EPI, USAF_BF16>(g, (unsigned)blocks, st)
+         : dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_BF16>(g, (unsigned)blocks, st)
          : dma ? launch_q4_one<EPI, USAF_BF16>(g, (unsigned)blocks, st)
                : launch_nk_one<EPI, BQ_Q4, USAF_BF16>(g, (unsigned)blocks, st);
   else if (dt == USAF_F16)
-    rc = dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_F16>(g, (unsigned)blocks, st)
+    rc = dw ? launch_dw_one<EPI, USAF_F16>(g, (unsigned)blocks, st)
+         : dense ? launch_nk_one<EPI, BQ_DENSE16, USAF_F16>(g, (unsigned)blocks, st)
          : dma ? launch_q4_one<EPI, USAF_F16>(g, (unsigned)blocks, st)
                : launch_nk_one<EPI, BQ_Q4, USAF_F16>(g, (unsigned)blocks, st);
   else
@@ -2096,6 +2232,8 @@ void prepare_dt() {
   q4_prepare<EPI_STORE, DT, false, true>();
   q4_prepare<EPI_SWIGLU_BWD, DT, true, true>();
   q4_prepare<EPI_STORE, DT, true, true>();
+  q4_prepare<EPI_SWIGLU_FWD, DT, false, false, true>();
+  q4_prepare<EPI_STORE, DT, false, false, true>();
   ws_prepare<BMODE_KN, EPI_SWIGLU_BWD, BQ_Q4, DT>();
   ws_prepare<BMODE_KN, EPI_SWIGLU_BWD, BQ_DENSE16, DT>();
   ws_prepare<BMODE_KN, EPI_STORE, BQ_Q4, DT>();
