@@ -101,6 +101,25 @@ int usaf_hip_dequant_q4_slices(const int8_t* packed, const uint16_t* scale_f16, 
                                void* stream);
 
 /*
+ * The same on-demand fill of the per-expert copy cache (moe_loader.py:183-224),
+ * written in the fragment order the *_fwd_slots GEMMs read: job j dequantizes
+ * expert src_expert[j] of a [n_experts, w_rows, K] 4-bit tensor (group size 128
+ * along K) into slot dst_slot[j] of an arena of n_slots slots, each
+ * usaf_hip_frag_slot_elems(w_rows, K, inter) elements of out_dtype (fp16 / bf16).
+ * Values are those of usaf_hip_dequant_q4; only the order differs.  inter > 0
+ * marks a gate_up block (w_rows == 2 inter, SwiGLU row pairing); inter == 0 a
+ * plain block such as down.  K % 128 == 0; codes 4-byte, out 16-byte aligned;
+ * jobs naming an expert or slot out of range are skipped.
+ */
+int usaf_hip_dequant_q4_slices_frag(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,
+                                    int64_t n_experts, int64_t w_rows, int64_t K, int64_t inter, int64_t n_jobs,
+                                    const int64_t* src_expert, const int64_t* dst_slot, int64_t n_slots, void* out,
+                                    int32_t out_dtype, void* stream);
+/* Elements of one fragment-order slot (rows padded to whole GEMM tiles); -1 for
+ * shapes the layout does not take (K % 128 != 0, w_rows != 2 inter). */
+int64_t usaf_hip_frag_slot_elems(int64_t w_rows, int64_t K, int64_t inter);
+
+/*
  * 4-bit group quantization.
  * Replaces usaf/quantization.py:21-85 `quantize_4bit`.
  *   x       fp32 / fp16 / bf16 [numel]  (flattened tensor)
@@ -273,11 +292,13 @@ int usaf_hip_moe_down_fwd(const void* act, int64_t I, const int32_t* offsets, in
 
 /* usaf_hip_moe_gate_up_fwd / usaf_hip_moe_down_fwd with dense weights held in a
  * slot arena (dequantized expert copies of usaf_amd's per-expert cache, the
- * on-demand fp16 copies of moe_loader.py:130-181): expert e's weight is block
- * slot_of[e] of arena [n_slots, 2I, H] (gate_up) or [n_slots, H, I] (down), in
- * the activation dtype.  slot_of int32 [E] on the device; entries outside
- * [0, n_slots) are clamped (wrong weights, never an access outside the arena).
- * Same shape requirements as the non-arena calls. */
+ * on-demand fp16 copies of moe_loader.py:130-181): expert e's weight is slot
+ * slot_of[e] of the arena, in the fragment order of
+ * usaf_hip_dequant_q4_slices_frag (gate_up: w_rows 2I, K H, inter I; down:
+ * w_rows H, K I, inter 0), in the activation dtype.  slot_of int32 [E] on the
+ * device; entries outside [0, n_slots) are clamped (wrong weights, never an
+ * access outside the arena).  Needs the contraction dimension % 128 == 0,
+ * E <= 255, 16-byte aligned activations and arena. */
 int usaf_hip_moe_gate_up_fwd_slots(const void* x, int64_t T, int64_t H, const int32_t* token_idx,
                                    const int32_t* offsets, int64_t S, int64_t E, int64_t I, const void* arena,
                                    const int32_t* slot_of, int64_t n_slots, int32_t dtype, void* gu, void* act,

@@ -81,8 +81,9 @@ def test_slot_cache_lru_copies_and_forward(gpu_device):
             for j in torch.randint(0, len(keys), (3,), generator=g).tolist():
                 lname, e = keys[j]
                 s = cache.slot_of(lname, e)
-                assert torch.equal(cache.gu_arena[s].cpu().view(torch.int16), deq[lname][0][e].view(torch.int16))
-                assert torch.equal(cache.dn_arena[s].cpu().view(torch.int16), deq[lname][1][e].view(torch.int16))
+                assert torch.equal(cache.copy_of(s, "gate_up").cpu().view(torch.int16),
+                                   deq[lname][0][e].view(torch.int16))
+                assert torch.equal(cache.copy_of(s, "down").cpu().view(torch.int16), deq[lname][1][e].view(torch.int16))
             x = (x.float() + ref.float()).to(dt)
     assert cache.evictions > 0 and cache.hits > 0
     _say(f"  hits {cache.hits}, misses {cache.misses}, evictions {cache.evictions}")
@@ -138,7 +139,8 @@ def test_slot_cache_qwen3_layer_shape(gpu_device, dt):
             for j in torch.randint(0, len(keys), (4,), generator=g).tolist():
                 lname, e = keys[j]
                 s = cache.slot_of(lname, e)
-                assert torch.equal(cache.gu_arena[s].cpu().view(torch.int16), deq[lname][0][e].view(torch.int16))
-                assert torch.equal(cache.dn_arena[s].cpu().view(torch.int16), deq[lname][1][e].view(torch.int16))
+                assert torch.equal(cache.copy_of(s, "gate_up").cpu().view(torch.int16),
+                                   deq[lname][0][e].view(torch.int16))
+                assert torch.equal(cache.copy_of(s, "down").cpu().view(torch.int16), deq[lname][1][e].view(torch.int16))
     assert cache.evictions > 0 and cache.hits > 0
     _say(f"  hits {cache.hits}, misses {cache.misses}, evictions {cache.evictions}")

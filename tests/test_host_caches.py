@@ -88,3 +88,39 @@ def test_frozen_cache_build_reuse_and_invalidation(tmp_path):
     h = get_hidden(arr, 2, "cpu", torch.float32)
     exp = (samples[2]["input_ids"].float().unsqueeze(-1).repeat(1, hidden) / 7.0).half().float()
     assert h.shape == (1, seq, hidden) and torch.equal(h[0], exp)
+
+
+def _natural_chunk(w_rows, K, inter, nt, w, ks, j, lane):
+    """Row and column of the 8 elements lane `lane` of wave `w` loads into
+    register `j` at k-step `ks` of n-tile `nt` (the dense-weight GEMM's
+    fragment: row 32 w + (lane & 31) of the tile, or the gate/up pair of
+    SwiGLU row 16 w + (lane & 15); columns 64 ks + 32 (lane >> 5) + 8 j)."""
+    if inter > 0:
+        n = 128 * nt + 16 * w + lane % 16
+        row = n + (inter if lane % 32 >= 16 else 0)
+        ok = n < inter
+    else:
+        row = 256 * nt + 32 * w + lane % 32
+        ok = row < w_rows
+    return (row, 64 * ks + 32 * (lane // 32) + 8 * j) if ok else None
+
+
+def test_fragment_order_slot_layout():
+    from usaf_amd.expert_cache import frag_chunk_index
+    for w_rows, K, inter in ((256, 128, 128), (384, 256, 0), (256, 128, 0), (768, 384, 384)):
+        idx = frag_chunk_index(w_rows, K, inter)
+        n_nt = (inter + 127) // 128 if inter else (w_rows + 255) // 256
+        assert idx.numel() == n_nt * 256 * K // 8
+        valid = idx[idx >= 0]
+        # every natural chunk exactly once; the rest is padding
+        assert torch.equal(valid.sort().values, torch.arange(w_rows * K // 8))
+        # spot checks against the per-lane load pattern, walked chunk by chunk
+        nk = K // 64
+        for c in (0, 1, 63, 64, 255, 256, 4 * 64 * nk, idx.numel() - 1, idx.numel() // 2 + 17):
+            lane, t = c % 64, c // 64
+            j, t = t % 4, t // 4
+            ks, t = t % nk, t // nk
+            w, nt = t % 8, t // 8
+            nat = _natural_chunk(w_rows, K, inter, nt, w, ks, j, lane)
+            want = -1 if nat is None else nat[0] * (K // 8) + nat[1] // 8
+            assert int(idx[c]) == want, (w_rows, K, inter, c)

@@ -37,6 +37,8 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_dequant_q4_at": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p],
     "usaf_hip_topk_abs": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],
     "usaf_hip_dequant_q4_slices": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i32, _c_p],
+    "usaf_hip_dequant_q4_slices_frag": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64,
+                                        _c_p, _c_i32, _c_p],
     "usaf_hip_moe_gate_up_fwd_slots": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64,
                                        _c_i32, _c_p, _c_p, _c_p],
     "usaf_hip_moe_down_fwd_slots": [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i32, _c_p,
@@ -98,6 +100,7 @@ _VALUE_FUNCS: dict[str, tuple] = {
     "usaf_hip_combine_bwd_blocked_ws_floats": (_c_i64, [_c_i64, _c_i64]),
     "usaf_hip_router_dw_ws_floats": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "usaf_hip_topk_abs_ws_ints": (_c_i64, [_c_i64]),
+    "usaf_hip_frag_slot_elems": (_c_i64, [_c_i64, _c_i64, _c_i64]),
 }
 
 _lock = threading.Lock()

@@ -459,6 +459,118 @@ extern "C" int usaf_hip_dequant_q4_slices(const int8_t* packed, const uint16_t* 
   return check_launch("dequant_q4_slices");
 }
 
+namespace usaf {
+namespace {
+
+// Expert copies in the fragment order of the dense-weight grouped GEMM: the
+// 16-byte chunk c of a slot is (n-tile nt, wave w, k-step ks, fragment
+// register j, lane l) with c = (((nt * 8 + w) * nk + ks) * 4 + j) * 64 + l,
+// and holds weight row wrow(nt, 32 w + (l & 31)), elements k = 64 ks + 32 (l >> 5)
+// + 8 j + [0, 8): what lane l of wave w loads into register j at k-step ks.
+// Rows: inter > 0 pairs gate row n = 128 nt + 16 w + (l & 15) with up row
+// inter + n (the SwiGLU tile); inter == 0 takes row 256 nt + 32 w + (l & 31).
+// Rows past the matrix are zero.  One thread per chunk: one 32-bit code word
+// and one scale/zero pair in, one 16-byte store out (coalesced per wave).
+template <int OUT_DT>
+__global__ __launch_bounds__(256) void dequant_frag_kernel(const uint32_t* __restrict__ packed,
+                                                           const uint16_t* __restrict__ scale,
+                                                           const uint16_t* __restrict__ zero, u32x4* __restrict__ out,
+                                                           int64_t n_chunks, int64_t cps, int64_t w_rows, int64_t K,
+                                                           int64_t inter, const int64_t* __restrict__ src,
+                                                           const int64_t* __restrict__ dst, int64_t n_src,
+                                                           int64_t n_dst) {
+  const int64_t nk = K / 64;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < n_chunks; c += stride) {
+    const int64_t job = c / cps, cc = c - job * cps;
+    const int64_t e = src[job], d = dst[job];
+    if (e < 0 || e >= n_src || d < 0 || d >= n_dst) continue;
+    const int lane = (int)(cc & 63);
+    int64_t t = cc >> 6;
+    const int jf = (int)(t & 3);
+    t >>= 2;
+    const int64_t ks = t % nk;
+    t /= nk;
+    const int w = (int)(t & 7);
+    const int64_t nt = t >> 3;
+    int64_t row;
+    bool valid;
+    if (inter > 0) {
+      const int64_t n = nt * 128 + 16 * w + (lane & 15);
+      valid = n < inter;
+      row = ((lane & 16) ? inter : 0) + n;
+    } else {
+      row = nt * 256 + 32 * w + (lane & 31);
+      valid = row < w_rows;
+    }
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (valid) {
+      const int64_t el = (e * w_rows + row) * K + ks * 64 + 32 * (lane >> 5) + 8 * jf;  // multiple of 8
+      const uint32_t word = packed[el >> 3];
+      const uint16_t sb = scale[el >> 7], zb = zero[el >> 7];
+      const f16 sh = __builtin_bit_cast(f16, sb), zh = __builtin_bit_cast(f16, zb);
+      uint32_t h[4];
+      dequant_word_f16(word, f16x2{sh, sh}, f16x2{zh, zh}, h);
+      if constexpr (OUT_DT == USAF_F16) {
+        v = u32x4{h[0], h[1], h[2], h[3]};
+      } else if (((sb & 0x7C00u) != 0x7C00u) && ((zb & 0x7C00u) != 0x7C00u)) {
+        v = u32x4{f16pair_to_bf16pair(h[0]), f16pair_to_bf16pair(h[1]), f16pair_to_bf16pair(h[2]),
+                  f16pair_to_bf16pair(h[3])};
+      } else {
+        uint32_t b[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          b[q] = (uint32_t)f16bits_to_bf16bits((uint16_t)(h[q] & 0xFFFFu)) |
+                 ((uint32_t)f16bits_to_bf16bits((uint16_t)(h[q] >> 16)) << 16);
+        v = u32x4{b[0], b[1], b[2], b[3]};
+      }
+    }
+    out[d * cps + cc] = v;
+  }
+}
+
+}  // namespace
+}  // namespace usaf
+
+extern "C" int64_t usaf_hip_frag_slot_elems(int64_t w_rows, int64_t K, int64_t inter) {
+  if (w_rows <= 0 || K <= 0 || K % 128 != 0 || inter < 0 || (inter > 0 && w_rows != 2 * inter)) return -1;
+  const int64_t n_nt = inter > 0 ? (inter + 127) / 128 : (w_rows + 255) / 256;
+  return n_nt * 256 * K;
+}
+
+extern "C" int usaf_hip_dequant_q4_slices_frag(const int8_t* packed, const uint16_t* scale_f16,
+                                               const uint16_t* zero_f16, int64_t n_experts, int64_t w_rows, int64_t K,
+                                               int64_t inter, int64_t n_jobs, const int64_t* src_expert,
+                                               const int64_t* dst_slot, int64_t n_slots, void* out,
+                                               int32_t out_dtype, void* stream) {
+  const int64_t slot_elems = usaf_hip_frag_slot_elems(w_rows, K, inter);
+  if (slot_elems < 0 || n_experts < 0 || n_jobs < 0 || n_slots < 0)
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices_frag: needs K %% 128 == 0, w_rows = 2 inter (or inter 0), "
+                                       "non-negative counts");
+  if (out_dtype != USAF_F16 && out_dtype != USAF_BF16)
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices_frag: out_dtype must be fp16 or bf16");
+  if (n_jobs == 0) return clear_error();
+  if (!packed || !scale_f16 || !zero_f16 || !src_expert || !dst_slot || !out)
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices_frag: null pointer");
+  if ((((uintptr_t)packed) & 3) || (((uintptr_t)out) & 15))
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices_frag: codes must be 4-byte and out 16-byte aligned");
+  const int64_t cps = slot_elems / 8;
+  const int64_t n_chunks = n_jobs * cps;
+  int64_t blocks = (n_chunks + 255) / 256;
+  const int64_t cap = (int64_t)device_cu_count() * 16;
+  if (blocks > cap) blocks = cap;
+  hipStream_t st = as_stream(stream);
+  if (out_dtype == USAF_F16)
+    dequant_frag_kernel<USAF_F16><<<(unsigned)blocks, 256, 0, st>>>((const uint32_t*)packed, scale_f16, zero_f16,
+                                                                    (u32x4*)out, n_chunks, cps, w_rows, K, inter,
+                                                                    src_expert, dst_slot, n_experts, n_slots);
+  else
+    dequant_frag_kernel<USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>((const uint32_t*)packed, scale_f16, zero_f16,
+                                                                     (u32x4*)out, n_chunks, cps, w_rows, K, inter,
+                                                                     src_expert, dst_slot, n_experts, n_slots);
+  return check_launch("dequant_q4_slices_frag");
+}
+
 extern "C" int usaf_hip_quantize_q4(const void* x, int32_t x_dtype, int64_t numel, int64_t group_size,
                                     int8_t* packed, uint16_t* scale_f16, uint16_t* zero_f16, void* stream) {
   if (numel <= 0) return set_error(USAF_ERR_INVALID, "quantize_q4: Scalar tensors cannot be quantized; numel must be > 0");

@@ -85,6 +85,8 @@ struct GemmArgs {
   const int32_t* blk_table;       //   layout of blk_table (usaf_hip_blocked_layout), or nullptr
   const uint32_t* ovl;            // 4-bit DMA kernel: overlay entries (usaf_hip_overlay_* layout), or nullptr
   int64_t ovl_words;              //   and their count (checked against what the GEMM reads)
+  int w_frag;                     // dense weights (DW): 1 = each expert block in the GEMM's fragment order
+  int64_t w_blk_elems;            //   (usaf_hip_dequant_q4_slices_frag) of w_blk_elems elements; 0: w_rows * w_cols
 };
 
 // Workgroup barrier ordering LDS accesses only.  __syncthreads() also orders
@@ -1370,7 +1372,10 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   const int a_lc = (tid & 7) ^ q_swz(tid >> 3);  // logical chunk of this thread's DMA slot
   const uint32_t lda_b = (uint32_t)g.lda * 2;
   // DW: expert blocks of the dense weight; within one block the offsets are 32-bit
-  const uint64_t w_blk_bytes = (uint64_t)g.w_rows * (uint64_t)g.w_cols * 2u;
+  const uint64_t w_blk_bytes = (g.w_blk_elems ? (uint64_t)g.w_blk_elems : (uint64_t)g.w_rows * (uint64_t)g.w_cols) * 2u;
+  // fragment order: the wave's four registers of one k-step are 4 KiB in a row
+  // (register j at 1 KiB j, lane l at 16 l), its k-steps follow each other
+  const uint32_t w_kstep_bytes = g.w_frag ? 4096u : (uint32_t)(BK * 2);
   auto w_block_base = [&](const QTile& t) -> const uint8_t* {
     const uint32_t blk = (uint32_t)uni((int)weight_block(g, t.e));  // clamped to [0, n_slots)
     return reinterpret_cast<const uint8_t*>(g.w16) + (uint64_t)blk * w_blk_bytes;
@@ -1378,9 +1383,11 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   const uint8_t* c_wbase = nullptr;  // DW: weight block of the code stream's tile
   auto c_setup = [&](const QTile& t) {
     if constexpr (DW) {
-      // lane l touches row 32 wave + (l >> 1) of the wave, 64-byte half l & 1
       c_wbase = w_block_base(t);
-      c_off = (uint32_t)(wrow(t, 32 * wave + (lane >> 1)) * g.K * 2) + 64u * (uint32_t)(lane & 1);
+      if (g.w_frag)  // lane l touches bytes [64 l, 64 l + 4) of the wave's 4 KiB
+        c_off = (uint32_t)((((int64_t)t.nt * Q_WAVES + wave) * nk) * 4096) + 64u * (uint32_t)lane;
+      else  // lane l touches row 32 wave + (l >> 1) of the wave, 64-byte half l & 1
+        c_off = (uint32_t)(wrow(t, 32 * wave + (lane >> 1)) * g.K * 2) + 64u * (uint32_t)(lane & 1);
       return;
     }
     const int64_t base = (int64_t)t.e * g.w_rows;
@@ -1434,7 +1441,7 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
       // d = 0: the weight lines of the code stream's k-step, into the wave's
       // scratch words in the (unused) code area; d = 1..: activation chunks
       if (d == 0) {
-        dma4_vb(uni_ptr(c_wbase + c_kt_u * (BK * 2)), c_off, sc + wave * 256);
+        dma4_vb(uni_ptr(c_wbase + (uint32_t)c_kt_u * w_kstep_bytes), c_off, sc + wave * 256);
       } else {
         const int c = d - 1;
         const uint8_t* base = reinterpret_cast<const uint8_t*>(g.A) + a_kt_u * (BK * 2);
@@ -1482,7 +1489,10 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   uint32_t r_off = 0;
   auto r_setup = [&](const QTile& t) {
     r_base = w_block_base(t);
-    r_off = (uint32_t)(wrow(t, 32 * wave + l32) * g.K * 2) + 64u * (uint32_t)half;
+    if (g.w_frag)
+      r_off = (uint32_t)((((int64_t)t.nt * Q_WAVES + wave) * nk) * 4096) + 16u * (uint32_t)lane;
+    else
+      r_off = (uint32_t)(wrow(t, 32 * wave + l32) * g.K * 2) + 64u * (uint32_t)half;
   };
   // end of a k-step: advance both streams (past the last tile they repeat the
   // last k-step into a stage nobody reads).  The stream state goes through
@@ -1535,22 +1545,27 @@ __global__ __launch_bounds__(Q_THREADS) void moe_gemm_q4_kernel(const GemmArgs g
   // base comes out of readfirstlane (a VALU write of the SGPRs) and a VMEM
   // instruction may read such an SGPR only 5 wait states later; the compiler
   // does not look into the asm, so the asm supplies them (s_nop 4).
-#define USAF_WLOAD(X)                                                                          \
+#define USAF_WLOAD(X, O1, O2, O3)                                                              \
   asm volatile("s_nop 4\n\t"                                                                    \
                "global_load_dwordx4 %0, %4, %5\n\t"                                             \
-               "global_load_dwordx4 %1, %4, %5 offset:16\n\t"                                   \
-               "global_load_dwordx4 %2, %4, %5 offset:32\n\t"                                   \
-               "global_load_dwordx4 %3, %4, %5 offset:48"                                        \
+               "global_load_dwordx4 %1, %4, %5 offset:" #O1 "\n\t"                              \
+               "global_load_dwordx4 %2, %4, %5 offset:" #O2 "\n\t"                              \
+               "global_load_dwordx4 %3, %4, %5 offset:" #O3                                      \
                : "=&v"(wf[X][0]), "=&v"(wf[X][1]), "=&v"(wf[X][2]), "=&v"(wf[X][3])              \
                : "v"(woff), "s"(wbase))
 #define USAF_WWAIT(X, N)                                                                       \
   asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_barrier"                                          \
                : "+v"(wf[X][0]), "+v"(wf[X][1]), "+v"(wf[X][2]), "+v"(wf[X][3])::"memory")
   auto wload = [&](int set) {
-    const uint8_t* wbase = uni_ptr(r_base + uni(r_kt) * (BK * 2));
+    const uint8_t* wbase = uni_ptr(r_base + (uint32_t)uni(r_kt) * w_kstep_bytes);
     const uint32_t woff = r_off;
-    if (set == 0) USAF_WLOAD(0);
-    else USAF_WLOAD(1);
+    if (g.w_frag) {  // registers 1 KiB apart
+      if (set == 0) USAF_WLOAD(0, 1024, 2048, 3072);
+      else USAF_WLOAD(1, 1024, 2048, 3072);
+    } else {  // 16 bytes apart within the row's k-step
+      if (set == 0) USAF_WLOAD(0, 16, 32, 48);
+      else USAF_WLOAD(1, 16, 32, 48);
+    }
   };
   // the step's closing wait (vmcnt(5): all but its 5 DMAs) and barrier, with set `set` as operands
   auto wwait5 = [&](int set) {
@@ -2131,9 +2146,10 @@ bool q4_dma_ok(const GemmArgs& g, int64_t a_rows_total) {
 
 // dense weights (one expert's block below 4 GiB, 16-byte aligned) on the same kernel (DW)
 bool dw_dma_ok(const GemmArgs& g, int64_t a_rows_total) {
+  const int64_t blk = g.w_blk_elems ? g.w_blk_elems : g.w_rows * g.w_cols;
   return g.w16 != nullptr && ((uintptr_t)g.w16 & 15) == 0 && ((uintptr_t)g.A & 15) == 0 && g.lda % 8 == 0 &&
-         g.K % 128 == 0 && g.E <= Q_MAX_E && a_rows_total * g.lda * 2 < ((int64_t)1 << 32) &&
-         g.w_rows * g.w_cols * 2 < ((int64_t)1 << 32) && g.w_cols == g.K;
+         g.K % 128 == 0 && g.E <= Q_MAX_E && a_rows_total * g.lda * 2 < ((int64_t)1 << 32) && blk > 0 &&
+         blk * 2 < ((int64_t)1 << 32) && g.w_cols == g.K;
 }
 
 template <int EPI>
@@ -2327,6 +2343,11 @@ extern "C" int usaf_hip_moe_gate_up_fwd_slots(const void* x, int64_t T_rows, int
   g.w16 = (const uint16_t*)arena; g.w_slot = slot_of; g.n_slots = n_slots; g.w_rows = 2 * I; g.w_cols = H;
   g.N = I; g.K = H; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)act; g.ldo = I; g.out2 = (uint16_t*)gu; g.ldo2 = 2 * I;
+  g.w_frag = 1;
+  g.w_blk_elems = usaf_hip_frag_slot_elems(2 * I, H, I);
+  if (!dw_dma_ok(g, T_rows))
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_gate_up_fwd_slots: the fragment-order arena needs 16-byte aligned "
+                                           "activation rows, H %% 128 == 0, E <= %d and blocks below 4 GiB", Q_MAX_E);
   const int64_t max_tiles = (S / NK_BM + E) * ((I + 127) / 128);
   return launch_gemm_nk<EPI_SWIGLU_FWD>(g, dtype, max_tiles, T_rows, as_stream(stream), "moe_gate_up_fwd_slots");
 }
@@ -2346,6 +2367,11 @@ extern "C" int usaf_hip_moe_down_fwd_slots(const void* act, int64_t I, const int
   g.w16 = (const uint16_t*)arena; g.w_slot = slot_of; g.n_slots = n_slots; g.w_rows = H; g.w_cols = I;
   g.N = H; g.K = I; g.inter = I; g.offsets = offsets; g.E = (int)E;
   g.out = (uint16_t*)y; g.ldo = H;
+  g.w_frag = 1;
+  g.w_blk_elems = usaf_hip_frag_slot_elems(H, I, 0);
+  if (!dw_dma_ok(g, S))
+    return set_error(USAF_ERR_UNSUPPORTED, "moe_down_fwd_slots: the fragment-order arena needs 16-byte aligned "
+                                           "activation rows, I %% 128 == 0, E <= %d and blocks below 4 GiB", Q_MAX_E);
   const int64_t max_tiles = (S / NK_BM + E) * ((H + NK_BN - 1) / NK_BN);
   return launch_gemm_nk<EPI_STORE>(g, dtype, max_tiles, S, as_stream(stream), "moe_down_fwd_slots");
 }

@@ -22,6 +22,12 @@ layers of Qwen3-30B-A3B) and the copies are per expert:
   GEMMs (usaf_hip_moe_gate_up_fwd_slots / _down_fwd_slots), so no expert is
   ever copied into a contiguous [E, ...] tensor.
 
+A slot is written in the order the arena GEMMs read it
+(usaf_hip_dequant_q4_slices_frag): the four 16-byte weight registers each
+lane of a wave loads per 64-wide k-step sit next to each other, so every load
+instruction of the GEMM reads 1 KiB in a row instead of 64 rows' worth of
+cache lines.  ``copy_of`` gives a slot back in natural [rows, cols] order.
+
 Copies hold the reference's fp16 dequantized values (dtype fp16, the default,
 with fp16 activations) or their bf16 rounding (dtype bf16, for bf16
 activations: the MFMA operands of one product share a type).  A layer's
@@ -56,17 +62,18 @@ class ExpertSlotCache:
                 if not q.fused_ok():
                     raise ValueError(f"{name}: the slot cache needs group size 128 along whole rows")
         self.layers = dict(layers)
-        self.gu_elems = 2 * self.I * self.H
-        self.dn_elems = self.H * self.I
-        if self.gu_elems % 2048 or self.dn_elems % 2048:
-            raise ValueError("expert slices must be multiples of 2048 elements")
+        if self.H % 128 or self.I % 128:
+            raise ValueError("the slot cache needs hidden and intermediate sizes that are multiples of 128")
+        # fragment-order slots: rows padded to whole GEMM tiles
+        self.gu_elems = int(N.load().usaf_hip_frag_slot_elems(2 * self.I, self.H, self.I))
+        self.dn_elems = int(N.load().usaf_hip_frag_slot_elems(self.H, self.I, 0))
         elem = torch.empty(0, dtype=dtype).element_size()
         self.slot_bytes = (self.gu_elems + self.dn_elems) * elem
         self.n_slots = int(min(len(layers) * self.E, max_bytes // self.slot_bytes))
         if self.n_slots < self.E:
             raise ValueError(f"max_bytes={max_bytes} holds {self.n_slots} expert slots; one layer needs {self.E}")
-        self.gu_arena = torch.empty(self.n_slots, 2 * self.I, self.H, dtype=dtype, device=self.device)
-        self.dn_arena = torch.empty(self.n_slots, self.H, self.I, dtype=dtype, device=self.device)
+        self.gu_arena = torch.empty(self.n_slots, self.gu_elems, dtype=dtype, device=self.device)
+        self.dn_arena = torch.empty(self.n_slots, self.dn_elems, dtype=dtype, device=self.device)
         self._lru: "OrderedDict[Tuple[str, int], int]" = OrderedDict()
         self._free: List[int] = list(range(self.n_slots - 1, -1, -1))
         self._host_tables: Dict[str, List[int]] = {n: [0] * self.E for n in layers}
@@ -138,19 +145,36 @@ class ExpertSlotCache:
         if ev is not None:
             a = torch.cuda.Event(enable_timing=True)
             a.record()
-        for q, arena, elems in ((ew.gate_up, self.gu_arena, self.gu_elems), (ew.down, self.dn_arena, self.dn_elems)):
-            N.call("usaf_hip_dequant_q4_slices", q.q.data_ptr(), q.s.data_ptr(), q.z.data_ptr(), q.q.shape[0], elems,
-                   len(missed), jobs[0].data_ptr(), jobs[1].data_ptr(), self.n_slots, arena.data_ptr(),
+        for q, arena, rows, k, inter in ((ew.gate_up, self.gu_arena, 2 * self.I, self.H, self.I),
+                                         (ew.down, self.dn_arena, self.H, self.I, 0)):
+            N.call("usaf_hip_dequant_q4_slices_frag", q.q.data_ptr(), q.s.data_ptr(), q.z.data_ptr(), self.E, rows, k,
+                   inter, len(missed), jobs[0].data_ptr(), jobs[1].data_ptr(), self.n_slots, arena.data_ptr(),
                    N.dtype_code(self.dtype), st)
         if ev is not None:
             b = torch.cuda.Event(enable_timing=True)
             b.record()
             ev.append((a, b, len(missed)))
         # algorithmic bytes: codes + scale/zero in, dequantized copies out
-        n = len(missed) * (self.gu_elems + self.dn_elems)
+        n = len(missed) * 3 * self.H * self.I
         self.dequant_bytes += int(n * (0.5 + 4.0 / 128 + torch.empty(0, dtype=self.dtype).element_size()))
         # keep the job tensor alive until the launches have read it
         self._last_jobs = jobs
+
+    def copy_of(self, slot: int, role: str) -> torch.Tensor:
+        """Slot ``slot``'s copy of the gate_up [2I, H] or down [H, I] slice, in
+        natural row order (for checks; the arena holds fragment order)."""
+        if role == "gate_up":
+            arena, rows, k, inter = self.gu_arena, 2 * self.I, self.H, self.I
+        elif role == "down":
+            arena, rows, k, inter = self.dn_arena, self.H, self.I, 0
+        else:
+            raise ValueError(role)
+        idx = frag_chunk_index(rows, k, inter).to(arena.device)
+        frag = arena[slot].view(-1, 8)
+        keep = idx >= 0
+        out = torch.empty(rows * k // 8, 8, dtype=arena.dtype, device=arena.device)
+        out[idx[keep]] = frag[keep]
+        return out.view(rows, k)
 
     # ---- forward --------------------------------------------------------------------
 
@@ -189,6 +213,30 @@ class ExpertSlotCache:
         N.call("usaf_hip_moe_down_fwd_slots", act.data_ptr(), self.I, b.offsets.data_ptr(), S, self.E, self.H,
                self.dn_arena.data_ptr(), table.data_ptr(), self.n_slots, code, y.data_ptr(), st)
         return combine(y, weights, b.pair_slot, self.dtype)
+
+
+def frag_chunk_index(w_rows: int, K: int, inter: int) -> torch.Tensor:
+    """For each 16-byte chunk of a fragment-order slot, the natural chunk
+    (row * K / 8 + col / 8) it holds, or -1 for padding rows: chunk
+    c = (((nt * 8 + w) * nk + ks) * 4 + j) * 64 + l holds row wrow(nt, w, l),
+    columns 64 ks + 32 (l >> 5) + 8 j + [0, 8)."""
+    nk = K // 64
+    n_nt = (inter + 127) // 128 if inter > 0 else (w_rows + 255) // 256
+    nt = torch.arange(n_nt).view(-1, 1, 1, 1, 1)
+    w = torch.arange(8).view(1, -1, 1, 1, 1)
+    ks = torch.arange(nk).view(1, 1, -1, 1, 1)
+    j = torch.arange(4).view(1, 1, 1, -1, 1)
+    lane = torch.arange(64).view(1, 1, 1, 1, -1)
+    if inter > 0:
+        n = nt * 128 + 16 * w + (lane & 15)
+        valid = n < inter
+        row = torch.where((lane & 16) != 0, inter, 0) + n
+    else:
+        row = nt * 256 + 32 * w + (lane & 31)
+        valid = row < w_rows
+    col8 = ks * 8 + 4 * (lane >> 5) + j
+    idx = row * (K // 8) + col8
+    return torch.where(valid, idx, -1).reshape(-1)
 
 
 def q4_expert_slice(q: Q4Tensor, expert: int, dtype: torch.dtype) -> torch.Tensor:
