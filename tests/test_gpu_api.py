@@ -94,6 +94,8 @@ def test_expert_cache_lru_overlays_prefetch(gpu_device):
     masters = {full1: nn.Parameter(torch.randn(500, generator=g).to(gpu_device))}
     cache.apply_resident_overlays({full1: aidx.to(gpu_device)}, masters)
     cache.evict_all()
+    # a resident module dequantizes nothing its resident copy holds
+    assert cache._dequant(names[1], skip=cache._resident[names[1]].keys()) == {}
     w1 = cache.get_expert_weights(names[1])["gate_up_proj"]
     ref1 = _oracle_dequant(qd[full1]).reshape(-1).clone()
     ref1[aidx] = masters[full1].detach().cpu().half()

@@ -144,3 +144,45 @@ def test_slot_cache_qwen3_layer_shape(gpu_device, dt):
                 assert torch.equal(cache.copy_of(s, "down").cpu().view(torch.int16), deq[lname][1][e].view(torch.int16))
     assert cache.evictions > 0 and cache.hits > 0
     _say(f"  hits {cache.hits}, misses {cache.misses}, evictions {cache.evictions}")
+
+
+def test_slot_cache_slots_beyond_4gib(gpu_device):
+    """The arena addressing at the configs[4] scale: 700 Qwen3-shape slots
+    (a gate_up arena of 2.2e9 elements, 4.4 GB, past 2^31 elements and 4 GiB),
+    the free list taken from the top so a layer's experts land in the highest
+    slots; the forward and sampled copies checked against the reference's
+    dequant."""
+    E, H, I, T, k = 128, 2048, 768, 512, 8
+    dt = torch.float16
+    _say("slot cache: 700 Qwen3-shape slots, a layer placed in slots 572..699 (offsets past 4 GiB)")
+    torch.set_num_threads(16)
+    from oracle.codec_torch import dequant_opseq
+    g = torch.Generator().manual_seed(4949)
+    qs = [G.Q4Tensor.quantize((torch.randn(shp, generator=g) * 0.02).half().to(gpu_device))
+          for shp in ((E, 2 * I, H), (E, H, I))]
+    ew = G.ExpertWeights(*qs)
+    deq = tuple(dequant_opseq(q.q.cpu(), q.s.cpu(), q.z.cpu(), q.shape) for q in qs)
+    # six names over one set of weights: room for 768 keys, the arena caps it at 700
+    layers = {f"model.layers.{li}.mlp.experts": ew for li in range(6)}
+    cache = ExpertSlotCache(layers, gpu_device, max_bytes=700 * cache_slot_bytes(H, I, dt), dtype=dt)
+    assert cache.n_slots == 700 and cache.gu_arena.numel() > 2 ** 31
+    cache._free.reverse()  # pop() now hands out 699, 698, ...
+    name = "model.layers.3.mlp.experts"
+    w, _, _ = M.route(_zipf_logits(T, E, torch.randperm(E, generator=g), 1.1, g), k, False, dt)
+    x = torch.randn(T, H, generator=g).to(dt)
+    out = cache.forward(name, x.to(gpu_device), w.to(gpu_device), k)
+    torch.cuda.synchronize()
+    used = (w != 0).any(0).nonzero().reshape(-1).tolist()
+    slots = [cache.slot_of(name, e) for e in used]
+    assert min(slots) >= 700 - len(used) and max(slots) == 699
+    assert max(slots) * cache.gu_elems * 2 > 2 ** 32
+    check(f"out ({len(used)} experts in slots {min(slots)}..{max(slots)})", out,
+          M.experts_routed(x, w, deq[0].to(dt), deq[1].to(dt)), dt, say=_say)
+    for e in (used[0], used[-1]):
+        s = cache.slot_of(name, e)
+        assert torch.equal(cache.copy_of(s, "gate_up").cpu().view(torch.int16), deq[0][e].view(torch.int16))
+        assert torch.equal(cache.copy_of(s, "down").cpu().view(torch.int16), deq[1][e].view(torch.int16))
+
+
+def cache_slot_bytes(H, I, dt):
+    return 3 * H * I * torch.empty(0, dtype=dt).element_size()

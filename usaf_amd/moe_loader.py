@@ -157,12 +157,15 @@ class QuantizedExpertCache:
     def _nbytes(self, params: Dict[str, torch.Tensor]) -> int:
         return sum(t.numel() * t.element_size() for t in params.values())
 
-    def _dequant(self, expert_module_name: str, stream=None) -> Dict[str, torch.Tensor]:
-        """HBM dequant of a module's params with overlays applied (moe_loader.py:183-224)."""
+    def _dequant(self, expert_module_name: str, stream=None, skip=()) -> Dict[str, torch.Tensor]:
+        """HBM dequant of a module's params with overlays applied (moe_loader.py:183-224);
+        params named in ``skip`` are left out."""
         out: Dict[str, torch.Tensor] = {}
         ctx = torch.cuda.stream(stream) if stream is not None else torch.cuda.device(self._device)
         with ctx:
             for full_name, local in self._expert_to_params.get(expert_module_name, []):
+                if local in skip:
+                    continue
                 entry = self._q_dict.get(full_name)
                 if isinstance(entry, Q4Tensor):
                     t = entry.dequantize(self._dtype)
@@ -205,10 +208,10 @@ class QuantizedExpertCache:
             return {p: torch.nn.Parameter(t, requires_grad=t.requires_grad) for p, t in cached.items()}
         self.misses += 1
         if expert_module_name in self._resident:
-            # resident modules join the cache without evicting others (moe_loader.py:153-164)
+            # resident modules join the cache without evicting others (moe_loader.py:153-164);
+            # only params the resident copy lacks are dequantized
             params = self._get_resident(expert_module_name)
-            for k, v in self._dequant(expert_module_name).items():
-                params.setdefault(k, v)
+            params.update(self._dequant(expert_module_name, skip=params.keys()))
         else:
             pending = self._prefetched.pop(expert_module_name, None)
             if pending is not None:
