@@ -108,7 +108,7 @@ int usaf_hip_dequant_q4_slices(const int8_t* packed, const uint16_t* scale_f16, 
  * usaf_hip_frag_slot_elems(w_rows, K, inter) elements of out_dtype (fp16 / bf16).
  * Values are those of usaf_hip_dequant_q4; only the order differs.  inter > 0
  * marks a gate_up block (w_rows == 2 inter, SwiGLU row pairing); inter == 0 a
- * plain block such as down.  K % 128 == 0; codes 4-byte, out 16-byte aligned;
+ * plain block such as down.  K % 128 == 0; codes and out 16-byte aligned;
  * jobs naming an expert or slot out of range are skipped.
  */
 int usaf_hip_dequant_q4_slices_frag(const int8_t* packed, const uint16_t* scale_f16, const uint16_t* zero_f16,

@@ -469,63 +469,74 @@ namespace {
 // + 8 j + [0, 8): what lane l of wave w loads into register j at k-step ks.
 // Rows: inter > 0 pairs gate row n = 128 nt + 16 w + (l & 15) with up row
 // inter + n (the SwiGLU tile); inter == 0 takes row 256 nt + 32 w + (l & 31).
-// Rows past the matrix are zero.  One thread per chunk: one 32-bit code word
-// and one scale/zero pair in, one 16-byte store out (coalesced per wave).
+// Rows past the matrix are zero.  One thread per (tile row, k-step): it reads
+// the row's 32 code bytes of the k-step (two 16-byte loads) and its
+// scale/zero, and writes the 64 weights as the 8 chunks (j, l >> 5) of lane
+// l & 31; the 32 rows of a wave's unit sit in neighbouring threads, so each
+// chunk store of 32 threads covers 512 contiguous bytes.
 template <int OUT_DT>
-__global__ __launch_bounds__(256) void dequant_frag_kernel(const uint32_t* __restrict__ packed,
+__global__ __launch_bounds__(256) void dequant_frag_kernel(const uint8_t* __restrict__ packed,
                                                            const uint16_t* __restrict__ scale,
                                                            const uint16_t* __restrict__ zero, u32x4* __restrict__ out,
-                                                           int64_t n_chunks, int64_t cps, int64_t w_rows, int64_t K,
-                                                           int64_t inter, const int64_t* __restrict__ src,
+                                                           int64_t n_items, int64_t ips, int64_t cps, int64_t w_rows,
+                                                           int64_t K, int64_t inter, const int64_t* __restrict__ src,
                                                            const int64_t* __restrict__ dst, int64_t n_src,
                                                            int64_t n_dst) {
   const int64_t nk = K / 64;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < n_chunks; c += stride) {
-    const int64_t job = c / cps, cc = c - job * cps;
+  for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < n_items; it += stride) {
+    const int64_t job = it / ips, r = it - job * ips;
     const int64_t e = src[job], d = dst[job];
     if (e < 0 || e >= n_src || d < 0 || d >= n_dst) continue;
-    const int lane = (int)(cc & 63);
-    int64_t t = cc >> 6;
-    const int jf = (int)(t & 3);
-    t >>= 2;
-    const int64_t ks = t % nk;
-    t /= nk;
-    const int w = (int)(t & 7);
-    const int64_t nt = t >> 3;
+    const int l32 = (int)(r & 31);
+    const int64_t t = r >> 5;
+    const int64_t ks = t % nk, unit = t / nk;  // unit = nt * 8 + w
+    const int w = (int)(unit & 7);
+    const int64_t nt = unit >> 3;
     int64_t row;
     bool valid;
     if (inter > 0) {
-      const int64_t n = nt * 128 + 16 * w + (lane & 15);
+      const int64_t n = nt * 128 + 16 * w + (l32 & 15);
       valid = n < inter;
-      row = ((lane & 16) ? inter : 0) + n;
+      row = ((l32 & 16) ? inter : 0) + n;
     } else {
-      row = nt * 256 + 32 * w + (lane & 31);
+      row = nt * 256 + 32 * w + l32;
       valid = row < w_rows;
     }
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    u32x4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = u32x4{0u, 0u, 0u, 0u};
     if (valid) {
-      const int64_t el = (e * w_rows + row) * K + ks * 64 + 32 * (lane >> 5) + 8 * jf;  // multiple of 8
-      const uint32_t word = packed[el >> 3];
+      const int64_t el = (e * w_rows + row) * K + ks * 64;  // multiple of 64: the k-step's first element
+      const uint4 c0 = *reinterpret_cast<const uint4*>(packed + (el >> 1));
+      const uint4 c1 = *reinterpret_cast<const uint4*>(packed + (el >> 1) + 16);
+      const uint32_t words[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
       const uint16_t sb = scale[el >> 7], zb = zero[el >> 7];
       const f16 sh = __builtin_bit_cast(f16, sb), zh = __builtin_bit_cast(f16, zb);
-      uint32_t h[4];
-      dequant_word_f16(word, f16x2{sh, sh}, f16x2{zh, zh}, h);
-      if constexpr (OUT_DT == USAF_F16) {
-        v = u32x4{h[0], h[1], h[2], h[3]};
-      } else if (((sb & 0x7C00u) != 0x7C00u) && ((zb & 0x7C00u) != 0x7C00u)) {
-        v = u32x4{f16pair_to_bf16pair(h[0]), f16pair_to_bf16pair(h[1]), f16pair_to_bf16pair(h[2]),
-                  f16pair_to_bf16pair(h[3])};
-      } else {
-        uint32_t b[4];
+      const bool finite_sz = ((sb & 0x7C00u) != 0x7C00u) && ((zb & 0x7C00u) != 0x7C00u);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          b[q] = (uint32_t)f16bits_to_bf16bits((uint16_t)(h[q] & 0xFFFFu)) |
-                 ((uint32_t)f16bits_to_bf16bits((uint16_t)(h[q] >> 16)) << 16);
-        v = u32x4{b[0], b[1], b[2], b[3]};
+      for (int q = 0; q < 8; ++q) {
+        uint32_t h[4];
+        dequant_word_f16(words[q], f16x2{sh, sh}, f16x2{zh, zh}, h);
+        if constexpr (OUT_DT == USAF_F16) {
+          v[q] = u32x4{h[0], h[1], h[2], h[3]};
+        } else if (finite_sz) {
+          v[q] = u32x4{f16pair_to_bf16pair(h[0]), f16pair_to_bf16pair(h[1]), f16pair_to_bf16pair(h[2]),
+                       f16pair_to_bf16pair(h[3])};
+        } else {
+          uint32_t b2[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            b2[u] = (uint32_t)f16bits_to_bf16bits((uint16_t)(h[u] & 0xFFFFu)) |
+                    ((uint32_t)f16bits_to_bf16bits((uint16_t)(h[u] >> 16)) << 16);
+          v[q] = u32x4{b2[0], b2[1], b2[2], b2[3]};
+        }
       }
     }
-    out[d * cps + cc] = v;
+    // word q: elements 8 q + [0, 8) of the k-step = register q & 3 of lane l32 + 32 (q >> 2)
+    u32x4* o = out + d * cps + (unit * nk + ks) * 256 + l32;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[(q & 3) * 64 + 32 * (q >> 2)] = v[q];
   }
 }
 
@@ -552,21 +563,22 @@ extern "C" int usaf_hip_dequant_q4_slices_frag(const int8_t* packed, const uint1
   if (n_jobs == 0) return clear_error();
   if (!packed || !scale_f16 || !zero_f16 || !src_expert || !dst_slot || !out)
     return set_error(USAF_ERR_INVALID, "dequant_q4_slices_frag: null pointer");
-  if ((((uintptr_t)packed) & 3) || (((uintptr_t)out) & 15))
-    return set_error(USAF_ERR_INVALID, "dequant_q4_slices_frag: codes must be 4-byte and out 16-byte aligned");
-  const int64_t cps = slot_elems / 8;
-  const int64_t n_chunks = n_jobs * cps;
-  int64_t blocks = (n_chunks + 255) / 256;
+  if ((((uintptr_t)packed) & 15) || (((uintptr_t)out) & 15))
+    return set_error(USAF_ERR_INVALID, "dequant_q4_slices_frag: codes and out must be 16-byte aligned");
+  const int64_t cps = slot_elems / 8;    // 16-byte chunks per slot
+  const int64_t ips = slot_elems / 64;   // (tile row, k-step) items per slot
+  const int64_t n_items = n_jobs * ips;
+  int64_t blocks = (n_items + 255) / 256;
   const int64_t cap = (int64_t)device_cu_count() * 16;
   if (blocks > cap) blocks = cap;
   hipStream_t st = as_stream(stream);
   if (out_dtype == USAF_F16)
-    dequant_frag_kernel<USAF_F16><<<(unsigned)blocks, 256, 0, st>>>((const uint32_t*)packed, scale_f16, zero_f16,
-                                                                    (u32x4*)out, n_chunks, cps, w_rows, K, inter,
+    dequant_frag_kernel<USAF_F16><<<(unsigned)blocks, 256, 0, st>>>((const uint8_t*)packed, scale_f16, zero_f16,
+                                                                    (u32x4*)out, n_items, ips, cps, w_rows, K, inter,
                                                                     src_expert, dst_slot, n_experts, n_slots);
   else
-    dequant_frag_kernel<USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>((const uint32_t*)packed, scale_f16, zero_f16,
-                                                                     (u32x4*)out, n_chunks, cps, w_rows, K, inter,
+    dequant_frag_kernel<USAF_BF16><<<(unsigned)blocks, 256, 0, st>>>((const uint8_t*)packed, scale_f16, zero_f16,
+                                                                     (u32x4*)out, n_items, ips, cps, w_rows, K, inter,
                                                                      src_expert, dst_slot, n_experts, n_slots);
   return check_launch("dequant_q4_slices_frag");
 }
