@@ -193,6 +193,17 @@ int usaf_hip_router_fwd(const void* x, const void* w, int64_t T, int64_t E, int6
  * dlogits [T, E] and x [T, H] row-major 16-bit; E and H multiples of 8, 16-byte
  * aligned; workspace fp32 [usaf_hip_router_dw_ws_floats(T, E, H)].
  */
+/*
+ * Grad-input of the router's F.linear (qwen3moe_dml.py:72):
+ *   accumulate == 0: dx = dtype(dlogits @ W)
+ *   accumulate != 0: dx = dtype(dtype(dlogits @ W) + dx)
+ * dlogits [T, E], W [E, H], dx [T, H] in the dtype, fp32 accumulation.  The
+ * accumulating form adds the gradient the experts' branch gave the same hidden
+ * states (on entry in dx) with autograd's two roundings: the matmul's, then the
+ * accumulation's.  Needs E % 16 == 0, H % 8 == 0, 16-byte aligned dlogits, W, dx.
+ */
+int usaf_hip_router_dx(const void* dlogits, const void* w, int64_t T, int64_t E, int64_t H, int32_t dtype, void* dx,
+                       int32_t accumulate, void* stream);
 int64_t usaf_hip_router_dw_ws_floats(int64_t T, int64_t E, int64_t H);
 int usaf_hip_router_dw(const void* dlogits, const void* x, int64_t T, int64_t E, int64_t H, int32_t dtype, void* dw,
                        float* workspace, void* stream);

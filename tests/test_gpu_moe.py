@@ -968,6 +968,37 @@ def test_router_dw_vs_fp64(gpu_device, T, E, H, dtype):
     assert torch.all((got - ref).abs() <= tol)
 
 
+@pytest.mark.parametrize("T,E,H", [(4096, 128, 2048), (300, 48, 136), (1, 16, 8), (129, 1024, 264)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_router_dx_vs_fp64(gpu_device, T, E, H, dtype, accumulate):
+    """usaf_hip_router_dx: dtype(dlogits @ W), or dtype(dtype(dlogits @ W) + dx)
+    (autograd's matmul rounding, then its accumulation with the experts' branch),
+    against the fp64 product: one rounding per step plus the fp32 summation bound."""
+    _say(f"router grad-input T={T} E={E} H={H} {dtype} accumulate={accumulate}")
+    from usaf_amd import _native as N
+    g = torch.Generator().manual_seed(T + 3 * E + H)
+    dl = torch.randn(T, E, generator=g).to(dtype)
+    w = (torch.randn(E, H, generator=g) / E ** 0.5).to(dtype)
+    dx0 = torch.randn(T, H, generator=g).to(dtype)
+    dl_d, w_d = dl.to(gpu_device), w.to(gpu_device)
+    dx = dx0.to(gpu_device) if accumulate else torch.full((T, H), 7.0, dtype=dtype, device=gpu_device)
+    N.call("usaf_hip_router_dx", dl_d.data_ptr(), w_d.data_ptr(), T, E, H, N.dtype_code(dtype), dx.data_ptr(),
+           1 if accumulate else 0, N.stream_ptr(gpu_device))
+    torch.cuda.synchronize()
+    exact = dl.double() @ w.double()
+    mag = dl.double().abs() @ w.double().abs()
+    eps = torch.finfo(dtype).eps
+    ref = exact + dx0.double() if accumulate else exact
+    tol = eps * (exact.abs() + ref.abs()) + E * 2.0 ** -23 * mag + 1e-30
+    got = dx.cpu().double()
+    assert torch.all((got - ref).abs() <= tol)
+    if accumulate:
+        # the two roundings: the fp64 product rounded to the dtype, plus dx, rounded
+        two = (exact.to(dtype).float() + dx0.float()).to(dtype)
+        assert (dx.cpu() != two).float().mean() < 1e-2
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_momentum_sgd_matches_torch(gpu_device, dtype):
     _say(f"MomentumSGD vs torch.optim.SGD single-tensor, 3 steps from equal states, {dtype}")

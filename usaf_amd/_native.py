@@ -37,6 +37,7 @@ _SIGNATURES: dict[str, list] = {
     "usaf_hip_dequant_q4_at": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p],
     "usaf_hip_topk_abs": [_c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p],
     "usaf_hip_dequant_q4_slices": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i32, _c_p],
+    "usaf_hip_router_dx": [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i32, _c_p],
     "usaf_hip_dequant_q4_slices_frag": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64,
                                         _c_p, _c_i32, _c_p],
     "usaf_hip_moe_gate_up_fwd_slots": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64,

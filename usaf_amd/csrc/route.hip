@@ -569,6 +569,92 @@ __global__ __launch_bounds__(256) void router_dw_kernel(const uint16_t* __restri
   }
 }
 
+// ---- router grad-input ------------------------------------------------------------
+// dx[t, h] = dtype( dtype(sum_e fp32(dl[t, e]) * fp32(W[e, h])) + fp32(dx[t, h]) )
+// (accumulate) or dtype(sum ...) (no accumulate): the grad-input of the router's
+// F.linear (qwen3moe_dml.py:72) -- autograd's matmul, rounded to the dtype --
+// plus, when accumulating, the gradient the experts' branch gave the same hidden
+// states, added and rounded once more as autograd's accumulation of the two.
+// A block computes 128 tokens x 128 columns with v_mfma_f32_32x32x16; wave w
+// owns tokens [32 w, 32 w + 32) x all 128 columns (4 accumulator blocks).  The
+// A fragments (8 consecutive experts of a token row) come straight from global
+// memory; W's 64-expert chunks are transposed through LDS (tt_write) so that a
+// B fragment (8 consecutive experts of one column) is one 16-byte LDS read.
+template <int DT>
+__global__ __launch_bounds__(256) void router_dx_kernel(const uint16_t* __restrict__ dl, const uint16_t* __restrict__ w,
+                                                        int64_t T, int E, int64_t H, uint16_t* __restrict__ dx,
+                                                        int accumulate) {
+#pragma clang fp contract(off)
+  __shared__ __align__(16) uint32_t sB[2][TT_DWORDS];  // columns h0 + [0, 64), h0 + [64, 128)
+  __shared__ __align__(16) uint16_t sC[128 * 136];      // the rounded tile, 128 tokens x 128 columns (+8 pad)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t h0 = (int64_t)blockIdx.x * 128;
+  const int64_t t0 = (int64_t)blockIdx.y * 128;
+  const int sp = tid >> 3, cg = tid & 7;  // writer cell: experts 2 sp, 2 sp + 1 of the chunk; 8 columns at 8 cg
+  const int64_t ta = t0 + 32 * wave + (lane & 31);  // this lane's A row (token)
+  const bool t_ok = ta < T;
+  rdw_f32x16 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = rdw_f32x16{};
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    uint4 rb[2][2];  // [column half][expert of the pair]
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int e = e0 + 2 * sp + u;
+        const int64_t h = h0 + 64 * q + 8 * cg;
+        rb[q][u] = (e < E && h < H) ? *reinterpret_cast<const uint4*>(w + (int64_t)e * H + h) : make_uint4(0, 0, 0, 0);
+      }
+    __syncthreads();  // the previous chunk's fragment reads are done
+#pragma unroll
+    for (int q = 0; q < 2; ++q) tt_write(sB[q], sp, cg, rb[q][0], rb[q][1]);
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < 64; kb += 16) {
+      const int e = e0 + kb + 8 * (lane >> 5);  // E % 16 == 0: e < E implies e + 8 <= E
+      const uint4 a = (t_ok && e < E) ? *reinterpret_cast<const uint4*>(dl + ta * E + e) : make_uint4(0, 0, 0, 0);
+      const int sg = (kb >> 3) + (lane >> 5);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int hb = 32 * j + (lane & 31);
+        acc[j] = rdw_mfma<DT>(a, tt_read(sB[hb >> 6], hb & 63, sg), acc[j]);
+      }
+    }
+  }
+  // acc[j][r]: token 32 wave + 8 (r >> 2) + 4 (lane >> 5) + (r & 3), column 32 j + (lane & 31) of
+  // the tile; rounded to the dtype into LDS, then out (and, accumulating, dx in)
+  // as 16-byte row chunks
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int tl = 32 * wave + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), hl = 32 * j + (lane & 31);
+      sC[tl * 136 + hl] = DT == USAF_F16 ? f32_to_f16_bits(acc[j][r]) : f32_to_bf16_bits(acc[j][r]);
+    }
+  __syncthreads();
+  for (int c = tid; c < 128 * 16; c += 256) {
+    const int tl = c >> 4, hc = 8 * (c & 15);
+    const int64_t t = t0 + tl, h = h0 + hc;
+    if (t >= T || h >= H) continue;  // H % 8 == 0: a chunk is inside or outside
+    const uint4 g = *reinterpret_cast<const uint4*>(&sC[tl * 136 + hc]);
+    uint4* const o = reinterpret_cast<uint4*>(dx + t * H + h);
+    if (accumulate) {
+      const uint4 d = *o;
+      const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, dw[4] = {d.x, d.y, d.z, d.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x2 a = unpack2<DT>(gw[q]), b = unpack2<DT>(dw[q]);
+        ow[q] = pack2<DT>(a.x + b.x, a.y + b.y);
+      }
+      *o = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    } else {
+      *o = g;
+    }
+  }
+}
+
 // ---- router forward: the logits GEMM ------------------------------------------------
 // logits[t, e] = dtype( sum_h x[t, h] * W[e, h] ), the router's F.linear
 // (qwen3moe_dml.py:72).  A block computes 32 tokens x 32 experts with
@@ -885,6 +971,28 @@ extern "C" int usaf_hip_router_dw(const void* dlogits, const void* x, int64_t T,
     router_dw_reduce_kernel<USAF_F16><<<rb, 256, 0, st>>>(workspace, (int)ks, n, (uint16_t*)dw);
   }
   return check_launch("router_dw");
+}
+
+extern "C" int usaf_hip_router_dx(const void* dlogits, const void* w, int64_t T, int64_t E, int64_t H, int32_t dtype,
+                                  void* dx, int32_t accumulate, void* stream) {
+  if (T < 0 || E <= 0 || H <= 0) return set_error(USAF_ERR_INVALID, "router_dx: bad sizes");
+  if (dtype != USAF_F16 && dtype != USAF_BF16) return set_error(USAF_ERR_INVALID, "router_dx: dtype must be fp16/bf16");
+  if (T == 0) return clear_error();
+  if (!dlogits || !w || !dx) return set_error(USAF_ERR_INVALID, "router_dx: null pointer");
+  if (E % 16 != 0 || H % 8 != 0 || (((uintptr_t)dlogits | (uintptr_t)w | (uintptr_t)dx) & 15))
+    return set_error(USAF_ERR_UNSUPPORTED, "router_dx: needs E %% 16 == 0, H %% 8 == 0 and 16-byte aligned operands");
+  if (E > 0x7fffffff || H > 0x7fffffff) return set_error(USAF_ERR_INVALID, "router_dx: too large");
+  const int64_t tiles_h = (H + 127) / 128, tiles_t = (T + 127) / 128;
+  if (tiles_h > 0x7fffffff || tiles_t > 65535) return set_error(USAF_ERR_INVALID, "router_dx: too large");
+  hipStream_t st = as_stream(stream);
+  const dim3 grid((unsigned)tiles_h, (unsigned)tiles_t);
+  if (dtype == USAF_BF16)
+    router_dx_kernel<USAF_BF16><<<grid, 256, 0, st>>>((const uint16_t*)dlogits, (const uint16_t*)w, T, (int)E, H,
+                                                      (uint16_t*)dx, accumulate ? 1 : 0);
+  else
+    router_dx_kernel<USAF_F16><<<grid, 256, 0, st>>>((const uint16_t*)dlogits, (const uint16_t*)w, T, (int)E, H,
+                                                     (uint16_t*)dx, accumulate ? 1 : 0);
+  return check_launch("router_dx");
 }
 
 extern "C" int usaf_hip_router_fwd(const void* x, const void* w, int64_t T, int64_t E, int64_t H, int32_t dtype,

@@ -62,6 +62,21 @@ __global__ __launch_bounds__(256) void gather_transpose_kernel(const uint16_t* _
   }
 }
 
+// Value of lane (l + R) mod 16 of the lane's 16-lane row (DPP row_ror), so that
+// four adds with R = 8, 4, 2, 1 leave the row's sum in every lane of it: one
+// VALU instruction per step instead of an LDS-routed ds_bpermute.
+template <int R>
+__device__ __forceinline__ float row_ror_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + R, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += row_ror_f32<8>(v);
+  v += row_ror_f32<4>(v);
+  v += row_ror_f32<2>(v);
+  v += row_ror_f32<1>(v);
+  return v;
+}
+
 // Products of two 16-bit pairs accumulated in fp32 (v_dot2_f32_bf16 / _f16).
 template <int DT>
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -129,8 +144,7 @@ __global__ __launch_bounds__(256) void sddmm_kernel(const uint16_t* __restrict__
         }
       }
     }
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+    acc = row16_sum(acc);
     if (gl == 0) {
       const int64_t pos = pos_map ? pos_map[p] : p;
       compact[pos] += round_to<DT>(acc);
@@ -475,8 +489,7 @@ __global__ __launch_bounds__(256) void sddmm_blocked_kernel(const uint16_t* __re
         acc = dot2<DT>(a.z, c.z, acc);
         acc = dot2<DT>(a.w, c.w, acc);
       }
-#pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+      acc = row16_sum(acc);
       if (gl == j) my_sum = round_to<DT>(acc);
     }
     // positions with an invalid row code or column: left alone when accumulating, 0 otherwise

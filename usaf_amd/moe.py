@@ -485,7 +485,7 @@ class RoutedExpertsFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hs: torch.Tensor, weights: torch.Tensor, ew: ExpertWeights, capture,
                 w_gate_up: Optional[torch.Tensor] = None, w_down: Optional[torch.Tensor] = None,
-                slots: Optional[Tuple[int, torch.Tensor]] = None):
+                slots: Optional[Tuple[int, torch.Tensor]] = None, link: Optional["HsGradLink"] = None):
         # w_gate_up / w_down: the dense expert Parameters the kernels' weights were
         # taken from, passed only so that autograd delivers their gradients;
         # slots: (capacity, overflow) for bucketing without a host read (bucket_by_expert)
@@ -527,6 +527,7 @@ class RoutedExpertsFn(torch.autograd.Function):
         out = combine(y, weights, b.pair_slot, dt)
         ctx.ew = ew
         ctx.capture = capture
+        ctx.link = link
         ctx.b = b
         ctx.act_blk = act_blk
         ctx.wdt = (None if w_gate_up is None else w_gate_up.dtype, None if w_down is None else w_down.dtype)
@@ -601,7 +602,12 @@ class RoutedExpertsFn(torch.autograd.Function):
             _capture(capture, "gate_up_proj", dgu, hs, b.token_idx, b, (E, 2 * I, H), dt)
         if want_gu:
             _dense_weight_grad(d_wgu, dgu, hs, b.token_idx, b)
-        return dhs, dweights, None, None, d_wgu, d_wdn, None
+        if ctx.link is not None and dweights is not None:
+            # the router's backward (next, it needs dweights) adds its grad-input to
+            # this one in the same kernel: one sum instead of autograd's extra add
+            ctx.link.dx = dhs
+            dhs = None
+        return dhs, dweights, None, None, d_wgu, d_wdn, None, None
 
 
 def _no_overlay(ew: ExpertWeights, which: str) -> None:
@@ -678,19 +684,33 @@ def slot_major(x: torch.Tensor, rows: Optional[torch.Tensor] = None) -> torch.Te
     return out[:, :S]
 
 
+class HsGradLink:
+    """Hands the experts' hidden-state gradient from RoutedExpertsFn.backward to
+    RouterFn.backward of the same block (moe_block), which adds the router's
+    grad-input to it in one kernel (usaf_hip_router_dx) with autograd's
+    roundings; the experts' backward then returns no gradient for the hidden
+    states, the router's returns the sum."""
+
+    def __init__(self) -> None:
+        self.dx: Optional[torch.Tensor] = None
+
+
 def routed_experts(hs: torch.Tensor, weights: torch.Tensor, experts: ExpertWeights, capture=None,
                    weight_params: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
-                   slot_capacity: Optional[int] = None, overflow: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   slot_capacity: Optional[int] = None, overflow: Optional[torch.Tensor] = None,
+                   link: Optional[HsGradLink] = None) -> torch.Tensor:
     """Experts forward with the reference signature's data: hs [T, H], weights [T, E].
 
     weight_params: optional (gate_up, down) dense Parameters that ``experts``
     holds (possibly as converted copies); when they require grad they receive
     dense gradients, as the reference's autograd through the expert loop.
     slot_capacity / overflow: bucket without reading the slot count back to the
-    host (graph capture, no stall before the GEMMs); see bucket_by_expert."""
+    host (graph capture, no stall before the GEMMs); see bucket_by_expert.
+    link: set by moe_block when the router's backward takes the hidden-state
+    gradient of both branches (HsGradLink)."""
     wg, wd = weight_params if weight_params is not None else (None, None)
     slots = None if slot_capacity is None and overflow is None else (slot_capacity, overflow)
-    return RoutedExpertsFn.apply(hs, weights, experts, capture, wg, wd, slots)
+    return RoutedExpertsFn.apply(hs, weights, experts, capture, wg, wd, slots, link)
 
 
 class RouteTopKFn(torch.autograd.Function):
@@ -751,10 +771,12 @@ class RouterFn(torch.autograd.Function):
     """The router of qwen3moe_dml.py:72-83 from one call (usaf_hip_router_fwd):
     logits = F.linear(hs, W) in the activation dtype, fp32 softmax, top-k
     threshold mask, optional renormalisation.  Backward: usaf_hip_route_topk_bwd to
-    dlogits, the library GEMM for dhs, usaf_hip_router_dw for dW."""
+    dlogits, usaf_hip_router_dx for dhs (with the experts' dhs added in the same
+    kernel when moe_block links the two), usaf_hip_router_dw for dW."""
 
     @staticmethod
-    def forward(ctx, x: torch.Tensor, w: torch.Tensor, top_k: int, norm: bool, out_dtype: torch.dtype):
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, top_k: int, norm: bool, out_dtype: torch.dtype,
+                link: Optional[HsGradLink] = None):
         T, H = x.shape
         E = w.shape[0]
         logits = torch.empty(T, E, dtype=x.dtype, device=x.device)
@@ -763,7 +785,7 @@ class RouterFn(torch.autograd.Function):
         N.call("usaf_hip_router_fwd", x.data_ptr(), w.data_ptr(), T, E, H, N.dtype_code(x.dtype), int(top_k),
                1 if norm else 0, logits.data_ptr(), weights.data_ptr(), N.dtype_code(out_dtype), probs.data_ptr(),
                N.stream_ptr(x.device))
-        ctx.top_k, ctx.norm = top_k, norm
+        ctx.top_k, ctx.norm, ctx.link = top_k, norm, link
         ctx.save_for_backward(x, w, probs)
         return weights
 
@@ -775,9 +797,23 @@ class RouterFn(torch.autograd.Function):
         dlogits = torch.empty(T, E, dtype=x.dtype, device=x.device)
         N.call("usaf_hip_route_topk_bwd", dweights.data_ptr(), N.dtype_code(dweights.dtype), probs.data_ptr(), T, E,
                ctx.top_k, 1 if ctx.norm else 0, dlogits.data_ptr(), N.dtype_code(x.dtype), N.stream_ptr(x.device))
-        dx = torch.mm(dlogits, w) if ctx.needs_input_grad[0] else None
+        dx = None
+        if ctx.needs_input_grad[0]:
+            # dx = dtype(dlogits @ W), plus (link) the experts' gradient of the same
+            # hidden states with autograd's accumulation rounding
+            link = ctx.link
+            acc = link is not None and link.dx is not None
+            if acc:
+                dx, link.dx = link.dx, None
+            elif E % 16 == 0:
+                dx = torch.empty(T, x.shape[1], dtype=x.dtype, device=x.device)
+            else:  # shapes the kernel does not take (moe_block links only E % 16 == 0)
+                dx = torch.mm(dlogits, w)
+            if acc or E % 16 == 0:
+                N.call("usaf_hip_router_dx", dlogits.data_ptr(), w.data_ptr(), T, E, x.shape[1],
+                       N.dtype_code(x.dtype), dx.data_ptr(), 1 if acc else 0, N.stream_ptr(x.device))
         dw = _router_dw(x, dlogits, w.dtype) if ctx.needs_input_grad[1] else None
-        return dx, dw, None, None, None
+        return dx, dw, None, None, None, None
 
 
 def _router_fused_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
@@ -805,8 +841,11 @@ def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_to
     slots past the routed pairs cost no GEMM work."""
     shape = hs.shape
     x = hs.reshape(-1, shape[-1])
+    link = None
     if _router_fused_ok(x, router_weight):
-        weights = RouterFn.apply(x, router_weight, top_k, norm_topk_prob, x.dtype)
+        # the router's backward sums both branches' hidden-state gradients (HsGradLink)
+        link = HsGradLink() if (x.requires_grad and router_weight.shape[0] % 16 == 0) else None
+        weights = RouterFn.apply(x, router_weight, top_k, norm_topk_prob, x.dtype, link)
     else:
         if _router_dw_ok(x, router_weight):
             logits = RouterLinearFn.apply(x, router_weight)
@@ -814,5 +853,5 @@ def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_to
             logits = torch.nn.functional.linear(x, router_weight)
         weights = RouteTopKFn.apply(logits, top_k, norm_topk_prob, x.dtype)
     cap = None if overflow is None else x.shape[0] * min(top_k + 1, router_weight.shape[0])
-    out = routed_experts(x, weights, experts, capture, slot_capacity=cap, overflow=overflow)
+    out = routed_experts(x, weights, experts, capture, slot_capacity=cap, overflow=overflow, link=link)
     return out.view(shape)
