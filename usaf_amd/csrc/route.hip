@@ -596,8 +596,8 @@ __global__ __launch_bounds__(256) void router_dx_kernel(const uint16_t* __restri
   rdw_f32x16 acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = rdw_f32x16{};
-  for (int e0 = 0; e0 < E; e0 += 64) {
-    uint4 rb[2][2];  // [column half][expert of the pair]
+  uint4 rb[2][2];  // W rows of the next chunk: [column half][expert of the pair]
+  auto load_w = [&](int e0) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -606,19 +606,28 @@ __global__ __launch_bounds__(256) void router_dx_kernel(const uint16_t* __restri
         const int64_t h = h0 + 64 * q + 8 * cg;
         rb[q][u] = (e < E && h < H) ? *reinterpret_cast<const uint4*>(w + (int64_t)e * H + h) : make_uint4(0, 0, 0, 0);
       }
+  };
+  load_w(0);
+  for (int e0 = 0; e0 < E; e0 += 64) {
     __syncthreads();  // the previous chunk's fragment reads are done
 #pragma unroll
     for (int q = 0; q < 2; ++q) tt_write(sB[q], sp, cg, rb[q][0], rb[q][1]);
-    __syncthreads();
+    // the chunk's four A fragments (E % 16 == 0: e < E implies e + 8 <= E)
+    uint4 a[4];
 #pragma unroll
-    for (int kb = 0; kb < 64; kb += 16) {
-      const int e = e0 + kb + 8 * (lane >> 5);  // E % 16 == 0: e < E implies e + 8 <= E
-      const uint4 a = (t_ok && e < E) ? *reinterpret_cast<const uint4*>(dl + ta * E + e) : make_uint4(0, 0, 0, 0);
-      const int sg = (kb >> 3) + (lane >> 5);
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int e = e0 + 16 * s4 + 8 * (lane >> 5);
+      a[s4] = (t_ok && e < E) ? *reinterpret_cast<const uint4*>(dl + ta * E + e) : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    if (e0 + 64 < E) load_w(e0 + 64);  // the next chunk's W rows in flight during these MFMAs
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int sg = 2 * s4 + (lane >> 5);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int hb = 32 * j + (lane & 31);
-        acc[j] = rdw_mfma<DT>(a, tt_read(sB[hb >> 6], hb & 63, sg), acc[j]);
+        acc[j] = rdw_mfma<DT>(a[s4], tt_read(sB[hb >> 6], hb & 63, sg), acc[j]);
       }
     }
   }
