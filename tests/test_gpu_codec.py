@@ -177,3 +177,70 @@ def test_state_dict_wrappers(gpu_device):
     p_o, s_o, z_o = oracle.quantize(sd["a"].float().numpy().reshape(-1), 128)
     assert np.array_equal(_bits(dd["a"]), oracle.dequant(p_o, s_o, z_o, 2100, 128))
     assert dd["a"].shape == (300, 7)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+def test_dequant_slices_jobs(gpu_device, out_dtype):
+    """usaf_hip_dequant_q4_slices: job j dequantizes slice src[j] into arena slot
+    dst[j] (natural order), bit-exact against the oracle's dequant of that slice;
+    slots no job names keep their contents, jobs naming a slice or slot out of
+    range are skipped."""
+    from usaf_amd import _native as N
+    _say(f"slice dequant jobs into an arena, {out_dtype}")
+    E, rows, cols = 6, 64, 256
+    slice_elems = rows * cols
+    g = torch.Generator().manual_seed(31)
+    w = (torch.randn(E, rows, cols, generator=g) * 0.02).half().to(gpu_device)
+    p, s, z, shape = Q.quantize_4bit(w, 128)
+    n_slots = 5
+    arena = torch.full((n_slots, slice_elems), 7.0, dtype=out_dtype, device=gpu_device)
+    src = torch.tensor([4, 0, 2, 9, 1], dtype=torch.int64)   # 9: past the tensor
+    dst = torch.tensor([0, 3, 1, 2, 7], dtype=torch.int64)   # 7: past the arena
+    src_d, dst_d = src.to(gpu_device), dst.to(gpu_device)
+    N.call("usaf_hip_dequant_q4_slices", p.data_ptr(), s.data_ptr(), z.data_ptr(), p.shape[0], slice_elems,
+           len(src), src_d.data_ptr(), dst_d.data_ptr(), n_slots, arena.data_ptr(), N.dtype_code(out_dtype),
+           N.stream_ptr(gpu_device))
+    torch.cuda.synchronize()
+    pc, sc, zc = p.cpu().numpy(), _bits(s), _bits(z)
+    gps = slice_elems // 128
+    odt = "bf16" if out_dtype == torch.bfloat16 else "f16"
+    filled = set()
+    for e, d in zip(src.tolist(), dst.tolist()):
+        if e >= E or d >= n_slots:
+            continue
+        ref = oracle.dequant(pc[e * gps:(e + 1) * gps], sc[e * gps:(e + 1) * gps], zc[e * gps:(e + 1) * gps],
+                             slice_elems, 128, out_dtype=odt)
+        assert np.array_equal(_bits(arena[d]), ref), (e, d)
+        filled.add(d)
+    for d in set(range(n_slots)) - filled:
+        assert torch.all(arena[d] == 7.0), d
+
+
+@pytest.mark.parametrize("w_rows,K,inter", [(384, 128, 0), (384, 256, 192), (256, 128, 128)])
+def test_dequant_slices_frag_layout(gpu_device, w_rows, K, inter):
+    """usaf_hip_dequant_q4_slices_frag: the dequant of each named expert in the
+    fragment order of the slot GEMMs (padding rows zero), bit-exact against
+    the oracle's dequant permuted by the layout map; jobs out of range skipped."""
+    from usaf_amd import _native as N
+    from usaf_amd.expert_cache import frag_chunk_index
+    _say(f"fragment-order fill w_rows={w_rows} K={K} inter={inter}")
+    E = 3
+    g = torch.Generator().manual_seed(w_rows + K + inter)
+    w = (torch.randn(E, w_rows, K, generator=g) * 0.02).half().to(gpu_device)
+    p, s, z, shape = Q.quantize_4bit(w, 128)
+    slot = int(N.load().usaf_hip_frag_slot_elems(w_rows, K, inter))
+    n_slots = 3
+    arena = torch.full((n_slots, slot), 7.0, dtype=torch.float16, device=gpu_device)
+    src = torch.tensor([2, 0, 5], dtype=torch.int64, device=gpu_device)  # 5: past the tensor
+    dst = torch.tensor([0, 2, 1], dtype=torch.int64, device=gpu_device)
+    N.call("usaf_hip_dequant_q4_slices_frag", p.data_ptr(), s.data_ptr(), z.data_ptr(), E, w_rows, K, inter, 3,
+           src.data_ptr(), dst.data_ptr(), n_slots, arena.data_ptr(), N.F16, N.stream_ptr(gpu_device))
+    torch.cuda.synchronize()
+    idx = frag_chunk_index(w_rows, K, inter)
+    ref_all = oracle.dequant(p.cpu().numpy(), _bits(s), _bits(z), E * w_rows * K, 128).reshape(E, -1, 8)
+    for e, d in ((2, 0), (0, 2)):
+        got = _bits(arena[d]).reshape(-1, 8)
+        keep = (idx >= 0).numpy()
+        assert np.array_equal(got[keep], ref_all[e][idx[idx >= 0].numpy()])
+        assert np.all(got[~keep] == 0)
+    assert torch.all(arena[1] == 7.0)

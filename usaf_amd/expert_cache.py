@@ -13,7 +13,7 @@ layers of Qwen3-30B-A3B) and the copies are per expert:
   (layer, expert) in the given order -- a hit moves the key to the most
   recent end, a miss takes a free slot or evicts the least recently used key
   -- and fills every missed slot with one batched dequant launch per tensor
-  (usaf_hip_dequant_q4_slices), reading the 4-bit slices from HBM;
+  (usaf_hip_dequant_q4_slices_frag), reading the 4-bit slices from HBM;
 * ``forward`` buckets the tokens first and touches only the experts the
   routing selected (one host read of the per-expert counts): a copy is made
   on demand, when an expert is used and missing, as the reference dequantizes
