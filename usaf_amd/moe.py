@@ -829,8 +829,10 @@ def _router_dw_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
 
 def moe_block(hs: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_topk_prob: bool,
               experts: ExpertWeights, capture=None, overflow: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """qwen3moe_dml.py:67-86: router F.linear (library GEMM), routing kernel,
-    routed experts; hs [B, S, H] or [T, H].
+    """qwen3moe_dml.py:67-86: the router (RouterFn: logits MFMA kernel and
+    routing kernel; RouterLinearFn + RouteTopKFn for shapes it does not take),
+    the routed experts; hs [B, S, H] or [T, H].  The two branches' gradients of
+    the hidden states are summed by the router's grad-input kernel (HsGradLink).
 
     overflow: optional int32 device tensor.  Given, the experts are bucketed
     into T * (top_k + 1) slots with no host read of the slot count, and
