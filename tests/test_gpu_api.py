@@ -525,3 +525,51 @@ def test_olmoe_streaming_capture(gpu_device):
     p = dict(model.named_parameters())["model.layers.0.mlp.experts.down_proj"]
     assert torch.allclose(p.grad, g_before * 0.5)
     assert model._stream_state["max"] == 1 and model._stream_state["resident"] == 0
+
+
+def test_patched_olmoe_block_real_shape(gpu_device):
+    """The OLMoE-1B-7B MoE layer shape (hidden 2048, intermediate 1024, 64
+    experts, top-8): the patched block (dense fp32 expert Parameters, bf16 MFMA,
+    fp32 accumulation): the output against the routed loop at the same rounding
+    points (normwise and elementwise bars), and the output and the dense
+    expert-weight gradients against the reference's fp32 loop with autograd
+    (normwise bar)."""
+    _say("patch_olmoe_for_dml at the OLMoE layer shape: E=64 H=2048 I=1024 k=8, T=256, bf16")
+    from parity import check
+    from usaf_amd.olmoe_dml import patch_olmoe_for_dml
+    patch_olmoe_for_dml()
+    torch.set_num_threads(16)
+    E, H, I, k = 64, 2048, 1024, 8
+    block = _tiny_olmoe(E=E, H=H, I=I, k=k, seed=21)
+    block.gate.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(22)
+    hs = torch.randn(2, 128, H, generator=g).to(torch.bfloat16)
+    dout = torch.randn(2, 128, H, generator=g).to(torch.bfloat16)
+    wg = block.experts.gate_up_proj.detach().clone().requires_grad_(True)
+    wd = block.experts.down_proj.detach().clone().requires_grad_(True)
+    x = hs.float().reshape(-1, H)
+    block = block.to(gpu_device)
+    xg = hs.to(gpu_device).requires_grad_(True)
+    # the oracle routes from the block's own logits (the GPU's F.linear): routing is
+    # bit-exact given the logits, and a near-tie flipped by the summation order of a
+    # CPU product would change whole tokens
+    with torch.no_grad():
+        logits = torch.nn.functional.linear(xg.reshape(-1, H), block.gate.weight).float().cpu()
+    w, _, _ = M.route(logits, k, False, torch.bfloat16)
+    ref = M.experts_routed(x, w.float(), wg, wd)
+    ref.backward(dout.float().reshape(-1, H))
+    out = block(xg)
+    out.backward(dout.to(gpu_device))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and out.shape == hs.shape
+    # the same computation at the GPU's rounding points (bf16 operands and
+    # intermediates, fp32 accumulation): both bars
+    with torch.no_grad():
+        ref16 = M.experts_routed(hs.reshape(-1, H), w, wg.detach().to(torch.bfloat16), wd.detach().to(torch.bfloat16))
+    check("out vs the bf16 routed loop", out.reshape(-1, H), ref16, torch.bfloat16, say=_say)
+    # the reference's fp32 expert math (olmoe_dml.py:10-33): within the bf16 normwise bar
+    for name, got, r in (("out", out.reshape(-1, H), ref), ("dW gate_up", block.experts.gate_up_proj.grad, wg.grad),
+                         ("dW down", block.experts.down_proj.grad, wd.grad)):
+        e = rel_err(got, r)
+        _say(f"  {name} vs the fp32 loop: normwise {e:.2e} (bar 1e-2)")
+        assert e <= 1e-2, name
