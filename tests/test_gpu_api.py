@@ -269,7 +269,9 @@ def test_fused_overlays_follow_reselect(gpu_device, resident):
     overlays (:603-608) followed by sync_resident: the fused view is rebuilt on
     the new positions.  Dropped positions read the 4-bit base for a streamed
     tensor (dequant + overlays, moe_loader.py:183-224) and keep their last
-    trained value for a resident one (in-place scatter, moe_loader.py:411-443)."""
+    trained value for a resident one (in-place scatter, moe_loader.py:411-443).
+    Masters changed without a sync reach the forward after evict_all, as the
+    reference's re-dequant with the current overlay values does."""
     _say(f"fused overlays through start-up, sync and a same-size reselect, resident={resident}")
     from parity import check
     from usaf_amd.importance import reselect_active
@@ -339,6 +341,15 @@ def test_fused_overlays_follow_reselect(gpu_device, resident):
             # the resident copy the reference would multiply holds the same weights
             res = cache._resident["model.layers.0.mlp.experts"][n.rsplit(".", 1)[1]]
             assert torch.equal(_bits(res), _bits(w_new[n]))
+    # masters changed in place with no sync: the reference's cache keeps a module's
+    # dequantized copy until it is evicted, then dequantizes it again with the
+    # overlays' current values (moe_loader.py:183-247)
+    for n in names:
+        new_masters[n].data.add_(0.03)
+    run_and_check(w_new, "changed masters, not evicted")
+    cache.evict_all()
+    run_and_check({n: _scattered(w_new[n], new_active[n], new_masters[n]) for n in names},
+                  "changed masters after evict_all")
 
 
 def test_fused_overlay_dense_fallback_for_clustered_masks(gpu_device):

@@ -106,6 +106,11 @@ class QuantizedExpertCache:
         # built from ``overlays`` / sync_resident for this activation dtype
         self.fused_overlays: Dict[str, "FusedOverlay"] = {}
         self.fused_dtype: Optional[torch.dtype] = None
+        # fused views whose values were written from the masters since the last
+        # evict_all: the reference re-applies ``overlays`` with their current values
+        # whenever a module is dequantized again after an eviction, so a fused view
+        # not in this set takes the current values at its next access
+        self._fused_fresh: set = set()
         # optional per-expert LRU of dequantized copies (make_slot_cache), used by
         # forwards that need no gradients through layers without trained values
         self.slot_cache: Optional[ExpertSlotCache] = None
@@ -322,13 +327,15 @@ class QuantizedExpertCache:
     def _sync_one(self, fname: str, aidx: torch.Tensor, vals, refresh: bool) -> None:
         """Make the fused view of ``fname`` hold ``vals`` at ``aidx``: refresh the
         values when the positions are the ones it was built for (``refresh``, or
-        when ``vals`` is another tensor than last time), otherwise rebuild it."""
+        when ``vals`` is another tensor than last time), otherwise rebuild it.
+        The view then counts as written since the last evict_all."""
         entry = self._fused_target(fname)
         if entry is None:
             return
         fo = self.fused_overlays.get(fname)
         v = vals.data if isinstance(vals, torch.nn.Parameter) else vals
         v = v.detach().reshape(-1).to(device=self._device, dtype=torch.float32).contiguous()
+        self._fused_fresh.add(fname)
         if fo is not None and fo.same_positions(aidx):
             if refresh or fo.vals_src is not vals:
                 fo.refresh(v)
@@ -350,14 +357,17 @@ class QuantizedExpertCache:
     def _fused_from_overlays(self, expert_module_name: str) -> None:
         """Before a fused forward: the trained values set in ``overlays`` (the
         trainer sets them at start-up, after a resume and after a reselect,
-        train.py:467, 607) reach the fused view of each 4-bit tensor; values
-        already synced (sync_resident) are not rewritten."""
+        train.py:467, 607) reach the fused view of each 4-bit tensor, with the
+        values they hold now when the view was not written since the last
+        evict_all (the reference dequantizes an evicted module again with the
+        current overlay values, moe_loader.py:183-247); a view written since
+        (sync_resident, an earlier access) is not rewritten."""
         if self.fused_dtype is None:
             return
         for full_name, _ in self._expert_to_params.get(expert_module_name, []):
             ov = self.overlays.get(full_name)
             if ov is not None:
-                self._sync_one(full_name, ov[0], ov[1], refresh=False)
+                self._sync_one(full_name, ov[0], ov[1], refresh=full_name not in self._fused_fresh)
 
     def _scatter_masters(self, active_idx, masters) -> None:
         for fname, aidx in active_idx.items():
@@ -395,6 +405,7 @@ class QuantizedExpertCache:
 
     def evict_all(self) -> None:
         self._cache.clear()
+        self._fused_fresh.clear()
 
     @property
     def cached_experts(self) -> List[str]:
