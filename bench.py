@@ -3,17 +3,22 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
-Workloads (BASELINE.json):
+Workloads (the benchmark configurations configs[0..4]):
   * step (the reported `value`, configs[2]): one training step of the
     Qwen3-30B-A3B-shaped 4-bit MoE expert layer on 4096 bf16 tokens --
     router linear + softmax/top-8, fused dequant-GEMM forward (gate_up+SwiGLU,
-    down, combine), backward grad-input through the 4-bit experts and the
-    router, weight gradients sampled at a uniform 0.5 % mask of each expert
-    tensor into fp32 compact vectors, the finite check, SparseAdam on the
-    3,019,897 active elements and the router SGD step (train.py:661-672).
+    down, combine) with the trained values over the 4-bit weights, backward on
+    the loss-scaled gradient through the 4-bit experts and the router, weight
+    gradients sampled at a uniform 0.5 % mask of each expert tensor into fp32
+    compact vectors, unscale and finite check, SparseAdam on the 3,019,897
+    active elements, the router SGD step and the loss-scale schedule
+    (train.py:31, 351-353, 649-677);
   * dequant: kernel (a) over one Qwen3-30B-A3B MoE layer's expert weights held
     as one flat 4-bit arena (gate_up [128,1536,2048] + down [128,2048,768] =
-    603,979,776 elements, 1,528,823,808 algorithmic bytes per launch).
+    603,979,776 elements, 1,528,823,808 algorithmic bytes per launch);
+  * mixtral (configs[3]): one Mixtral-8x7B-shaped layer, 8192 tokens, fwd+bwd;
+  * cache_stress: 48 Qwen3 layers streamed through the per-expert
+    copy cache at two arena sizes, and through the fused 4-bit path.
 Synthetic data: weights ~ N(0, 0.02) quantized on the GPU with the reference's
 scheme, activations and router logits ~ N(0, 1); everything is resident in HBM
 before timing starts.  Prints ONE JSON line.
